@@ -1,0 +1,144 @@
+/*
+ * tilequant.h -- C ABI of the MI355X (gfx950) TileQuant mixed INT8/BF16 tile
+ * path, exported by tilequant_amd/_lib/libtilequant_hip.so.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer owned by the caller (plain hipMalloc /
+ *    torch allocations).  The library allocates and frees nothing.
+ *  - Matrices are row-major with an explicit row stride in ELEMENTS; unless a
+ *    parameter says otherwise the column stride is 1.
+ *  - `stream` is a hipStream_t (0 = null stream).  Work is only enqueued; no
+ *    entry point synchronizes the host, so every call is hipGraph-capturable.
+ *  - Return value: 0 on success, a positive hipError_t from the launch, or a
+ *    negative TQ_ERR_* for an argument error (nothing is enqueued then).
+ *    tq_error_string() names either kind.
+ *  - Activation / 16-bit tile dtypes are TQ_DTYPE_BF16 or TQ_DTYPE_FP16.
+ *
+ * Reference interface each entry point replaces (paths relative to the
+ * TileQuant repository root) is cited above each declaration.
+ */
+#ifndef TILEQUANT_H
+#define TILEQUANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TQ_DTYPE_BF16 = 0, TQ_DTYPE_FP16 = 1 };
+
+/* Storage order of the 64x64 elements inside one packed tile.
+ * ROW_MAJOR: tile[j][k] at j*64+k (the reference packer's order, pack.py:115-175).
+ * MFMA: operand-major order of the gfx950 MFMA B operand. */
+enum { TQ_LAYOUT_ROW_MAJOR = 0, TQ_LAYOUT_MFMA = 1 };
+
+enum {
+  TQ_OK = 0,
+  TQ_ERR_ARG = -1,       /* bad size / null pointer / inconsistent shape */
+  TQ_ERR_DTYPE = -2,     /* unsupported dtype or layout code */
+  TQ_ERR_ALIGN = -3,     /* a tile pointer is not 16-byte aligned */
+  TQ_ERR_WORKSPACE = -4  /* workspace missing or too small */
+};
+
+const char* tq_error_string(int code);
+/* ABI version of this header (bumped on any signature change). */
+int tq_abi_version(void);
+
+/* ---- activation quantization ------------------------------------------
+ * Per 64-column tile c of x [n, k]:  a = max |x[:, 64c:64c+64]| over ALL n
+ * rows;  sx[c] = 1 if a == 0 else f32(round_to_x_dtype(f32(a) / 127));
+ * q = clamp(rint(f32(x) / sx[c]), -127, 127).  q is written [n, k] with row
+ * stride q_stride_n; sx has ceil(k / 64) entries.                        */
+
+/* Replaces quantize_activation_tile_absmax_fused
+ * (src/kernels/triton/quantize_activation.py:118-155, kernel :77-112).
+ * One launch; any n (the reference routes n <= 128 here, quant_utils.py:119-134). */
+int tq_act_quant_fused(const void* x, int64_t x_stride_n, int64_t x_stride_k, int x_dtype,
+                       int n, int k, int8_t* q, int64_t q_stride_n, float* sx, void* stream);
+
+/* Elements of fp32 workspace tq_act_absmax_scales needs for (n, k); 0 when
+ * the scales are produced in a single pass. */
+int64_t tq_act_absmax_workspace_elems(int n, int k);
+
+/* Replaces activation_tile_absmax_scales_64_fused
+ * (quantize_activation.py:158-176, kernel :13-44) / activation_tile_absmax_scales
+ * (src/kernels/quant_utils.py:41-74).  Scales only. */
+int tq_act_absmax_scales(const void* x, int64_t x_stride_n, int64_t x_stride_k, int x_dtype,
+                         int n, int k, float* sx, float* workspace, int64_t workspace_elems,
+                         void* stream);
+
+/* Replaces quantize_activation_tile_with_scales_64_fused
+ * (quantize_activation.py:179-203, kernel :47-74) / quantize_activation_tile_with_scales
+ * (quant_utils.py:78-115).  Codes from given scales. */
+int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64_t x_stride_k,
+                             int x_dtype, int n, int k, const float* sx, int8_t* q,
+                             int64_t q_stride_n, void* stream);
+
+/* ---- mixed INT8/BF16 tile GEMM -----------------------------------------
+ * out[n, m] = sum over the INT8 tiles t of output row tile r = m / 64:
+ *               f32(int32 dot(x_int8[n, 64c:64c+64], tile_t[m % 64, :])) * (sx[c] * sw[t])
+ *           + sum over the 16-bit tiles of r: fp32 dot(x_fp[n, tile c], tile[m % 64, :])
+ * rounded to out_dtype; with bias: round(f32(y) + f32(bias[m])).
+ * Tiles of row tile r occupy positions row_ptr[r] .. row_ptr[r+1]-1 of their
+ * arena, in ascending tile id (id = r * n_tc + c).  Columns >= k read as 0,
+ * output columns >= m are not written.  x_fp and the 16-bit tiles share
+ * x_dtype; bias (nullable) has out_dtype.  split_k <= 0 selects the schedule
+ * automatically; a positive value fixes how many partitions of each row
+ * tile's tile list are reduced (deterministically, in fixed order) per
+ * output tile.  Results are bitwise reproducible for fixed arguments.
+ *
+ * Replaces gemm_mixed_rows_splitk (src/kernels/triton/gemm_rows_splitk_64x64.py:225-323,
+ * kernel :78-190).  workspace / counters are the reference's per-stream
+ * split-K buffers (:193-215); size them with tq_gemm_workspace_elems. */
+int64_t tq_gemm_workspace_elems(int n, int m, int n_tr, int n_tc, int split_k);
+int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                       const int8_t* int8_tiles, const float* int8_scales,
+                       const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                       const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                       const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                       const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                       int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                       int n_tc, int split_k, int tile_layout, float* workspace,
+                       int64_t workspace_elems, void* stream);
+
+/* TEST-ONLY.  Writes the exact INT32 product of every INT8 tile with every
+ * token row, products[t][row][j] (int32 [T8, n, 64]), computed by the same
+ * device tile routine the GEMM uses.  No reference counterpart: it exposes
+ * the quantity the reference's tl.dot produces at gemm_rows_splitk_64x64.py:134. */
+int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
+                              const int8_t* int8_tiles, const int32_t* int8_tile_ids,
+                              const int32_t* int8_row_ptr, int n, int k, int n_tr, int n_tc,
+                              int tile_layout, int32_t* products, void* stream);
+
+/* ---- load-time packing -------------------------------------------------
+ * w [m, k] (x_dtype, row stride w_stride_m) is read as if zero-padded to
+ * multiples of 64.  tile_ids are flat ids r * n_tc + c.                  */
+
+/* Replaces the INT8 branch of _pack_weight_with_tile_ids (src/kernels/pack.py:119-167):
+ * per tile sw = 1 if a == 0 else f32(a) / 127, codes clamp(rint(f32(w) / sw)).
+ * col_importance (nullable, fp32 [n_tc * 64]) selects the IAA search over
+ * sw * {0.75, 1, 1.25} (pack.py:132-159): lowest mean((dq - w)^2 * max(imp, 1e-8)),
+ * first candidate kept on ties.  Tiles are written in `layout`. */
+int tq_pack_int8_tiles(const void* w, int64_t w_stride_m, int w_dtype, int m, int k,
+                       const int32_t* tile_ids, int64_t n_tiles, int n_tc, int layout,
+                       const float* col_importance, int8_t* tiles, float* scales,
+                       void* stream);
+
+/* Replaces the 16-bit branch of _pack_weight_with_tile_ids (pack.py:172-175):
+ * copies the selected tiles unchanged, in `layout`. */
+int tq_pack_16bit_tiles(const void* w, int64_t w_stride_m, int w_dtype, int m, int k,
+                        const int32_t* tile_ids, int64_t n_tiles, int n_tc, int layout,
+                        void* tiles, void* stream);
+
+/* No reference counterpart (the reference has one tile order): converts
+ * n_tiles packed tiles of elem_bytes (1 or 2) between layouts.  src and dst
+ * must not overlap. */
+int tq_tiles_relayout(const void* src, void* dst, int64_t n_tiles, int elem_bytes,
+                      int from_layout, int to_layout, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEQUANT_H */

@@ -1,0 +1,117 @@
+"""GPU parity: activation quantization kernels vs the oracle (bit-exact codes and scales)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import make_x, values
+from oracle import numerics as nm
+from tilequant_amd import quant_utils
+from tilequant_amd.quantize_activation import (
+    activation_tile_absmax_scales_64_fused,
+    quantize_activation_tile_absmax_fused,
+    quantize_activation_tile_with_scales_64_fused,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(x_cpu: torch.Tensor, q: torch.Tensor, sx: torch.Tensor):
+    is_bf16 = x_cpu.dtype == torch.bfloat16
+    q_ref, sx_ref = nm.act_quant(values(x_cpu), is_bf16)
+    sx_got = sx.cpu().numpy()
+    assert np.array_equal(sx_got.view(np.uint32), sx_ref.view(np.uint32)), "scales differ"
+    q_got = q.cpu().numpy()
+    bad = np.argwhere(q_got != q_ref)
+    assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[0].tolist()}"
+
+
+@pytest.mark.parametrize("n", [1, 4, 16, 64, 128])
+@pytest.mark.parametrize("k", [3072, 8192, 100, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_vs_oracle(n, k, dtype):
+    x = make_x(n, k, seed=1000 + n + k, dtype=dtype)
+    q, sx = quantize_activation_tile_absmax_fused(x.cuda())
+    _check(x, q, sx)
+
+
+@pytest.mark.parametrize("n,k", [(129, 3072), (600, 1000), (4096, 3072), (8192, 3072), (4100, 8192)])
+def test_scales_then_codes_vs_oracle(n, k):
+    x = make_x(n, k, seed=2000 + n + k)
+    xd = x.cuda()
+    sx = activation_tile_absmax_scales_64_fused(xd)
+    q = quantize_activation_tile_with_scales_64_fused(xd, sx)
+    _check(x, q, sx)
+    q2, sx2 = quant_utils.quantize_activation_tile_absmax(xd)
+    assert torch.equal(q2, q) and torch.equal(sx2, sx)
+    # the single-launch kernel gives the same bits at any size
+    q3, sx3 = quantize_activation_tile_absmax_fused(xd)
+    assert torch.equal(q3, q) and torch.equal(sx3, sx)
+
+
+def test_strided_inputs():
+    base = make_x(24, 3 * 512, seed=7)
+    # row stride 1536 with every other row, start offset 5 (unaligned rows)
+    xd = base.cuda()[::2, 5:5 + 1000]
+    q, sx = quantize_activation_tile_absmax_fused(xd)
+    _check(base[::2, 5:5 + 1000].contiguous(), q, sx)
+    # column stride != 1
+    src = make_x(300, 64, seed=8)
+    xt = src.cuda().t()
+    q, sx = quantize_activation_tile_absmax_fused(xt)
+    _check(src.t().contiguous(), q, sx)
+    sx2 = activation_tile_absmax_scales_64_fused(xt)
+    assert torch.equal(sx2, sx)
+    assert torch.equal(quantize_activation_tile_with_scales_64_fused(xt, sx2), q)
+
+
+def test_every_bf16_absmax_gives_the_oracle_scale():
+    # one 64-column tile per positive finite bf16 value: the tile's absmax is
+    # that value (exhaustive over the scale's domain); other entries are
+    # random fractions of it so the codes sweep the whole int8 range
+    vals = np.arange(1, 0x7F80, dtype=np.uint16)
+    a = nm.bf16_bits_to_f32(vals)
+    rng = np.random.default_rng(0)
+    frac = rng.uniform(-1, 1, size=(2, vals.size, 64)).astype(np.float32)
+    x = nm.round_bf16(frac * a[None, :, None])
+    x[0, :, 7] = a
+    x = x.reshape(2, -1)
+    xt = torch.from_numpy(nm.f32_to_bf16_bits(x).view(np.int16)).view(torch.bfloat16)
+    q, sx = quantize_activation_tile_absmax_fused(xt.cuda())
+    _check(xt, q, sx)
+    sx2 = activation_tile_absmax_scales_64_fused(xt.cuda())
+    assert torch.equal(sx2, sx)
+
+
+def test_every_fp16_absmax_gives_the_oracle_scale():
+    vals = np.arange(1, 0x7C00, dtype=np.uint16)
+    a = vals.view(np.float16).astype(np.float32)
+    rng = np.random.default_rng(1)
+    x = (rng.uniform(-1, 1, size=(2, vals.size, 64)).astype(np.float32) * a[None, :, None]).astype(np.float16)
+    x[0, :, 3] = a.astype(np.float16)
+    xt = torch.from_numpy(x.reshape(2, -1))
+    q, sx = quantize_activation_tile_absmax_fused(xt.cuda())
+    _check(xt, q, sx)
+
+
+def test_zero_and_tiny_tiles():
+    x = torch.zeros((5, 256), dtype=torch.bfloat16)
+    x[:, 64:128] = 2.5
+    tiny = torch.tensor(2.0 ** -133, dtype=torch.float32).to(torch.bfloat16)
+    x[0, 130] = tiny
+    x[3, 140] = -tiny
+    q, sx = quantize_activation_tile_absmax_fused(x.cuda())
+    _check(x, q, sx)
+    s = sx.cpu()
+    assert s[0] == 1.0 and s[3] == 1.0 and s[2] == 0.0
+    qq = q.cpu()
+    assert torch.all(qq[:, :64] == 0) and qq[0, 130] == 127 and qq[3, 140] == -127 and qq[1, 131] == 127
+
+
+def test_empty_inputs():
+    x = torch.empty((0, 192), dtype=torch.bfloat16, device="cuda")
+    q, sx = quantize_activation_tile_absmax_fused(x)
+    assert q.shape == (0, 192) and torch.equal(sx.cpu(), torch.ones(3))
+    q, sx = quantize_activation_tile_absmax_fused(torch.empty((4, 0), dtype=torch.bfloat16, device="cuda"))
+    assert q.shape == (4, 0) and sx.numel() == 0

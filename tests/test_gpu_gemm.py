@@ -1,0 +1,217 @@
+"""GPU parity: packer, INT32 tile products and the mixed tile GEMM vs the oracle.
+
+Bars: packed tiles / scales and INT32 tile products bit-exact; outputs within
+2 bf16 ulp + the fp32 accumulation bound of the float64 oracle
+(helpers.assert_gemm_close); bitwise run-to-run reproducibility.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_gemm_close, bits, complement, make_w, make_x, oracle_pack, uniform_fp16_ids, values
+from oracle import native as onat
+from oracle import numerics as nm
+from oracle import packing as opk
+from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk, gemm_tile_products_i32
+from tilequant_amd.pack import pack_weight_from_tile_ids, relayout_pack
+from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+pytestmark = pytest.mark.gpu
+
+CFG = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+
+
+def _case(m, k, frac, seed, dtype=torch.bfloat16, layout="mfma"):
+    W = make_w(m, k, seed=seed, dtype=dtype)
+    n_tr, n_tc = -(-m // 64), -(-k // 64)
+    ids16 = uniform_fp16_ids(n_tr, n_tc, frac, seed=seed + 1) if frac > 0 else np.zeros(0, np.int64)
+    ids8 = complement(ids16, n_tr * n_tc)
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(ids8),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=CFG, tile_layout=layout)
+    return W, pack, ids16
+
+
+def _oracle_f64(pack, op, x_cpu, xq, sx):
+    w16 = (nm.bf16_bits_to_f32(op.fp16_tiles) if x_cpu.dtype == torch.bfloat16
+           else op.fp16_tiles.view(np.float16).astype(np.float32))
+    _, acc, sab = onat.gemm_mixed(xq, sx, values(x_cpu), op.int8_tiles, op.int8_scales, op.int8_tile_ids,
+                                  op.int8_row_ptr, w16, op.fp16_tile_ids, op.fp16_row_ptr, pack.n_tr, pack.n_tc,
+                                  pack.M_orig, pack.K_orig, want_f64=True)
+    return acc, sab
+
+
+def _oracle_pack_any(W, ids16):
+    if W.dtype == torch.bfloat16:
+        return oracle_pack(W, ids16)
+    # fp16 weights: same numerics on fp16 values
+    wv = values(W)
+    p = opk.pack_weight(nm.f32_to_bf16_bits(np.zeros_like(wv)), ids16)  # bookkeeping only
+    wp = opk.pad64(wv)
+    ids8 = p.int8_tile_ids.astype(np.int64)
+    q, sw = nm.weight_tile_quant(nm.tiles_of(wp, ids8, p.n_tc))
+    p.int8_tiles, p.int8_scales = q, sw
+    p.fp16_tiles = nm.tiles_of(opk.pad64(bits(W)), p.fp16_tile_ids.astype(np.int64), p.n_tc)
+    return p
+
+
+def _gemm(pack, xd, xq, sx, bias=None, out=None, split_k=None, out_dtype=torch.bfloat16):
+    return gemm_mixed_rows_splitk(
+        x_fp=xd, x_int8=xq, sx=sx, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales,
+        int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles,
+        fp16_tile_ids=pack.fp16_tile_ids, fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig,
+        n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=out_dtype, bias=bias, split_k=split_k, out=out,
+        tile_layout=pack.tile_layout)
+
+
+def test_config1_packer_products_and_output():
+    """3072->3072, 16 tokens, keep01 uniform, outlier activations."""
+    W, pack, ids16 = _case(3072, 3072, 0.01, seed=100)
+    op = oracle_pack(W, ids16)
+    assert pack.int8_tiles.shape[0] == 2280 and pack.fp16_tiles.shape[0] == 24
+    # packer: scales, codes and 16-bit tiles bit-exact (after undoing the MFMA layout)
+    assert np.array_equal(pack.int8_scales.cpu().numpy().view(np.uint32), op.int8_scales.view(np.uint32))
+    assert np.array_equal(opk.from_mfma_int8(pack.int8_tiles.cpu().numpy()), op.int8_tiles)
+    assert np.array_equal(opk.from_mfma_16bit(bits(pack.fp16_tiles.cpu())), op.fp16_tiles)
+    for f in ("int8_tile_ids", "int8_row_ptr", "fp16_tile_ids", "fp16_row_ptr"):
+        assert np.array_equal(getattr(pack, f).cpu().numpy(), getattr(op, f)), f
+    x = make_x(16, 3072, seed=101)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref) and np.array_equal(sx.cpu().numpy(), sx_ref)
+    # INT32 tile products: bit-exact, through the GEMM's own device routine
+    P = gemm_tile_products_i32(x_int8=xq, int8_tiles=pack.int8_tiles, int8_tile_ids=pack.int8_tile_ids,
+                               int8_row_ptr=pack.int8_row_ptr, K=3072, n_tr=48, n_tc=48, tile_layout="mfma")
+    P_ref = onat.tile_products_i32(xq_ref, op.int8_tiles, op.int8_tile_ids, 48)
+    assert np.array_equal(P.cpu().numpy(), P_ref)
+    # output within tolerance of the exact sum
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    worst_ulp = assert_gemm_close(y, acc, sab, 48)
+    assert worst_ulp <= 2.0
+    # run-to-run bitwise reproducible
+    for _ in range(3):
+        assert torch.equal(_gemm(pack, xd, xq, sx), y)
+    # the reference's row-major tile order gives bitwise the same output
+    rm = relayout_pack(pack, "row_major")
+    assert np.array_equal(rm.int8_tiles.cpu().numpy(), op.int8_tiles)
+    assert torch.equal(_gemm(rm, xd, xq, sx), y)
+    P_rm = gemm_tile_products_i32(x_int8=xq, int8_tiles=rm.int8_tiles, int8_tile_ids=rm.int8_tile_ids,
+                                  int8_row_ptr=rm.int8_row_ptr, K=3072, n_tr=48, n_tc=48, tile_layout="row_major")
+    assert torch.equal(P_rm, P)
+    back = relayout_pack(rm, "mfma")
+    assert torch.equal(back.int8_tiles, pack.int8_tiles) and torch.equal(back.fp16_tiles, pack.fp16_tiles)
+
+
+@pytest.mark.parametrize("m,k", [(1024, 3072), (8192, 3072), (3072, 8192), (5120, 3072)])
+@pytest.mark.parametrize("n", [1, 4, 16, 64])
+def test_llama_decode_shapes(m, k, n):
+    """BASELINE configs[1] shapes (k/v, gate/up, down, fused QKV) at decode token counts."""
+    W, pack, ids16 = _case(m, k, 0.01, seed=m + k + n)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=7 * n + m)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+@pytest.mark.parametrize("n", [2, 33, 100, 257])
+def test_token_counts_and_ragged_shapes(n):
+    W, pack, ids16 = _case(200, 300, 0.2, seed=300 + n)       # pads to 256 x 320, K % 64 != 0
+    op = oracle_pack(W, ids16)
+    x = make_x(n, 300, seed=301 + n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    P = gemm_tile_products_i32(x_int8=xq, int8_tiles=pack.int8_tiles, int8_tile_ids=pack.int8_tile_ids,
+                               int8_row_ptr=pack.int8_row_ptr, K=300, n_tr=pack.n_tr, n_tc=pack.n_tc,
+                               tile_layout="mfma")
+    assert np.array_equal(P.cpu().numpy(), onat.tile_products_i32(xq_ref, op.int8_tiles, op.int8_tile_ids, 5, K=300))
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+@pytest.mark.parametrize("frac", [0.0, 1.0, 0.5])
+def test_all_int8_all_bf16_and_half(frac):
+    W, pack, ids16 = _case(256, 512, frac, seed=400)
+    op = oracle_pack(W, ids16)
+    x = make_x(8, 512, seed=401)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+def test_bias_fp16_output_and_out_slices():
+    W, pack, ids16 = _case(384, 640, 0.05, seed=500)
+    op = oracle_pack(W, ids16)
+    x = make_x(12, 640, seed=501)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    bias = (torch.randn(384, generator=torch.Generator().manual_seed(5)) * 0.5).to(torch.bfloat16)
+    y = _gemm(pack, xd, xq, sx, bias=bias.cuda())
+    assert_gemm_close(y, acc, sab, pack.n_tc, bias=values(bias))
+    # bias semantics: round(round(acc) + bias), as the reference's epilogue
+    y_nb = _gemm(pack, xd, xq, sx)
+    want = (y_nb.float() + bias.cuda().float()).to(torch.bfloat16)
+    assert torch.equal(y, want)
+    # fp16 output
+    y16 = _gemm(pack, xd, xq, sx, out_dtype=torch.float16)
+    assert y16.dtype == torch.float16
+    assert np.all(np.abs(values(y16).astype(np.float64) - acc) <= 2 * np.abs(acc) * 2.0 ** -10 + 1e-5 * sab + 1e-7)
+    # writing into a row slice of a larger output (the chunked path)
+    big = torch.full((20, 384), 7.0, dtype=torch.bfloat16, device="cuda")
+    _gemm(pack, xd, xq, sx, out=big[4:16])
+    assert torch.equal(big[4:16], y_nb) and torch.all(big[:4] == 7) and torch.all(big[16:] == 7)
+    with pytest.raises(ValueError):
+        _gemm(pack, xd, xq, sx, out=torch.empty((12, 383), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError):
+        _gemm(pack, xd, xq, sx, out=torch.empty((12, 384), dtype=torch.float16, device="cuda"))
+
+
+def test_fp16_activations_and_weights():
+    W, pack, ids16 = _case(256, 384, 0.1, seed=600, dtype=torch.float16)
+    op = _oracle_pack_any(W, ids16)
+    assert np.array_equal(pack.int8_scales.cpu().numpy(), op.int8_scales)
+    assert np.array_equal(opk.from_mfma_int8(pack.int8_tiles.cpu().numpy()), op.int8_tiles)
+    x = make_x(6, 384, seed=601, dtype=torch.float16)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x), is_bf16=False)
+    assert np.array_equal(xq.cpu().numpy(), xq_ref) and np.array_equal(sx.cpu().numpy(), sx_ref)
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+@pytest.mark.parametrize("split_k", [1, 2, 3, 8, 16])
+def test_split_k_is_deterministic_and_within_tolerance(split_k):
+    W, pack, ids16 = _case(512, 2048, 0.05, seed=700)
+    op = oracle_pack(W, ids16)
+    x = make_x(4, 2048, seed=701)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y = _gemm(pack, xd, xq, sx, split_k=split_k)
+    assert torch.equal(_gemm(pack, xd, xq, sx, split_k=split_k), y)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+def test_empty_token_batch():
+    W, pack, _ = _case(128, 128, 0.1, seed=800)
+    xd = torch.empty((0, 128), dtype=torch.bfloat16, device="cuda")
+    xq = torch.empty((0, 128), dtype=torch.int8, device="cuda")
+    y = _gemm(pack, xd, xq, torch.ones(2, device="cuda"))
+    assert y.shape == (0, 128)

@@ -1,0 +1,152 @@
+"""GPU parity at the module level: MixedLinear forward (2D/3D, chunked prefill
+with whole-input scales), projection groups, IAA packing."""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_gemm_close, complement, make_w, make_x, oracle_pack, uniform_fp16_ids, values
+from oracle import native as onat
+from oracle import numerics as nm
+from tilequant_amd.mixed_linear import MixedLinear, fuse_projection_groups
+from tilequant_amd.pack import pack_weight_from_tile_ids
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear(m, k, frac, seed, cfg, bias=False, layout="mfma"):
+    W = make_w(m, k, seed=seed)
+    n_tr, n_tc = -(-m // 64), -(-k // 64)
+    ids16 = uniform_fp16_ids(n_tr, n_tc, frac, seed=seed + 1)
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc,
+                                     int8_tile_ids=torch.from_numpy(complement(ids16, n_tr * n_tc)),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=cfg, tile_layout=layout)
+    b = (torch.randn(m, generator=torch.Generator().manual_seed(seed)) * 0.1).to(torch.bfloat16) if bias else None
+    return MixedLinear(pack, b.cuda() if b is not None else None, cfg), W, ids16, b
+
+
+def _expected(W, ids16, x_cpu, sx_ref=None):
+    op = oracle_pack(W, ids16)
+    xv = values(x_cpu)
+    if sx_ref is None:
+        xq, sx = nm.act_quant(xv)
+    else:
+        sx = sx_ref
+        xq = nm.act_quant_codes(xv, sx)
+    _, acc, sab = onat.gemm_mixed(xq, sx, xv, op.int8_tiles, op.int8_scales, op.int8_tile_ids, op.int8_row_ptr,
+                                  nm.bf16_bits_to_f32(op.fp16_tiles), op.fp16_tile_ids, op.fp16_row_ptr,
+                                  op.n_tr, op.n_tc, op.M_orig, op.K_orig, want_f64=True)
+    return acc, sab, op.n_tc
+
+
+def test_forward_2d_and_3d():
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    lin, W, ids16, b = _linear(512, 1024, 0.02, 10, cfg, bias=True)
+    x = make_x(8, 1024, seed=11)
+    y2 = lin(x.cuda())
+    acc, sab, n_tc = _expected(W, ids16, x)
+    assert y2.dtype == torch.bfloat16 and y2.shape == (8, 512)
+    assert_gemm_close(y2, acc, sab, n_tc, bias=values(b))
+    y3 = lin(x.cuda().view(2, 4, 1024))
+    assert y3.shape == (2, 4, 512) and torch.equal(y3.view(8, 512), y2)
+
+
+def test_default_out_dtype_is_fp16_like_reference():
+    lin, _, _, _ = _linear(128, 128, 0.1, 20, SimpleNamespace(quant_style="gi"))
+    assert lin(make_x(2, 128).cuda()).dtype == torch.float16
+
+
+def test_chunked_rows_use_whole_input_scales():
+    # activation_row_chunk_size smaller than N: the scale is taken over ALL rows
+    # before chunking (mixed_linear.py:240-250)
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16", activation_row_chunk_size=64)
+    lin, W, ids16, _ = _linear(256, 512, 0.05, 30, cfg)
+    x = make_x(200, 512, seed=31)
+    x[150:, :64] *= 50                     # the last chunk holds the first tile's absmax
+    y = lin(x.cuda())
+    sx_all = nm.act_tile_scales(values(x))
+    acc, sab, n_tc = _expected(W, ids16, x, sx_ref=sx_all)
+    assert_gemm_close(y, acc, sab, n_tc)
+    # per-chunk scales would differ measurably in the first tile's rows
+    acc_bad, _, _ = _expected(W, ids16, x[:64])
+    assert not np.allclose(acc_bad, acc[:64], rtol=1e-3)
+
+
+def test_prefill_8192_rows_two_chunks():
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    lin, W, ids16, _ = _linear(256, 3072, 0.05, 40, cfg)
+    x = make_x(8192, 3072, seed=41)
+    y = lin(x.cuda())
+    # check a sample of rows from both chunks against the oracle with whole-input scales
+    sx_all = nm.act_tile_scales(values(x))
+    rows = np.r_[0:8, 4090:4100, 8184:8192]
+    acc, sab, n_tc = _expected(W, ids16, x[rows], sx_ref=sx_all)
+    assert_gemm_close(y[rows], acc, sab, n_tc)
+
+
+def test_projection_groups_equal_members_bitwise():
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+
+    class Attn(torch.nn.Module):
+        pass
+
+    parent = Attn()
+    members = {}
+    for i, (name, m) in enumerate((("q_proj", 512), ("k_proj", 128), ("v_proj", 128))):
+        lin, _, _, _ = _linear(m, 768, 0.05, 50 + i, cfg)
+        setattr(parent, name, lin)
+        members[name] = lin
+    for n in (1, 4, 40):
+        x = make_x(n, 768, seed=60 + n).cuda()
+        want = {name: members[name](x) for name in members}
+        solo = Attn()
+        for name, lin in members.items():
+            setattr(solo, name, lin)
+        assert fuse_projection_groups(solo) == 1
+        with torch.inference_mode():
+            got = {name: getattr(solo, name)(x) for name in members}
+        for name in members:
+            assert torch.equal(got[name], want[name]), name
+
+
+def test_iaa_packing_matches_torch_restatement():
+    """IAA scale search (pack.py:132-159): codes/scales match a torch-op
+    restatement except where two candidates' errors tie to ~1e-6 (sum order)."""
+    W = make_w(256, 512, seed=70)
+    n_tr, n_tc = 4, 8
+    ids16 = uniform_fp16_ids(n_tr, n_tc, 0.1, seed=71)
+    ids8 = complement(ids16, n_tr * n_tc)
+    imp = torch.rand(512, generator=torch.Generator().manual_seed(72)) * 3
+    cfg = SimpleNamespace(quant_style="iaa", dtype_out="bf16")
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(ids8),
+                                     fp16_tile_ids=torch.from_numpy(ids16), iaa_col_importance=imp, cfg=cfg,
+                                     tile_layout="row_major")
+    # torch-op restatement on the CPU
+    view = W.view(n_tr, 64, n_tc, 64).permute(0, 2, 1, 3)
+    r, c = torch.from_numpy(ids8 // n_tc), torch.from_numpy(ids8 % n_tc)
+    src = view[r, c]
+    base = src.abs().amax(dim=(1, 2)).to(torch.float32)
+    base = torch.where(base == 0, torch.ones_like(base), base / 127.0)
+    wm = imp.view(n_tc, 64)[c].clamp_min(1e-8)[:, None, :]
+    srcf = src.to(torch.float32)
+    errs, cands = [], []
+    for mlt in (0.75, 1.0, 1.25):
+        s = (base * torch.tensor(mlt, dtype=torch.float32)).clamp_min(1e-12)
+        dq = torch.clamp(torch.round(srcf / s[:, None, None]), -127, 127) * s[:, None, None]
+        errs.append(((dq - srcf) ** 2 * wm).mean(dim=(1, 2)))
+        cands.append(s)
+    E = torch.stack(errs)
+    best = torch.zeros_like(base, dtype=torch.long)
+    for i in (1, 2):
+        best = torch.where(E[i] < E.gather(0, best[None])[0], torch.full_like(best, i), best)
+    want_s = torch.stack(cands).gather(0, best[None])[0]
+    got_s = pack.int8_scales.cpu()
+    srt = E.sort(dim=0).values
+    near_tie = (srt[1] - srt[0]) <= 1e-5 * srt[0]
+    assert torch.equal(got_s[~near_tie], want_s[~near_tie])
+    assert int(near_tie.sum()) <= max(1, len(ids8) // 20)
+    q_want = torch.clamp(torch.round(srcf / got_s[:, None, None]), -127, 127).to(torch.int8)
+    assert torch.equal(pack.int8_tiles.cpu(), q_want)

@@ -1,0 +1,186 @@
+"""Host-side logic on the CPU: API checks, bookkeeping, Decision/ archives,
+target selection, module plumbing.  No GPU; compute entry points must refuse
+CPU tensors (there is no CPU fallback)."""
+from __future__ import annotations
+
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import make_w, oracle_pack, uniform_fp16_ids
+from oracle import masks as om
+from oracle import packing as opk
+from tilequant_amd import mask_io, pack as tpack, quant_utils, rules
+from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+from tilequant_amd.mixed_linear import MixedLinear, fuse_projection_groups, MixedLinearSlice
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_quant_ops_refuse_cpu_tensors():
+    x = torch.randn(4, 128).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        quant_utils.quantize_activation_tile_absmax(x)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        quant_utils.activation_tile_absmax_scales(x)
+    with pytest.raises(ValueError):
+        quant_utils.quantize_activation_tile_absmax(x.view(2, 2, 128))
+    with pytest.raises(ValueError):
+        quant_utils.quantize_activation_tile_absmax(x, tile_n=32)
+
+
+def _cpu_pack(m=128, k=192, frac=0.3, seed=0):
+    W = make_w(m, k, seed=seed)
+    n_tr, n_tc = -(-m // 64), -(-k // 64)
+    ids16 = uniform_fp16_ids(n_tr, n_tc, frac, seed=seed + 1)
+    op = oracle_pack(W, ids16)
+    t = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)) if dt is None else torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+    return tpack.Pack(
+        M_orig=m, K_orig=k, M=op.M, K=op.K, tile_m=64, tile_n=64, n_tr=n_tr, n_tc=n_tc,
+        int8_tiles=t(op.int8_tiles), int8_scales=t(op.int8_scales), int8_tile_ids=t(op.int8_tile_ids),
+        int8_row_ptr=t(op.int8_row_ptr), int8_row_indices=torch.arange(op.int8_tile_ids.size, dtype=torch.int32),
+        fp16_tiles=t(op.fp16_tiles.view(np.int16)).view(torch.bfloat16), fp16_tile_ids=t(op.fp16_tile_ids),
+        fp16_row_ptr=t(op.fp16_row_ptr), fp16_row_indices=torch.arange(op.fp16_tile_ids.size, dtype=torch.int32),
+        tile_layout="row_major"), op
+
+
+def test_gemm_refuses_cpu_tensors():
+    p, _ = _cpu_pack()
+    x = torch.zeros(2, 192, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        gemm_mixed_rows_splitk(x_fp=x, x_int8=torch.zeros(2, 192, dtype=torch.int8), sx=torch.ones(3),
+                               int8_tiles=p.int8_tiles, int8_scales=p.int8_scales, int8_tile_ids=p.int8_tile_ids,
+                               int8_row_ptr=p.int8_row_ptr, fp16_tiles=p.fp16_tiles, fp16_tile_ids=p.fp16_tile_ids,
+                               fp16_row_ptr=p.fp16_row_ptr, M=128, K=192, n_tr=2, n_tc=3, out_dtype=torch.bfloat16)
+
+
+def test_row_schedule_matches_oracle():
+    ids = torch.tensor([1, 4, 5, 9, 10, 11], dtype=torch.int64)
+    rp, ri = tpack._build_row_schedule(ids, n_tr=4, n_tc=3)
+    assert rp.tolist() == opk.row_ptr_of(ids.numpy(), 4, 3).tolist() == [0, 1, 3, 3, 6]
+    assert ri.tolist() == list(range(6))
+    rp0, ri0 = tpack._build_row_schedule(torch.empty(0, dtype=torch.int64), n_tr=2, n_tc=3)
+    assert rp0.tolist() == [0, 0, 0] and ri0.numel() == 0
+
+
+def test_concat_packs_matches_oracle_and_checks():
+    (a, oa), (b, ob) = _cpu_pack(128, 192, 0.3, 1), _cpu_pack(64, 192, 0.5, 2)
+    cat = tpack.concat_packs_along_rows([a, b])
+    ocat = opk.concat_rows([oa, ob])
+    assert cat.n_tr == 3 and cat.M == 192
+    for f in ("int8_tile_ids", "int8_row_ptr", "fp16_tile_ids", "fp16_row_ptr", "int8_scales"):
+        assert np.array_equal(getattr(cat, f).numpy(), getattr(ocat, f)), f
+    c, _ = _cpu_pack(128, 256, 0.3, 3)
+    with pytest.raises(ValueError, match="input geometry"):
+        tpack.concat_packs_along_rows([a, c])
+    d, _ = _cpu_pack(128, 192, 0.3, 4)
+    d.tile_layout = "mfma"
+    with pytest.raises(ValueError, match="tile layout"):
+        tpack.concat_packs_along_rows([a, d])
+    with pytest.raises(ValueError):
+        tpack.concat_packs_along_rows([])
+
+
+def test_pack_validation_errors_before_device_work():
+    W = make_w(128, 192)
+    cfg = {"quant_style": "gi"}
+    ids = torch.arange(6, dtype=torch.int32)
+    with pytest.raises(ValueError, match="dimensions mismatch"):
+        tpack.pack_weight_from_tile_ids(W, n_tr=3, n_tc=3, int8_tile_ids=ids, fp16_tile_ids=ids[:0], cfg=cfg)
+    with pytest.raises(ValueError, match="quant_style"):
+        tpack.pack_weight_from_tile_ids(W, n_tr=2, n_tc=3, int8_tile_ids=ids, fp16_tile_ids=ids[:0],
+                                        cfg={"quant_style": "awq"})
+    with pytest.raises(ValueError, match="pad_to_tile=False"):
+        tpack.pack_weight_from_tile_ids(make_w(100, 192), n_tr=2, n_tc=3, int8_tile_ids=ids, fp16_tile_ids=ids[:0],
+                                        cfg={"pad_to_tile": False})
+    with pytest.raises(ValueError):
+        tpack.pack_weight_from_tile_ids(W.float(), n_tr=2, n_tc=3, int8_tile_ids=ids, fp16_tile_ids=ids[:0], cfg=cfg)
+
+
+def test_mask_io_roundtrip_and_errors(tmp_path):
+    masks = {"model_layers_0_self_attn_q_proj": np.eye(4, 6, dtype=np.uint8),
+             "model_layers_10_mlp_up_proj": np.zeros((2, 3), np.uint8)}
+    path = mask_io.save_mask_keep_archive(tmp_path, masks)
+    assert path.name == "fp16_keep_ids_tile64x64.npz"
+    ids, shape = mask_io.load_fp16_keep_ids_for_layer(tmp_path, "model.layers.0.self_attn.q_proj")
+    assert shape == (4, 6) and ids.tolist() == [0, 7, 14, 21] and ids.dtype == torch.int32
+    assert torch.equal(mask_io.load_mask_keep_for_layer(tmp_path, "model.layers.0.self_attn.q_proj"),
+                       torch.from_numpy(masks["model_layers_0_self_attn_q_proj"]))
+    assert set(mask_io.load_mask_keep_stem_dict(tmp_path)) == set(masks)
+    # the oracle's independent reader sees the same content
+    arch = om.read_archive(path)
+    assert arch["model_layers_0_self_attn_q_proj"][1].tolist() == [0, 7, 14, 21]
+    with pytest.raises(FileNotFoundError):
+        mask_io.load_fp16_keep_ids_for_layer(tmp_path, "model.layers.3.mlp.up_proj")
+    with pytest.raises(FileNotFoundError):
+        mask_io.load_fp16_keep_ids_for_layer(tmp_path / "nope", "x")
+    with pytest.raises(ValueError):
+        mask_io.save_mask_keep_archive(tmp_path, {"a": np.full((2, 2), 2)})
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    np.savez_compressed(bad / "fp16_keep_ids_tile64x64.npz", stems=np.asarray(["s"]),
+                        shape_0=np.asarray([2, 2], np.int32), ids_0=np.asarray([4], np.uint16))
+    with pytest.raises(RuntimeError, match="Out-of-bound"):
+        mask_io.load_fp16_keep_ids_for_layer(bad, "s")
+
+
+def test_mask_io_reads_released_archive_like_oracle():
+    keep = GOLDEN / "llama32_3b_gi_keep01"
+    amap = mask_io._load_archive_map(keep, 64, 64)
+    oarch = om.read_archive(keep / "fp16_keep_ids_tile64x64.npz")
+    assert set(amap) == set(oarch)
+    for stem in list(amap)[:20]:
+        assert amap[stem][0] == oarch[stem][0] and np.array_equal(amap[stem][1], oarch[stem][1])
+
+
+def test_iter_target_linears_on_llama_architecture():
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=64)
+    model = LlamaForCausalLM(cfg)
+    found = rules.iter_target_linears(model, cfg={}, model_type="llama")
+    assert len(found) == 14
+    names = {f for _, _, f, _ in found}
+    assert "model.layers.1.mlp.down_proj" in names and "lm_head" not in names
+    only_attn = rules.iter_target_linears(model, cfg={"module_filters": ["*self_attn*"]}, model_type="llama")
+    assert len(only_attn) == 8
+
+
+def test_mixed_linear_module_plumbing_on_cpu():
+    p, _ = _cpu_pack()
+    cfg = SimpleNamespace(dtype_out="bf16")
+    m = MixedLinear(p, torch.zeros(128, dtype=torch.bfloat16), cfg)
+    sd = m.state_dict()
+    assert {"int8_tiles", "int8_scales", "int8_tile_ids", "int8_row_ptr", "int8_row_indices", "fp16_tiles",
+            "fp16_tile_ids", "fp16_row_ptr", "fp16_row_indices", "bias"} <= set(sd)
+    assert sd["_extra_state"] == {"tile_layout": "row_major"}
+    m2 = MixedLinear(p, None, cfg)
+    m2.tile_layout = "mfma"
+    m2.load_state_dict({k: v for k, v in sd.items() if k != "bias"}, strict=False)
+    assert m2.tile_layout == "row_major"
+    with pytest.raises(ValueError, match="K mismatch"):
+        m(torch.zeros(2, 100, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="rank"):
+        m(torch.zeros(192, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        m(torch.zeros(2, 3, 192, dtype=torch.bfloat16))
+    assert m.to_pack().tile_layout == "row_major"
+
+
+def test_fuse_projection_groups_structure_on_cpu():
+    class Attn(torch.nn.Module):
+        pass
+
+    cfg = SimpleNamespace(dtype_out="bf16")
+    parent = Attn()
+    for i, name in enumerate(("q_proj", "k_proj", "v_proj")):
+        p, _ = _cpu_pack(128 if name == "q_proj" else 64, 192, 0.3, 10 + i)
+        setattr(parent, name, MixedLinear(p, None, cfg))
+    assert fuse_projection_groups(parent) == 1
+    assert isinstance(parent.q_proj, MixedLinearSlice)
+    assert parent.tilequant_qkv.bounds == ((0, 128), (128, 192), (192, 256))
+    assert parent.tilequant_qkv.linear.n_tr == 4

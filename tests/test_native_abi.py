@@ -1,0 +1,64 @@
+"""The C-ABI library loads and exports every symbol include/tilequant.h declares.
+
+No compute: only pure host entry points are called (argument validation,
+workspace sizing, error strings), so this runs without a GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tilequant_amd import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tilequant.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tq_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return nat.load()
+
+
+def test_header_declares_what_the_binding_knows():
+    assert header_functions() == sorted(nat.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_abi_version_and_error_strings(lib):
+    assert lib.tq_abi_version() == nat.ABI_VERSION
+    assert lib.tq_error_string(0) == b"ok"
+    for code in (-1, -2, -3, -4):
+        assert b"unknown" not in lib.tq_error_string(code)
+
+
+def test_argument_errors_return_before_any_launch(lib):
+    # negative sizes / bad dtype codes are rejected on the host
+    assert lib.tq_act_quant_fused(None, 0, 1, 0, -1, 64, None, 64, None, None) == -1
+    assert lib.tq_act_quant_fused(None, 64, 1, 7, 1, 64, None, 64, None, None) == -2
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, -1, 64, 64, 1, 1, 0, 1, None, 0, None) == -1
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, 1, 64, 64, 1, 1, 0, 5, None, 0, None) == -2
+    assert lib.tq_tiles_relayout(None, None, 1, 3, 0, 1, None) == -1
+    # empty problems are a no-op success
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, 0, 64, 64, 1, 1, 0, 1, None, 0, None) == 0
+    assert lib.tq_pack_int8_tiles(None, 64, 0, 64, 64, None, 0, 1, 1, None, None, None, None) == 0
+
+
+def test_workspace_sizing(lib):
+    assert lib.tq_act_absmax_workspace_elems(128, 3072) == 0
+    assert lib.tq_act_absmax_workspace_elems(8192, 3072) == 32 * 48
+    assert lib.tq_gemm_workspace_elems(16, 3072, 48, 48, 0) == 0

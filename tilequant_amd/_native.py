@@ -1,0 +1,113 @@
+"""ctypes binding of ``_lib/libtilequant_hip.so`` (C ABI: ``include/tilequant.h``).
+
+The library is built in-tree for gfx950 by ``tilequant_amd.build.build()``.
+There is no fallback: if the library is missing, or a tensor is not on a ROCm
+device, the calling op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtilequant_hip.so"
+ABI_VERSION = 1
+
+TQ_DTYPE = {torch.bfloat16: 0, torch.float16: 1}
+TQ_LAYOUT = {"row_major": 0, "mfma": 1}
+
+TQ_ERR_ARG = -1
+
+_LIB: Optional[ctypes.CDLL] = None
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes); mirrors include/tilequant.h
+_SIGNATURES = {
+    "tq_error_string": (ctypes.c_char_p, [_i]),
+    "tq_abi_version": (_i, []),
+    "tq_act_quant_fused": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _i64, _p, _p]),
+    "tq_act_absmax_workspace_elems": (_i64, [_i, _i]),
+    "tq_act_absmax_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
+    "tq_act_quant_with_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
+    "tq_gemm_workspace_elems": (_i64, [_i, _i, _i, _i, _i]),
+    "tq_gemm_mixed_rows": (_i, [_p, _i64, _p,
+                                _p, _p, _p, _p,
+                                _p, _i64, _i,
+                                _p, _p, _p,
+                                _p, _i64, _i, _p,
+                                _i, _i, _i, _i, _i,
+                                _i, _i, _p, _i64, _p]),
+    "tq_gemm_tile_products_i32": (_i, [_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
+    "tq_pack_int8_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
+    "tq_pack_16bit_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p]),
+    "tq_tiles_relayout": (_i, [_p, _p, _i64, _i, _i, _i, _p]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load the library and attach signatures.  Loading needs no GPU."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise NativeLibraryMissing(
+            f"{p} is not built; run tilequant_amd.build.build() (hipcc --offload-arch=gfx950)"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.tq_abi_version() != ABI_VERSION:
+        raise NativeLibraryMissing(f"{p} has ABI {lib.tq_abi_version()}, expected {ABI_VERSION}; rebuild it")
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def lib() -> ctypes.CDLL:
+    return _LIB if _LIB is not None else load()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().tq_error_string(int(rc)).decode()
+        if rc == TQ_ERR_ARG:
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "tilequant_amd kernels run on a ROCm GPU only (no CPU fallback); got a tensor on "
+                f"{t.device}"
+            )
+
+
+def stream_handle(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else int(t.data_ptr())
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return TQ_DTYPE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected torch.bfloat16 or torch.float16") from None

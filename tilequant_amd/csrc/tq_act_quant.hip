@@ -1,0 +1,256 @@
+// tq_act_quant.hip -- per-64-column-tile INT8 activation quantization (gfx950).
+//
+// Numerics (one scale per 64-column tile, shared by ALL rows of the call):
+//   a     = max |x[:, 64c:64c+64]|                       (exact in the 16-bit type)
+//   sx[c] = a == 0 ? 1 : f32(round_to_x_dtype(f32(a) / 127))     IEEE divide
+//   q     = max(min(rint(f32(x) / sx[c]), 127), -127)            IEEE divide, half-even
+// following src/kernels/triton/quantize_activation.py:29-43, 66-71, 96-112.
+// The clamp is min-then-max with NaN-ignoring min/max, as the reference
+// kernel's tl.minimum / tl.maximum, so a zero-scale tile (a < 127 * 2^-134)
+// maps x == 0 to 127; the codes of such a tile never reach the output
+// because every product with it is scaled by sx == 0.
+//
+// Kernels
+//   act_quant_fused      grid n_tc, 256 threads: absmax -> scale -> codes in one
+//                        launch (reference :77-112 for n <= 128; any n works).
+//   act_absmax_partial   grid (n_tc, n_rb): max over a 256-row block; writes the
+//                        scale directly when n_rb == 1, else a partial.
+//   act_scales_finalize  max over the n_rb partials (fixed order; max is exact
+//                        so the result is order-free) -> scale.
+//   act_quant_scaled     codes from given scales, 8 elements (16 B in, 8 B out)
+//                        per thread on the aligned path.
+// Every kernel has a vector path (unit column stride, 16-byte aligned rows,
+// full tiles) and a scalar path for everything else.
+#include "tq_common.h"
+
+namespace tq {
+
+constexpr int kQuantThreads = 256;
+constexpr int kRowsPerPass = kQuantThreads / 8;  // 8 threads x 8 elements per 64-col row
+constexpr int kPartialRows = 256;                 // rows per absmax partial block
+constexpr int kSinglePassMaxRows = 512;           // above this the scales are two-level
+
+struct XView {
+  const uint16_t* x;
+  int64_t sn, sk;
+  int n, k;
+};
+
+// Loads 8 consecutive elements of row `row`, columns col..col+7 (vector path).
+__device__ inline u32x4 load8(const XView& v, int row, int col) {
+  return *reinterpret_cast<const u32x4*>(v.x + (int64_t)row * v.sn + col);
+}
+
+template <class T>
+__device__ inline float max8(u32x4 w, float m) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] & 0xffffu))));
+    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] >> 16))));
+  }
+  return m;
+}
+
+template <class T>
+__device__ inline u32x2 codes8(u32x4 w, float s) {
+  u32x2 out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t word = w[h * 2 + i];
+      uint32_t lo = (uint32_t)(quant_code(T::to_f32((uint16_t)(word & 0xffffu)), s) & 0xff);
+      uint32_t hi = (uint32_t)(quant_code(T::to_f32((uint16_t)(word >> 16)), s) & 0xff);
+      packed |= (lo | (hi << 8)) << (16 * i);
+    }
+    out[h] = packed;
+  }
+  return out;
+}
+
+// Vector path is legal for tile c when rows are 16-byte aligned, the column
+// stride is 1 and the tile lies fully inside k.
+__device__ inline bool tile_vec_ok(const XView& v, int c) {
+  return v.sk == 1 && (v.sn % 8) == 0 && aligned16(v.x) && (c + 1) * kTile <= v.k;
+}
+
+template <class T>
+__device__ float tile_absmax(const XView& v, int c, int row0, int row1) {
+  const int t = threadIdx.x;
+  float m = 0.0f;
+  if (tile_vec_ok(v, c)) {
+    const int col = c * kTile + (t % 8) * 8;
+    for (int row = row0 + t / 8; row < row1; row += kRowsPerPass) m = max8<T>(load8(v, row, col), m);
+  } else {
+    const int cols = min(kTile, v.k - c * kTile);
+    for (int64_t e = t; e < (int64_t)(row1 - row0) * kTile; e += kQuantThreads) {
+      int row = row0 + (int)(e / kTile), kk = (int)(e % kTile);
+      if (kk < cols) m = fmaxf(m, fabsf(T::to_f32(v.x[(int64_t)row * v.sn + (int64_t)(c * kTile + kk) * v.sk])));
+    }
+  }
+  return m;
+}
+
+template <class T>
+__global__ void __launch_bounds__(kQuantThreads)
+act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
+  __shared__ float red[kQuantThreads / kWave];
+  const int c = blockIdx.x, t = threadIdx.x;
+  const float a = block_max(tile_absmax<T>(v, c, 0, v.n), red, kQuantThreads / kWave);
+  const float s = act_scale_from_absmax<T>(a);
+  if (t == 0) sx[c] = s;
+  const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
+  if (tile_vec_ok(v, c) && qvec) {
+    const int col = c * kTile + (t % 8) * 8;
+    for (int row = t / 8; row < v.n; row += kRowsPerPass)
+      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), s);
+  } else {
+    const int cols = min(kTile, v.k - c * kTile);
+    for (int64_t e = t; e < (int64_t)v.n * kTile; e += kQuantThreads) {
+      int row = (int)(e / kTile), kk = (int)(e % kTile);
+      if (kk < cols) {
+        float xv = T::to_f32(v.x[(int64_t)row * v.sn + (int64_t)(c * kTile + kk) * v.sk]);
+        q[(int64_t)row * ldq + c * kTile + kk] = (int8_t)quant_code(xv, s);
+      }
+    }
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(kQuantThreads)
+act_absmax_partial_kernel(XView v, float* __restrict__ out, int rows_per_block, int write_scale) {
+  __shared__ float red[kQuantThreads / kWave];
+  const int c = blockIdx.x, rb = blockIdx.y;
+  const int row0 = rb * rows_per_block, row1 = min(v.n, row0 + rows_per_block);
+  const float a = block_max(tile_absmax<T>(v, c, row0, row1), red, kQuantThreads / kWave);
+  if (threadIdx.x == 0) {
+    const int n_tc = gridDim.x;
+    if (write_scale) out[c] = act_scale_from_absmax<T>(a);
+    else out[(int64_t)rb * n_tc + c] = a;
+  }
+}
+
+template <class T>
+__global__ void act_scales_finalize_kernel(const float* __restrict__ partial, int n_rb, int n_tc,
+                                           float* __restrict__ sx) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n_tc) return;
+  float a = 0.0f;
+  for (int rb = 0; rb < n_rb; ++rb) a = fmaxf(a, partial[(int64_t)rb * n_tc + c]);
+  sx[c] = act_scale_from_absmax<T>(a);
+}
+
+template <class T>
+__global__ void __launch_bounds__(kQuantThreads)
+act_quant_scaled_kernel(XView v, const float* __restrict__ sx, int8_t* __restrict__ q, int64_t ldq,
+                        int vec) {
+  const int64_t stride = (int64_t)gridDim.x * kQuantThreads;
+  const int64_t first = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x;
+  if (vec) {
+    const int kv = v.k / 8;
+    const int64_t items = (int64_t)v.n * kv;
+    for (int64_t it = first; it < items; it += stride) {
+      const int row = (int)(it / kv), col = (int)(it % kv) * 8;
+      const float s = sx[col / kTile];
+      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), s);
+    }
+  } else {
+    const int64_t items = (int64_t)v.n * v.k;
+    for (int64_t it = first; it < items; it += stride) {
+      const int row = (int)(it / v.k), col = (int)(it % v.k);
+      const float xv = T::to_f32(v.x[(int64_t)row * v.sn + (int64_t)col * v.sk]);
+      q[(int64_t)row * ldq + col] = (int8_t)quant_code(xv, sx[col / kTile]);
+    }
+  }
+}
+
+static int n_tiles_of(int k) { return (k + kTile - 1) / kTile; }
+
+static int check_x(const void* x, int64_t sn, int64_t sk, int dtype, int n, int k) {
+  if (n < 0 || k < 0 || sn < 0 || sk < 0) return TQ_ERR_ARG;
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (n > 0 && k > 0 && x == nullptr) return TQ_ERR_ARG;
+  return TQ_OK;
+}
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" int tq_act_quant_fused(const void* x, int64_t x_stride_n, int64_t x_stride_k, int x_dtype,
+                                  int n, int k, int8_t* q, int64_t q_stride_n, float* sx,
+                                  void* stream) {
+  int rc = check_x(x, x_stride_n, x_stride_k, x_dtype, n, k);
+  if (rc) return rc;
+  if (k == 0) return TQ_OK;
+  if (sx == nullptr || (n > 0 && (q == nullptr || q_stride_n < k))) return TQ_ERR_ARG;
+  XView v{static_cast<const uint16_t*>(x), x_stride_n, x_stride_k, n, k};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid(n_tiles_of(k));
+  if (x_dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(act_quant_fused_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx);
+  else
+    hipLaunchKernelGGL(act_quant_fused_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t tq_act_absmax_workspace_elems(int n, int k) {
+  if (n <= kSinglePassMaxRows || k <= 0) return 0;
+  const int64_t n_rb = (n + kPartialRows - 1) / kPartialRows;
+  return n_rb * n_tiles_of(k);
+}
+
+extern "C" int tq_act_absmax_scales(const void* x, int64_t x_stride_n, int64_t x_stride_k, int x_dtype,
+                                    int n, int k, float* sx, float* workspace, int64_t workspace_elems,
+                                    void* stream) {
+  int rc = check_x(x, x_stride_n, x_stride_k, x_dtype, n, k);
+  if (rc) return rc;
+  if (k == 0) return TQ_OK;
+  if (sx == nullptr) return TQ_ERR_ARG;
+  const int n_tc = n_tiles_of(k);
+  XView v{static_cast<const uint16_t*>(x), x_stride_n, x_stride_k, n, k};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t need = tq_act_absmax_workspace_elems(n, k);
+  const bool bf = x_dtype == TQ_DTYPE_BF16;
+  if (need == 0) {
+    // one block per tile covers every row; n == 0 gives a == 0 -> scale 1
+    dim3 grid(n_tc, 1);
+    if (bf) hipLaunchKernelGGL(act_absmax_partial_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, sx, n, 1);
+    else hipLaunchKernelGGL(act_absmax_partial_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, sx, n, 1);
+    return (int)hipGetLastError();
+  }
+  if (workspace == nullptr || workspace_elems < need) return TQ_ERR_WORKSPACE;
+  const int n_rb = (n + kPartialRows - 1) / kPartialRows;
+  dim3 grid(n_tc, n_rb);
+  dim3 fgrid((n_tc + 255) / 256);
+  if (bf) {
+    hipLaunchKernelGGL(act_absmax_partial_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, workspace, kPartialRows, 0);
+    hipLaunchKernelGGL(act_scales_finalize_kernel<Bf16>, fgrid, dim3(256), 0, s, workspace, n_rb, n_tc, sx);
+  } else {
+    hipLaunchKernelGGL(act_absmax_partial_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, workspace, kPartialRows, 0);
+    hipLaunchKernelGGL(act_scales_finalize_kernel<Fp16>, fgrid, dim3(256), 0, s, workspace, n_rb, n_tc, sx);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64_t x_stride_k,
+                                        int x_dtype, int n, int k, const float* sx, int8_t* q,
+                                        int64_t q_stride_n, void* stream) {
+  int rc = check_x(x, x_stride_n, x_stride_k, x_dtype, n, k);
+  if (rc) return rc;
+  if (k == 0 || n == 0) return TQ_OK;
+  if (sx == nullptr || q == nullptr || q_stride_n < k) return TQ_ERR_ARG;
+  XView v{static_cast<const uint16_t*>(x), x_stride_n, x_stride_k, n, k};
+  const int vec = (x_stride_k == 1 && (x_stride_n % 8) == 0 && (k % 8) == 0 && aligned16(x) &&
+                   (q_stride_n % 8) == 0 && (((uintptr_t)q & 7u) == 0)) ? 1 : 0;
+  const int64_t items = vec ? (int64_t)n * (k / 8) : (int64_t)n * k;
+  int64_t blocks = (items + kQuantThreads - 1) / kQuantThreads;
+  if (blocks > 8192) blocks = 8192;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(act_quant_scaled_kernel<Bf16>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, s, v, sx, q, q_stride_n, vec);
+  else
+    hipLaunchKernelGGL(act_quant_scaled_kernel<Fp16>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, s, v, sx, q, q_stride_n, vec);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,124 @@
+"""Mixed INT8/BF16 64x64-tile GEMM (HIP, gfx950).
+
+``gemm_mixed_rows_splitk`` keeps the keyword interface, output validation and
+return value of the reference (src/kernels/triton/gemm_rows_splitk_64x64.py:225-323)
+and launches ``tq_gemm_mixed_rows`` (``csrc/tq_gemm.hip``) on the current
+stream.  One extra keyword, ``tile_layout``, names the storage order inside
+each packed tile: ``"row_major"`` (the reference packer's order, the default)
+or ``"mfma"`` (the operand-major order this build's packer writes).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+
+
+def _check_tiles(name: str, t: torch.Tensor, dtype) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must have dtype {dtype}, got {t.dtype}")
+    if t.numel() and (not t.is_contiguous() or t.data_ptr() % 16):
+        raise ValueError(f"{name} must be contiguous and 16-byte aligned")
+
+
+def gemm_mixed_rows_splitk(
+    *,
+    x_fp: torch.Tensor,
+    x_int8: torch.Tensor,
+    sx: torch.Tensor,
+    int8_tiles: torch.Tensor,
+    int8_scales: torch.Tensor,
+    int8_tile_ids: torch.Tensor,
+    int8_row_ptr: torch.Tensor,
+    fp16_tiles: torch.Tensor,
+    fp16_tile_ids: torch.Tensor,
+    fp16_row_ptr: torch.Tensor,
+    M: int,
+    K: int,
+    n_tr: int,
+    n_tc: int,
+    out_dtype: torch.dtype,
+    bias: Optional[torch.Tensor] = None,
+    split_k: Optional[int] = None,
+    out: Optional[torch.Tensor] = None,
+    tile_layout: str = "row_major",
+) -> torch.Tensor:
+    """Return x @ W^T (+ bias) for a packed mixed INT8/16-bit weight.
+
+    ``bias`` must already have dtype ``out_dtype`` and be contiguous.  ``out``
+    (optional) is an (N, M) tensor with unit column stride to write into.
+    ``split_k`` (optional, >= 1) fixes how many partitions of each row tile's
+    tile list are reduced per output tile (in fixed order); ``None`` picks it
+    from the shape.  Results are bitwise reproducible for fixed arguments.
+    """
+    nat.require_device(x_fp, x_int8, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+                       fp16_tiles, fp16_tile_ids, fp16_row_ptr, bias, out)
+    n = int(x_fp.shape[0])
+    M, K, n_tr, n_tc = int(M), int(K), int(n_tr), int(n_tc)
+    if out is None:
+        out = torch.empty((n, M), device=x_fp.device, dtype=out_dtype)
+    elif tuple(out.shape) != (n, M) or out.dtype != out_dtype or out.stride(1) != 1:
+        raise ValueError("out must be an (N, M) tensor of out_dtype with unit column stride")
+    if x_int8.dim() != 2 or x_int8.shape[0] != n or x_int8.shape[1] < K or x_int8.stride(1) != 1:
+        raise ValueError("x_int8 must be an (N, >=K) int8 tensor with unit column stride")
+    if x_fp.dim() != 2 or x_fp.shape[1] < K or x_fp.stride(1) != 1:
+        raise ValueError("x_fp must be an (N, >=K) tensor with unit column stride")
+    if sx.dtype != torch.float32 or sx.numel() < n_tc or not sx.is_contiguous():
+        raise ValueError("sx must be a contiguous float32 tensor of n_tc scales")
+    _check_tiles("int8_tiles", int8_tiles, torch.int8)
+    has16 = fp16_tiles.numel() != 0
+    if has16:
+        _check_tiles("fp16_tiles", fp16_tiles, x_fp.dtype)
+    if bias is not None and (bias.dtype != out_dtype or not bias.is_contiguous() or bias.numel() < M):
+        raise ValueError("bias must be a contiguous tensor of out_dtype with M entries")
+    if split_k is not None and int(split_k) < 1:
+        raise ValueError(f"split_k must be >= 1, got {split_k}")
+    if tile_layout not in nat.TQ_LAYOUT:
+        raise ValueError(f"tile_layout must be one of {tuple(nat.TQ_LAYOUT)}, got {tile_layout!r}")
+    for name, t in (("int8_tile_ids", int8_tile_ids), ("int8_row_ptr", int8_row_ptr),
+                    ("fp16_tile_ids", fp16_tile_ids), ("fp16_row_ptr", fp16_row_ptr)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 tensor")
+    if n == 0 or M == 0:
+        return out
+    rc = nat.lib().tq_gemm_mixed_rows(
+        nat.ptr(x_int8), x_int8.stride(0), nat.ptr(sx),
+        nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
+        nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
+        nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
+        nat.ptr(fp16_row_ptr) if has16 else None,
+        nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
+        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], None, 0,
+        nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_gemm_mixed_rows")
+    return out
+
+
+def gemm_tile_products_i32(
+    *,
+    x_int8: torch.Tensor,
+    int8_tiles: torch.Tensor,
+    int8_tile_ids: torch.Tensor,
+    int8_row_ptr: torch.Tensor,
+    K: int,
+    n_tr: int,
+    n_tc: int,
+    tile_layout: str = "row_major",
+) -> torch.Tensor:
+    """TEST ONLY: exact INT32 products [T8, N, 64] of every INT8 tile with every
+    token row, from the same device tile routine as the GEMM (the quantity the
+    reference's tl.dot produces at gemm_rows_splitk_64x64.py:134)."""
+    nat.require_device(x_int8, int8_tiles, int8_tile_ids, int8_row_ptr)
+    _check_tiles("int8_tiles", int8_tiles, torch.int8)
+    n = int(x_int8.shape[0])
+    out = torch.zeros((int8_tiles.shape[0], n, 64), device=x_int8.device, dtype=torch.int32)
+    if n == 0 or int8_tiles.shape[0] == 0:
+        return out
+    rc = nat.lib().tq_gemm_tile_products_i32(
+        nat.ptr(x_int8), x_int8.stride(0), nat.ptr(int8_tiles), nat.ptr(int8_tile_ids),
+        nat.ptr(int8_row_ptr), n, int(K), int(n_tr), int(n_tc), nat.TQ_LAYOUT[tile_layout],
+        nat.ptr(out), nat.stream_handle(x_int8.device))
+    nat.check(rc, "tq_gemm_tile_products_i32")
+    return out

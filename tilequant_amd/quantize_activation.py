@@ -1,0 +1,86 @@
+"""Activation INT8 quantization launchers (HIP, gfx950).
+
+Same names, arguments and return values as the reference's Triton launchers
+(src/kernels/triton/quantize_activation.py:118-203); the kernels behind them
+are ``tq_act_*`` in ``csrc/tq_act_quant.hip``.  One scale per 64-column tile,
+taken over ALL rows of the call.
+"""
+from __future__ import annotations
+
+from typing import Dict, Tuple
+
+import torch
+
+from . import _native as nat
+
+_WORKSPACE: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _absmax_workspace(x: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Per (device, stream) fp32 partial-max buffer, grown only (the analogue of
+    the reference's per-stream split-K workspace, gemm_rows_splitk_64x64.py:193-215)."""
+    need = int(nat.lib().tq_act_absmax_workspace_elems(n, k))
+    dev = x.device
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), nat.stream_handle(dev))
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty((max(need, 1 << 14),), device=dev, dtype=torch.float32)
+        _WORKSPACE[key] = ws
+    return ws
+
+
+def _check_x(x_fp: torch.Tensor) -> None:
+    if x_fp.dim() != 2:
+        raise ValueError(f"Expected 2D activation tensor, got shape={tuple(x_fp.shape)}")
+    nat.require_device(x_fp)
+    nat.dtype_code(x_fp.dtype)
+
+
+def quantize_activation_tile_absmax_fused(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """absmax -> scale -> codes in one launch (reference :118-155)."""
+    _check_x(x_fp)
+    n, k = x_fp.shape
+    if k == 0:
+        return torch.empty_like(x_fp, dtype=torch.int8), torch.empty((0,), device=x_fp.device, dtype=torch.float32)
+    n_tc = (int(k) + 63) // 64
+    x_q = torch.empty((n, k), device=x_fp.device, dtype=torch.int8)
+    sx = torch.empty((n_tc,), device=x_fp.device, dtype=torch.float32)
+    rc = nat.lib().tq_act_quant_fused(
+        nat.ptr(x_fp), x_fp.stride(0), x_fp.stride(1), nat.dtype_code(x_fp.dtype), int(n), int(k),
+        nat.ptr(x_q), x_q.stride(0), nat.ptr(sx), nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_act_quant_fused")
+    return x_q, sx
+
+
+def activation_tile_absmax_scales_64_fused(x_fp: torch.Tensor) -> torch.Tensor:
+    """Scales only, over all rows (reference :158-176)."""
+    _check_x(x_fp)
+    n, k = x_fp.shape
+    if k == 0:
+        return torch.empty((0,), device=x_fp.device, dtype=torch.float32)
+    n_tc = (int(k) + 63) // 64
+    sx = torch.empty((n_tc,), device=x_fp.device, dtype=torch.float32)
+    ws = _absmax_workspace(x_fp, int(n), int(k))
+    rc = nat.lib().tq_act_absmax_scales(
+        nat.ptr(x_fp), x_fp.stride(0), x_fp.stride(1), nat.dtype_code(x_fp.dtype), int(n), int(k),
+        nat.ptr(sx), nat.ptr(ws), ws.numel(), nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_act_absmax_scales")
+    return sx
+
+
+def quantize_activation_tile_with_scales_64_fused(x_fp: torch.Tensor, sx: torch.Tensor) -> torch.Tensor:
+    """Codes from given per-tile scales (reference :179-203)."""
+    _check_x(x_fp)
+    nat.require_device(sx)
+    n, k = x_fp.shape
+    if k == 0:
+        return torch.empty_like(x_fp, dtype=torch.int8)
+    n_tc = (int(k) + 63) // 64
+    if sx.numel() != n_tc or sx.dtype != torch.float32 or not sx.is_contiguous():
+        raise ValueError(f"sx must be a contiguous float32 tensor of {n_tc} scales")
+    x_q = torch.empty((n, k), device=x_fp.device, dtype=torch.int8)
+    rc = nat.lib().tq_act_quant_with_scales(
+        nat.ptr(x_fp), x_fp.stride(0), x_fp.stride(1), nat.dtype_code(x_fp.dtype), int(n), int(k),
+        nat.ptr(sx), nat.ptr(x_q), x_q.stride(0), nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_act_quant_with_scales")
+    return x_q
