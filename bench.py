@@ -1,0 +1,345 @@
+#!/usr/bin/env python3
+"""Benchmark of the mixed INT8/BF16 tile linear path on one MI355X.
+
+Workload ("M=4 decode"): the Llama-3.2-3B decoder
+linear set -- Q/K/V (stacked, 5120x3072), O (3072x3072), Gate/Up (stacked,
+16384x3072), Down (3072x8192) -- for all 28 layers, 4 tokens, a seeded
+uniform keep01 tile mask per projection, W ~ N(0, 0.02) bf16, activations
+N(0, 1) with 0.5% outlier channels x20.  A step is one pass of the hot path
+(activation quantization + mixed tile GEMM) through the 112 projections of
+the 28 layers: 2.85 GB of distinct packed weights, well above the 256 MB
+Infinity Cache.  The step is captured once as a HIP graph and replayed.
+
+Prints ONE JSON line: value = whole-job TOPS (2*tokens*M*K summed over the
+step / step time); roofline = the GEMM kernel's packed-weight GB/s against
+8 TB/s HBM, from HIP events bracketing every GEMM launch; cpu_baseline = the
+CPU oracle (oracle/tq_oracle.c, the reference's arithmetic) on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+from types import SimpleNamespace
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HIDDEN, KV, MLP, LAYERS = 3072, 1024, 8192, 28
+HBM_PEAK_GBPS = 8000.0
+# projection groups of one decoder layer: (name, member output widths, K)
+GROUPS = (("qkv", (HIDDEN, KV, KV), HIDDEN), ("o", (HIDDEN,), HIDDEN),
+          ("gate_up", (MLP, MLP), HIDDEN), ("down", (HIDDEN,), MLP))
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=4)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--keep", type=float, default=0.01)
+    ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU work timed for the baseline")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense bf16 context measurement")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def keep_ids(n_tr, n_tc, frac, rng):
+    import numpy as np
+
+    n = n_tr * n_tc
+    k = max(1, int(math.ceil(frac * n)))
+    return np.sort(rng.choice(n, size=k, replace=False)).astype(np.int64)
+
+
+def build_layers(args, device):
+    """Pack every projection of every layer with the HIP packer (weights made on the GPU)."""
+    import numpy as np
+    import torch
+    from tilequant_amd.mixed_linear import MixedLinear
+    from tilequant_amd.pack import concat_packs_along_rows, pack_weight_from_tile_ids
+
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    rng = np.random.default_rng(args.seed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed)
+    layers, packed_bytes, ops, t16_total, t8_total, max_row16 = [], 0, 0, 0, 0, 0
+    for _ in range(args.layers):
+        mods = {}
+        for name, widths, k in GROUPS:
+            packs = []
+            for m in widths:
+                W = (torch.randn((m, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+                n_tr, n_tc = m // 64, k // 64
+                ids16 = keep_ids(n_tr, n_tc, args.keep, rng)
+                mask = np.zeros(n_tr * n_tc, bool)
+                mask[ids16] = True
+                ids8 = np.flatnonzero(~mask)
+                packs.append(pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc,
+                                                       int8_tile_ids=torch.from_numpy(ids8),
+                                                       fp16_tile_ids=torch.from_numpy(ids16), cfg=cfg))
+                del W
+            pack = packs[0] if len(packs) == 1 else concat_packs_along_rows(packs)
+            lin = MixedLinear(pack, None, cfg)
+            t8, t16 = int(pack.int8_tiles.shape[0]), int(pack.fp16_tiles.shape[0])
+            t8_total += t8
+            t16_total += t16
+            packed_bytes += 4096 * t8 + 8192 * t16 + 4 * t8
+            ops += 2 * args.tokens * pack.M_orig * pack.K_orig
+            rp = pack.fp16_row_ptr.cpu()
+            max_row16 = max(max_row16, int((rp[1:] - rp[:-1]).max()))
+            mods[name] = lin
+        layers.append(mods)
+    torch.cuda.synchronize()
+    return layers, dict(packed_bytes=packed_bytes, ops=ops, t8=t8_total, t16=t16_total, max_bf16_per_row=max_row16)
+
+
+def make_inputs(args, device):
+    import torch
+
+    g = torch.Generator(device="cpu")
+    g.manual_seed(args.seed + 1)
+    xs = {}
+    for name, _, k in GROUPS:
+        x = torch.randn((args.tokens, k), generator=g)
+        ch = torch.randperm(k, generator=g)[: round(0.005 * k)]
+        x[:, ch] *= 20
+        xs[name] = x.to(torch.bfloat16).to(device)
+    return xs
+
+
+def cpu_baseline(args, layers, xs):
+    """Time the CPU oracle (reference arithmetic, OpenMP) on the first cpu_layers layers."""
+    import numpy as np
+    import torch
+    from oracle import native as onat
+    from oracle import numerics as nm
+    from oracle import packing as opk
+
+    onat.lib()
+    work = []
+    ops = 0
+    for li in range(min(args.cpu_layers, len(layers))):
+        for name, _, k in GROUPS:
+            lin = layers[li][name]
+            w8 = opk.from_mfma_int8(lin.int8_tiles.cpu().numpy())
+            w16 = nm.bf16_bits_to_f32(opk.from_mfma_16bit(lin.fp16_tiles.cpu().view(torch.int16).numpy().view(np.uint16)))
+            work.append(dict(x=xs[name].float().cpu().numpy(), w8=w8, sw=lin.int8_scales.cpu().numpy(),
+                             ids8=lin.int8_tile_ids.cpu().numpy(), rp8=lin.int8_row_ptr.cpu().numpy(), w16=w16,
+                             ids16=lin.fp16_tile_ids.cpu().numpy(), rp16=lin.fp16_row_ptr.cpu().numpy(),
+                             n_tr=lin.n_tr, n_tc=lin.n_tc, M=lin.M_orig, K=lin.K_orig))
+            ops += 2 * args.tokens * lin.M_orig * lin.K_orig
+
+    def run():
+        for w in work:
+            sx = onat.act_scales(w["x"])
+            xq = onat.act_quant(w["x"], sx)
+            onat.gemm_mixed(xq, sx, w["x"], w["w8"], w["sw"], w["ids8"], w["rp8"], w["w16"], w["ids16"],
+                            w["rp16"], w["n_tr"], w["n_tc"], w["M"], w["K"])
+
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t_start < args.cpu_seconds:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 30.0:
+            break
+    t = statistics.median(times)
+    return {"value": ops / t / 1e12, "unit": "TOPS", "cores": onat.num_threads(), "kind": "port",
+            "sample": f"{min(args.cpu_layers, len(layers))} of {len(layers)} layers of the same linear set at "
+                      f"{args.tokens} tokens (act quant + tile GEMM, reference-order fp32, oracle/tq_oracle.c, "
+                      f"OpenMP), median of {len(times)} reps over {sum(times):.1f} s, {t * 1e3:.1f} ms per sample",
+            "ms_per_sample": t * 1e3}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from tilequant_amd import _native
+    from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    _native.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    layers, info = build_layers(args, device)
+    xs = make_inputs(args, device)
+
+    def step():
+        outs = []
+        for mods in layers:
+            for name, _, _ in GROUPS:
+                outs.append(mods[name](xs[name]))
+        return outs
+
+    # eager warm-up, then capture one step as a HIP graph
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):   # the warm-up stream: workspaces already exist
+        outs = step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+
+    # eager step time (python dispatch + launches), for context
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    eager_s = (time.perf_counter() - t0) / 3
+
+    # GEMM kernel duration: HIP events on the launch stream bracket every GEMM
+    # launch of one step (activations quantized beforehand)
+    quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in GROUPS}
+    launches = []
+    for mods in layers:
+        for name, _, _ in GROUPS:
+            lin = mods[name]
+            xq, sx = quant[name]
+            launches.append((lin, name, xq, sx, torch.empty((args.tokens, lin.M_orig), device=device,
+                                                            dtype=torch.bfloat16)))
+
+    def gemm(lin, name, xq, sx, out):
+        gemm_mixed_rows_splitk(x_fp=xs[name], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                               int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                               int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                               fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr, M=lin.M_orig,
+                               K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc, out_dtype=torch.bfloat16, out=out,
+                               tile_layout=lin.tile_layout)
+
+    for item in launches:
+        gemm(*item)
+    torch.cuda.synchronize()
+    # Event pairs around every GEMM launch.  A calibrated spin kernel at the
+    # head of the stream keeps the GPU busy while the host enqueues all the
+    # pairs, so the GPU then runs them back to back and the events measure the
+    # kernels, not host launch overhead.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(1_000_000)
+    e1.record()
+    torch.cuda.synchronize()
+    cycles_per_ms = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    per_group = {name: [] for name, _, _ in GROUPS}
+    reps = max(3, min(args.steps, 10))
+    total_ms, n_launch = 0.0, 0
+    gemm_graph_ms = []
+    for _ in range(reps):
+        pairs = [(item[1], torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for item in launches]
+        torch.cuda._sleep(int(cycles_per_ms * 30))
+        for item, (_, a, b) in zip(launches, pairs):
+            a.record()
+            gemm(*item)
+            b.record()
+        torch.cuda.synchronize()
+        gemm_graph_ms.append(pairs[0][1].elapsed_time(pairs[-1][2]))
+        for name, a, b in pairs:
+            ms = a.elapsed_time(b)
+            per_group[name].append(ms)
+            total_ms += ms
+            n_launch += 1
+    gemm_avg_s = total_ms / n_launch / 1e3
+    bytes_per_launch = info["packed_bytes"] / len(launches)
+    achieved = bytes_per_launch / gemm_avg_s / 1e9
+    group_us = {name: statistics.median(v) * 1e3 for name, v in per_group.items()}
+
+    # dense bf16 context: the same linear set through torch.nn.functional.linear (hipBLASLt)
+    dense = None
+    if not args.no_dense:
+        ws = [{name: torch.randn((sum(w), k), device=device, dtype=torch.bfloat16) * 0.02 for name, w, k in GROUPS}
+              for _ in range(args.layers)]
+
+        def dstep():
+            return [torch.nn.functional.linear(xs[name], lw[name]) for lw in ws for name, _, _ in GROUPS]
+
+        for _ in range(2):
+            dstep()
+        torch.cuda.synchronize()
+        dg = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            dstep()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(dg, stream=s):
+            dstep()
+        for _ in range(args.warmup):
+            dg.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            dg.replay()
+        torch.cuda.synchronize()
+        d_s = (time.perf_counter() - t0) / args.steps
+        dense_bytes = sum(sum(w) * k * 2 for _, w, k in GROUPS) * args.layers
+        dense = {"ms_per_step": d_s * 1e3, "tops": info["ops"] / d_s / 1e12, "gbps": dense_bytes / d_s / 1e9,
+                 "speedup_of_tilequant": d_s / step_s}
+        del ws
+
+    cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
+
+    result = {
+        "metric": "mixed tile GEMM TOPS + % roofline (M=4 decode, M=8192 prefill); TPOT",
+        "value": info["ops"] / step_s / 1e12,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random-init weights and activations, uniform keep01 tile masks)",
+        "config": {"workload": f"Llama-3.2-3B decoder linear set x {args.layers} layers at decode "
+                               f"(BASELINE configs[1]), {args.tokens} tokens, keep{int(args.keep * 100):02d} "
+                               "uniform tile mask, HIP-graph step of quant + mixed GEMM for QKV/O/GateUp/Down",
+                   "tokens": args.tokens, "layers": args.layers, "keep": args.keep,
+                   "packed_weight_bytes": info["packed_bytes"], "int8_tiles": info["t8"], "bf16_tiles": info["t16"],
+                   "max_bf16_tiles_per_row_tile": info["max_bf16_per_row"]},
+        "gbps_packed_weights": info["packed_bytes"] / step_s / 1e9,
+        "hbm_frac_step": info["packed_bytes"] / step_s / 1e9 / HBM_PEAK_GBPS,
+        "eager_ms_per_step": eager_s * 1e3,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "tq::gemm_rows_kernel", "avg_launch_us": gemm_avg_s * 1e6,
+                     "bytes_per_launch": bytes_per_launch, "launches_per_step": len(launches),
+                     "group_median_us": group_us,
+                     "gemm_back_to_back_ms": statistics.median(gemm_graph_ms),
+                     "timing": "HIP events around each of the step's 112 GEMM launches, enqueued behind a "
+                               "spin kernel so they run back to back on the launch stream"},
+        "dense_bf16": dense,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

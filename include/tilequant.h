@@ -89,8 +89,15 @@ int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64_t x_stride
  * output tile.  Results are bitwise reproducible for fixed arguments.
  *
  * Replaces gemm_mixed_rows_splitk (src/kernels/triton/gemm_rows_splitk_64x64.py:225-323,
- * kernel :78-190).  workspace / counters are the reference's per-stream
- * split-K buffers (:193-215); size them with tq_gemm_workspace_elems. */
+ * kernel :78-190).  `workspace` is the reference's per-stream split-K buffer
+ * (:193-215): tq_gemm_workspace_elems() fp32 elements, ZERO-FILLED before its
+ * first use.  Its first 4096 elements are int32 arrival counters (one per row
+ * tile; more row tiles than that run unsplit), the fp32 split partials follow.
+ * Each launch leaves its arrival counters at zero again, so one
+ * buffer serves every launch on one stream (launches on different streams
+ * need different buffers).  Without a large enough workspace an automatic
+ * schedule uses one split; an explicit split_k > 1 then fails with
+ * TQ_ERR_WORKSPACE. */
 int64_t tq_gemm_workspace_elems(int n, int m, int n_tr, int n_tc, int split_k);
 int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
                        const int8_t* int8_tiles, const float* int8_scales,
@@ -101,6 +108,26 @@ int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const floa
                        int out_dtype, const void* bias, int n, int m, int k, int n_tr,
                        int n_tc, int split_k, int tile_layout, float* workspace,
                        int64_t workspace_elems, void* stream);
+
+/* Largest n tq_linear_mixed_fused accepts for input width k: at most 16, and
+ * the n x ceil(k/64)*64 int8 codes (+ scales) must fit 64 KiB of LDS. */
+int tq_linear_mixed_fused_max_tokens(int k);
+
+/* Activation quantization + the mixed tile GEMM in one launch, for decode
+ * sizes (n <= tq_linear_mixed_fused_max_tokens(k)).  Equivalent, bit for bit, to tq_act_quant_fused followed by
+ * tq_gemm_mixed_rows with the same split_k: each workgroup quantizes the
+ * column tiles of its own split (same closed form) instead of reading codes
+ * from memory.  No reference counterpart: the reference always runs the two
+ * kernels (src/models/mixed_linear.py:233-239 -> quant_utils.py:119-134 and
+ * gemm_rows_splitk_64x64.py:225-323).  Workspace as for tq_gemm_mixed_rows. */
+int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                          const int8_t* int8_tiles, const float* int8_scales,
+                          const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                          const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                          const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                          int out_dtype, const void* bias, int n, int m, int k, int n_tr, int n_tc,
+                          int split_k, int tile_layout, float* workspace, int64_t workspace_elems,
+                          void* stream);
 
 /* TEST-ONLY.  Writes the exact INT32 product of every INT8 tile with every
  * token row, products[t][row][j] (int32 [T8, n, 64]), computed by the same

@@ -115,3 +115,25 @@ def test_empty_inputs():
     assert q.shape == (0, 192) and torch.equal(sx.cpu(), torch.ones(3))
     q, sx = quantize_activation_tile_absmax_fused(torch.empty((4, 0), dtype=torch.bfloat16, device="cuda"))
     assert q.shape == (4, 0) and sx.numel() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_exact_half_integer_quotients_round_half_even(dtype):
+    # absmax 15.875 = 127/8 gives the scale 0.125 exactly; x = (k + 0.5) * 0.125
+    # are exact in bf16 and fp16, so every x / s is an exact tie k + 0.5 that
+    # must round to even (the reciprocal-multiply code path detects these)
+    # each 64-column tile: 63 tie values and its own absmax 15.875
+    x = np.zeros((2, 256), np.float32)
+    for t, (k0, sign) in enumerate([(0, 1), (0, -1), (63, 1), (63, -1)]):
+        k = np.arange(k0, k0 + 63, dtype=np.float32)
+        x[0, 64 * t:64 * t + 63] = sign * (k + 0.5) * 0.125
+        x[1, 64 * t + 63] = 15.875
+    xt = torch.from_numpy(x).to(dtype)
+    q, sx = quantize_activation_tile_absmax_fused(xt.cuda())
+    _check(xt, q, sx)
+    assert torch.all(sx.cpu() == 0.125)
+    qq = q.cpu()
+    assert int(qq[0, 0]) == 0 and int(qq[0, 1]) == 2 and int(qq[0, 2]) == 2      # 0.5->0, 1.5->2, 2.5->2
+    assert int(qq[0, 64]) == 0 and int(qq[0, 65]) == -2 and int(qq[0, 128]) == 64  # -1.5->-2, 63.5->64
+    sx2 = activation_tile_absmax_scales_64_fused(xt.cuda())
+    assert torch.equal(quantize_activation_tile_with_scales_64_fused(xt.cuda(), sx2), q)

@@ -215,3 +215,111 @@ def test_empty_token_batch():
     xq = torch.empty((0, 128), dtype=torch.int8, device="cuda")
     y = _gemm(pack, xd, xq, torch.ones(2, device="cuda"))
     assert y.shape == (0, 128)
+
+
+# --------------------------------------------------------------------------
+# split-K decode schedule and the fused quantize + GEMM launch
+# --------------------------------------------------------------------------
+
+from tilequant_amd.gemm_rows_splitk_64x64 import linear_mixed_fused  # noqa: E402
+
+
+def _fused(pack, xd, bias=None, split_k=None, out_dtype=torch.bfloat16):
+    return linear_mixed_fused(
+        x_fp=xd, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales, int8_tile_ids=pack.int8_tile_ids,
+        int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles, fp16_tile_ids=pack.fp16_tile_ids,
+        fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig, n_tr=pack.n_tr, n_tc=pack.n_tc,
+        out_dtype=out_dtype, bias=bias, split_k=split_k, tile_layout=pack.tile_layout)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 7, 8, 13, 16])
+def test_fused_equals_two_launch_path_bitwise(n):
+    W, pack, ids16 = _case(3072, 3072, 0.01, seed=900 + n)
+    x = make_x(n, 3072, seed=901 + n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    for split_k in (None, 1, 3, 8):
+        y2 = _gemm(pack, xd, xq, sx, split_k=split_k)
+        y1 = _fused(pack, xd, split_k=split_k)
+        assert torch.equal(y1, y2), f"split_k={split_k}"
+    op = oracle_pack(W, ids16)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y1, acc, sab, 48)
+
+
+@pytest.mark.parametrize("m,k,frac", [(200, 300, 0.2), (384, 640, 0.05), (128, 64, 0.5), (1024, 8192, 0.02)])
+def test_fused_ragged_bias_and_fp16(m, k, frac):
+    for dtype in (torch.bfloat16, torch.float16):
+        W, pack, ids16 = _case(m, k, frac, seed=m + k, dtype=dtype)
+        x = make_x(5, k, seed=m - k, dtype=dtype)
+        xd = x.cuda()
+        bias = (torch.randn(m, generator=torch.Generator().manual_seed(3)) * 0.3).to(torch.bfloat16).cuda()
+        xq, sx = quantize_activation_tile_absmax(xd)
+        assert torch.equal(_fused(pack, xd, bias=bias), _gemm(pack, xd, xq, sx, bias=bias))
+        assert torch.equal(_fused(pack, xd, out_dtype=torch.float16),
+                           _gemm(pack, xd, xq, sx, out_dtype=torch.float16))
+    # strided rows (a row slice of a wider activation)
+    W, pack, _ = _case(256, 512, 0.1, seed=77)
+    big = make_x(6, 1024, seed=78).cuda()
+    xs = big[:, 256:768]
+    xq, sx = quantize_activation_tile_absmax(xs.contiguous())
+    assert torch.equal(_fused(pack, xs), _gemm(pack, xs.contiguous(), xq, sx))
+
+
+def test_split_k_counters_reset_over_many_launches_and_graph_replays():
+    W, pack, ids16 = _case(1024, 3072, 0.01, seed=950)
+    x = make_x(4, 3072, seed=951).cuda()
+    y0 = _fused(pack, x, split_k=8)
+    for _ in range(50):
+        assert torch.equal(_fused(pack, x, split_k=8), y0)
+    # captured in a HIP graph: replays reuse the same workspace and counters
+    out = torch.empty_like(y0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _fused(pack, x, split_k=8)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):   # same stream as the warm-up: reuses its workspace
+        out.copy_(_fused(pack, x, split_k=8))
+    for _ in range(5):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y0)
+        assert torch.equal(_fused(pack, x, split_k=8), y0)   # eager work between replays
+
+
+def test_fused_rejects_more_than_16_rows():
+    W, pack, _ = _case(128, 128, 0.1, seed=960)
+    with pytest.raises(ValueError):
+        _fused(pack, make_x(17, 128).cuda())
+
+
+def test_workspace_shared_by_calls_with_different_row_tile_counts():
+    """Regression: a call with more row tiles must not read an earlier call's
+    split partials as its arrival counters (the workspace is shared per stream)."""
+    cases = [_case(m, 3072, 0.01, seed=970 + m // 64) for m in (3072, 8192, 1024, 16384, 3072)]
+    x = make_x(4, 3072, seed=975)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    for _round in range(2):
+        for W, pack, ids16 in cases:
+            y = _fused(pack, xd)
+            assert torch.equal(y, _gemm(pack, xd, xq, sx))
+            acc, sab = _oracle_f64(pack, oracle_pack(W, ids16), x, xq_ref, sx_ref)
+            assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+def test_fused_quantization_handles_exact_ties():
+    W, pack, ids16 = _case(256, 256, 0.1, seed=990)
+    x = np.zeros((3, 256), np.float32)
+    for t, (k0, sign) in enumerate([(0, 1), (0, -1), (63, 1), (40, -1)]):
+        k = np.arange(k0, k0 + 63, dtype=np.float32)
+        x[t % 3, 64 * t:64 * t + 63] = sign * (k + 0.5) * 0.125
+        x[(t + 1) % 3, 64 * t + 63] = 15.875   # absmax -> scale 0.125 exactly
+    xt = torch.from_numpy(x).to(torch.bfloat16).cuda()
+    xq, sx = quantize_activation_tile_absmax(xt)
+    assert torch.equal(xq.cpu(), torch.from_numpy(nm.act_quant(x)[0]))
+    assert torch.equal(_fused(pack, xt), _gemm(pack, xt, xq, sx))

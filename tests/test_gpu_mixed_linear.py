@@ -150,3 +150,13 @@ def test_iaa_packing_matches_torch_restatement():
     assert int(near_tie.sum()) <= max(1, len(ids8) // 20)
     q_want = torch.clamp(torch.round(srcf / got_s[:, None, None]), -127, 127).to(torch.int8)
     assert torch.equal(pack.int8_tiles.cpu(), q_want)
+
+
+def test_fused_decode_option_is_bitwise_identical():
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    lin, W, ids16, _ = _linear(1024, 3072, 0.01, 80, cfg, bias=True)
+    fused_cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16", fused_decode=True)
+    lin_f = MixedLinear(lin.to_pack(), lin.bias.detach(), fused_cfg)
+    for n in (1, 4, 16):
+        x = make_x(n, 3072, seed=81 + n).cuda()
+        assert torch.equal(lin_f(x), lin(x))

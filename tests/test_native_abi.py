@@ -61,4 +61,13 @@ def test_argument_errors_return_before_any_launch(lib):
 def test_workspace_sizing(lib):
     assert lib.tq_act_absmax_workspace_elems(128, 3072) == 0
     assert lib.tq_act_absmax_workspace_elems(8192, 3072) == 32 * 48
+    # automatic decode plan: no cross-workgroup split, no workspace
     assert lib.tq_gemm_workspace_elems(16, 3072, 48, 48, 0) == 0
+    assert lib.tq_gemm_workspace_elems(4, 16384, 256, 48, 0) == 0
+    # explicit split_k = 8: a fixed 4096-entry counter region, then partials per
+    # (unit, split, row, 64 cols); units = 4 j-block groups per row tile below
+    # 192 row tiles, whole row tiles from there on
+    assert lib.tq_gemm_workspace_elems(16, 3072, 48, 48, 8) == 4096 + 48 * 4 * 8 * 16 * 64
+    assert lib.tq_gemm_workspace_elems(4, 16384, 256, 48, 8) == 4096 + 256 * 8 * 4 * 64
+    assert lib.tq_gemm_workspace_elems(4, 1 << 20, 1 << 14, 48, 8) == 0   # beyond the counter cap
+    assert lib.tq_gemm_workspace_elems(100, 3072, 48, 48, 0) == 0     # general kernel: none

@@ -42,6 +42,13 @@ _SIGNATURES = {
                                 _p, _i64, _i, _p,
                                 _i, _i, _i, _i, _i,
                                 _i, _i, _p, _i64, _p]),
+    "tq_linear_mixed_fused_max_tokens": (_i, [_i]),
+    "tq_linear_mixed_fused": (_i, [_p, _i64, _i,
+                                   _p, _p, _p, _p,
+                                   _p, _p, _p,
+                                   _p, _i64, _i, _p,
+                                   _i, _i, _i, _i, _i,
+                                   _i, _i, _p, _i64, _p]),
     "tq_gemm_tile_products_i32": (_i, [_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
     "tq_pack_int8_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
     "tq_pack_16bit_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p]),

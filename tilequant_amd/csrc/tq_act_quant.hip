@@ -52,7 +52,7 @@ __device__ inline float max8(u32x4 w, float m) {
 }
 
 template <class T>
-__device__ inline u32x2 codes8(u32x4 w, float s) {
+__device__ inline u32x2 codes8(u32x4 w, const CodeScale& s) {
   u32x2 out;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -60,8 +60,8 @@ __device__ inline u32x2 codes8(u32x4 w, float s) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       uint32_t word = w[h * 2 + i];
-      uint32_t lo = (uint32_t)(quant_code(T::to_f32((uint16_t)(word & 0xffffu)), s) & 0xff);
-      uint32_t hi = (uint32_t)(quant_code(T::to_f32((uint16_t)(word >> 16)), s) & 0xff);
+      uint32_t lo = (uint32_t)(s.code(T::to_f32((uint16_t)(word & 0xffffu))) & 0xff);
+      uint32_t hi = (uint32_t)(s.code(T::to_f32((uint16_t)(word >> 16))) & 0xff);
       packed |= (lo | (hi << 8)) << (16 * i);
     }
     out[h] = packed;
@@ -99,19 +99,20 @@ act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __re
   const int c = blockIdx.x, t = threadIdx.x;
   const float a = block_max(tile_absmax<T>(v, c, 0, v.n), red, kQuantThreads / kWave);
   const float s = act_scale_from_absmax<T>(a);
+  const CodeScale cs(s);
   if (t == 0) sx[c] = s;
   const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
   if (tile_vec_ok(v, c) && qvec) {
     const int col = c * kTile + (t % 8) * 8;
     for (int row = t / 8; row < v.n; row += kRowsPerPass)
-      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), s);
+      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), cs);
   } else {
     const int cols = min(kTile, v.k - c * kTile);
     for (int64_t e = t; e < (int64_t)v.n * kTile; e += kQuantThreads) {
       int row = (int)(e / kTile), kk = (int)(e % kTile);
       if (kk < cols) {
         float xv = T::to_f32(v.x[(int64_t)row * v.sn + (int64_t)(c * kTile + kk) * v.sk]);
-        q[(int64_t)row * ldq + c * kTile + kk] = (int8_t)quant_code(xv, s);
+        q[(int64_t)row * ldq + c * kTile + kk] = (int8_t)cs.code(xv);
       }
     }
   }
@@ -152,8 +153,8 @@ act_quant_scaled_kernel(XView v, const float* __restrict__ sx, int8_t* __restric
     const int64_t items = (int64_t)v.n * kv;
     for (int64_t it = first; it < items; it += stride) {
       const int row = (int)(it / kv), col = (int)(it % kv) * 8;
-      const float s = sx[col / kTile];
-      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), s);
+      const CodeScale cs(sx[col / kTile]);
+      *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(load8(v, row, col), cs);
     }
   } else {
     const int64_t items = (int64_t)v.n * v.k;

@@ -69,13 +69,51 @@ __device__ inline int quant_code(float v, float s) {
   return (int)q;
 }
 
+// Codes of a whole tile share one scale s: q = rint(v * (1/s)) equals
+// rint(fl(v / s)) for 16-bit v and s except when v / s is exactly a
+// half-integer k + 0.5 (then the product may land on either side).  Proof
+// sketch: v = a*2^e, s = b*2^f with integer a, b < 2^11, so a quotient that is
+// not a half-integer is at least 1/(2*2047) from every half-integer within
+// the clamp range (|v/s| <= 128), while two roundings move the product by at
+// most 128 * 2^-23 = 2^-16.  An exact half is detected exactly with one fma:
+// h = floor(t) + 0.5 and h*s are exact (<= 19 significant bits), so
+// fma(-h, s, v) == 0 iff v == h*s; rint(h) then rounds half to even like the
+// reference.  Subnormal scales (1/s overflows) take the IEEE divide.
+struct CodeScale {
+  float s, rcp;
+  bool exact_div;
+  __device__ explicit CodeScale(float scale)
+      : s(scale), rcp(1.0f / scale), exact_div(!(scale >= 1.1754943508222875e-38f)) {}
+  __device__ inline int code(float v) const {
+    if (exact_div) return quant_code(v, s);
+    const float t = v * rcp;
+    const float h = __builtin_floorf(t) + 0.5f;
+    float q = (__builtin_fmaf(-h, s, v) == 0.0f) ? __builtin_rintf(h) : __builtin_rintf(t);
+    q = fmaxf(fminf(q, 127.0f), -127.0f);
+    return (int)q;
+  }
+};
+
 // ---- wave reductions ----------------------------------------------------
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+// Max over the 64 lanes of a NON-NEGATIVE float (absolute values): integer
+// order of the bit patterns is float order, so DPP row operations (quad
+// swaps, half-row and row mirrors) reduce each 16-lane row in registers and
+// four v_readlane finish in scalar registers -- no LDS round trips.
+__device__ inline float wave_max_nonneg(float x) {
+  uint32_t v = __float_as_uint(x);
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+  return __uint_as_float(max(max(a, b), max(c, d)));
 }
+
+__device__ inline float wave_max(float v) { return wave_max_nonneg(v); }
 
 // Block-wide max over `nwaves` waves through a small LDS array; every thread
 // receives the result.  `red` must hold at least nwaves floats.

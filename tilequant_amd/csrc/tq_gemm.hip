@@ -56,9 +56,15 @@ struct GemmArgs {
   int out_bf16;   // output dtype: 1 bf16, 0 fp16
   int layout;     // TQ_LAYOUT_*
   int xvec;       // activations allow 16-byte loads (aligned rows, k == 64 * n_tc)
+  int splits;       // split-K decode kernel: splits per row tile
+  int32_t* counters;  // [n_tr] arrival counters (zero between launches)
+  float* partials;    // [n_tr, splits, n, 64] fp32 split partials
 };
 
 constexpr int kMaxWaves = 16;
+constexpr int kDecodeMaxTokens = 64;  // token counts served by gemm_splitk_kernel
+constexpr int kFusedMaxTokens = 16;   // token counts the fused quantize+GEMM path takes
+constexpr size_t kFusedMaxLds = 64 * 1024;   // the fused path keeps n x k int8 codes in LDS
 constexpr int kUnroll8 = 4;   // INT8 tiles in flight per wave
 constexpr int kUnroll16 = 2;  // 16-bit tiles in flight per wave
 
@@ -81,10 +87,18 @@ __device__ inline v4i load_w16(const GemmArgs& a, int p, int jb, int h, int lane
 }
 
 // A operand: 16 int8 codes of token row `row`, columns col .. col+15.
+// XVEC (aligned rows, k == 64 * n_tc) is a template switch in the split-K
+// kernel and a runtime one in the general kernel.
+template <int XVEC = -1>
 __device__ inline v4i load_xq(const GemmArgs& a, int row, int col) {
+  if constexpr (XVEC == 1) {
+    // branch-free: read a valid row, zero the padding rows with a select
+    const v4i v = *reinterpret_cast<const v4i*>(a.xq + (int64_t)min(row, a.n - 1) * a.ldq + col);
+    return row < a.n ? v : v4i{0, 0, 0, 0};
+  }
   if (row >= a.n) return v4i{0, 0, 0, 0};
   const int8_t* p = a.xq + (int64_t)row * a.ldq + col;
-  if (a.xvec) return *reinterpret_cast<const v4i*>(p);
+  if (XVEC == 1 || (XVEC == -1 && a.xvec)) return *reinterpret_cast<const v4i*>(p);
   uint32_t w[4] = {0, 0, 0, 0};
   for (int e = 0; e < 16; ++e)
     if (col + e < a.k) w[e >> 2] |= (uint32_t)(uint8_t)p[e] << (8 * (e & 3));
@@ -92,10 +106,15 @@ __device__ inline v4i load_xq(const GemmArgs& a, int row, int col) {
 }
 
 // A operand: 8 16-bit activations of row `row`, columns col .. col+7.
+template <int XVEC = -1>
 __device__ inline v4i load_xf(const GemmArgs& a, int row, int col) {
+  if constexpr (XVEC == 1) {
+    const v4i v = *reinterpret_cast<const v4i*>(a.xf + (int64_t)min(row, a.n - 1) * a.ldx + col);
+    return row < a.n ? v : v4i{0, 0, 0, 0};
+  }
   if (row >= a.n) return v4i{0, 0, 0, 0};
   const uint16_t* p = a.xf + (int64_t)row * a.ldx + col;
-  if (a.xvec) return *reinterpret_cast<const v4i*>(p);
+  if (XVEC == 1 || (XVEC == -1 && a.xvec)) return *reinterpret_cast<const v4i*>(p);
   uint32_t w[4] = {0, 0, 0, 0};
   for (int e = 0; e < 8; ++e)
     if (col + e < a.k) w[e >> 1] |= (uint32_t)p[e] << (16 * (e & 1));
@@ -120,6 +139,39 @@ __device__ inline v4f mfma16<Fp16>(v4i av, v4i bv, v4f c) {
 // that a malformed pack can never index sx / x out of range.
 __device__ inline int col_of(int id, int rbase, int n_tc) {
   return (int)min((unsigned)(id - rbase), (unsigned)(n_tc - 1));
+}
+
+// Sum the W waves' partial accumulators through LDS in wave order 0..W-1 (a
+// fixed order: bitwise reproducible), round to the output dtype, add bias
+// with the reference's double rounding, store.  D layout: lane l holds
+// column jb*16 + l%16 and tokens n0 + tb*16 + 4*(l/16) + v.
+template <int TB>
+__device__ inline void reduce_store(const GemmArgs& a, float* red, const v4f* acc, int W, int wave,
+                                    int lane, int r, int jb, int n0) {
+  constexpr int E = TB * 4 * 64;
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[(wave * TB * 4 + tb * 4 + v) * 64 + lane] = acc[tb][v];
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float sum = red[e];
+    for (int w = 1; w < W; ++w) sum += red[w * E + e];
+    const int ln = e & 63, tv = e >> 6, tb = tv >> 2, v = tv & 3;
+    const int row = n0 + tb * 16 + 4 * (ln >> 4) + v;
+    const int col = r * 64 + jb * 16 + (ln & 15);
+    if (row < a.n && col < a.m) {
+      uint16_t y;
+      if (a.out_bf16) {
+        y = Bf16::from_f32(sum);
+        if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+      } else {
+        y = Fp16::from_f32(sum);
+        if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+      }
+      a.out[(int64_t)row * a.ldo + col] = y;
+    }
+  }
 }
 
 // ---- the kernel -----------------------------------------------------------
@@ -250,31 +302,337 @@ gemm_rows_kernel(GemmArgs a) {
     }
   }
 
-  // ---------------- fixed-order reduction over waves + epilogue ----------------
-  constexpr int E = TB * 4 * 64;
+  reduce_store<TB>(a, red, acc, W, wave, lane, r, jb, n0);
+}
+
+// ---- split-K decode kernel (N <= 64 tokens) ---------------------------------
+//
+// Workgroup (r, s), s < S, owns split s of row tile r: INT8 positions
+// [lo8 + n8*s/S, lo8 + n8*(s+1)/S) and 16-bit positions likewise (the
+// reference's row-owned split-K, gemm_rows_splitk_64x64.py:121-124, 140-143).
+// Each of its W waves takes WHOLE 4 KiB tiles round-robin and issues the
+// four 1 KiB j-block loads of up to U tiles before any dependent work, so a
+// wave streams contiguous memory and has U*4 KiB in flight.  Per INT8 tile:
+// 4 j-blocks x TB token blocks of v_mfma_i32_16x16x64_i8, fp32 FMA by
+// sx[c]*sw[t]; per 16-bit tile: 4 x TB x 2 v_mfma_f32_16x16x32_{bf16,f16}.
+//
+// FUSED: the wave quantizes column tile c of the activation itself (absmax
+// over all n <= 16 rows, bf16/fp16-rounded scale, IEEE-divide codes -- the
+// same closed form as tq_act_quant) into a 1 KiB LDS slot and reads its A
+// operand back from there.  A split only needs its own column tiles, so the
+// activation quantization costs one extra pass per row tile instead of a
+// launch, and its results are bitwise those of the separate quantizer.
+//
+// Reduction: waves sum through LDS in wave order; with S > 1 every split
+// stores its fp32 partial (rows < n only), releases it at device scope and
+// bumps the row tile's arrival counter; the last arriver acquires, sums the
+// S partials in split order 0..S-1 (bitwise reproducible) and resets the
+// counter to zero for the next launch, as the reference's semaphore epilogue
+// (gemm_rows_splitk_64x64.py:159-183).  No waiting: no workgroup ever spins.
+
+template <int NPOW>
+struct QuantLanes {
+  static constexpr int kVpl = NPOW;          // values per lane
+  static constexpr int kLpr = 64 / NPOW;     // lanes per row
+};
+
+// This lane's VPL raw 16-bit activations of column tile c: row lane / lpr,
+// columns c*64 + (lane % lpr)*VPL .. +VPL, zero past k or at rows >= n.
+template <int NPOW, bool XVEC>
+struct XSlice {
+  static constexpr int kVpl = NPOW, kLpr = 64 / NPOW;
+  uint16_t raw[kVpl];
+  __device__ inline void load(const GemmArgs& a, int c, int lane) {
+    const int row = lane / kLpr;
+    const int col0 = c * 64 + (lane % kLpr) * kVpl;
+    if constexpr (XVEC) {
+      // branch-free: read a valid row, zero rows >= n afterwards
+      const uint16_t* p = a.xf + (int64_t)min(row, a.n - 1) * a.ldx + col0;
+      if constexpr (kVpl >= 8) {
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
+        for (int i = 0; i < kVpl / 8; ++i) {
+          const u32x4 w = reinterpret_cast<const u32x4*>(p)[i];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[(wave * TB * 4 + tb * 4 + v) * 64 + lane] = acc[tb][v];
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    float sum = red[e];
-    for (int w = 1; w < W; ++w) sum += red[w * E + e];
-    const int ln = e & 63, tv = e >> 6, tb = tv >> 2, v = tv & 3;
-    const int row = n0 + tb * 16 + 4 * (ln >> 4) + v;
-    const int col = r * 64 + jb * 16 + (ln & 15);
-    if (row < a.n && col < a.m) {
-      uint16_t y;
-      if (a.out_bf16) {
-        y = Bf16::from_f32(sum);
-        if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+          for (int j = 0; j < 4; ++j) {
+            raw[8 * i + 2 * j] = (uint16_t)(w[j] & 0xffffu);
+            raw[8 * i + 2 * j + 1] = (uint16_t)(w[j] >> 16);
+          }
+        }
       } else {
-        y = Fp16::from_f32(sum);
-        if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) raw[i] = p[i];
       }
-      a.out[(int64_t)row * a.ldo + col] = y;
+      if (row >= a.n) {
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) raw[i] = 0;
+      }
+      return;
+    }
+    const uint16_t* p = a.xf + (int64_t)row * a.ldx + col0;
+    if (row >= a.n) {
+#pragma unroll
+      for (int i = 0; i < kVpl; ++i) raw[i] = 0;
+    } else {
+#pragma unroll
+      for (int i = 0; i < kVpl; ++i) raw[i] = (XVEC || col0 + i < a.k) ? p[i] : (uint16_t)0;
     }
   }
+};
+
+// Quantizes a loaded column tile c into slot[row*ld + col] (int8 codes,
+// rows < n, columns of the tile) and returns sx[c]: the closed form of
+// tq_act_quant over all n rows.  Columns >= k get code 0, as the masked loads
+// of the unfused GEMM read them.
+template <class XT, int NPOW, bool XVEC>
+__device__ inline float quant_col_tile(const GemmArgs& a, const XSlice<NPOW, XVEC>& xs, int c, int lane,
+                                       int8_t* slot, int ld) {
+  constexpr int kVpl = NPOW, kLpr = 64 / NPOW;
+  const int row = lane / kLpr;
+  const int col0 = c * 64 + (lane % kLpr) * kVpl;
+  float v[kVpl];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    v[i] = XT::to_f32(xs.raw[i]);
+    m = fmaxf(m, fabsf(v[i]));
+  }
+  const float s = act_scale_from_absmax<XT>(wave_max_nonneg(m));
+  const CodeScale cs(s);
+  if (row < a.n) {
+    uint32_t words[(kVpl + 3) / 4] = {};
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+      const int q = (XVEC || col0 + i < a.k) ? cs.code(v[i]) : 0;
+      words[i / 4] |= (uint32_t)(q & 0xff) << (8 * (i % 4));
+    }
+    int8_t* dst = slot + row * ld + (lane % kLpr) * kVpl;
+    if constexpr (kVpl >= 4) {
+#pragma unroll
+      for (int w = 0; w < kVpl / 4; ++w) reinterpret_cast<uint32_t*>(dst)[w] = words[w];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kVpl; ++i) dst[i] = (int8_t)((words[0] >> (8 * i)) & 0xff);
+    }
+  }
+  return s;
+}
+
+// JBW = j-blocks (16 output features each) per workgroup: 4 = whole 4 KiB
+// tiles per wave; 1 = one 1 KiB j-block of each tile (four workgroups share
+// a row tile, so narrow outputs still fill the GPU without any
+// cross-workgroup reduction).  Launch bound: 16 waves at JBW 1, 8 at JBW 4.
+template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW>
+__global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
+gemm_splitk_kernel(GemmArgs a) {
+  // dynamic LDS: FUSED codes [n][64*n_tc] + sx[n_tc] during the main loop,
+  // the wave partials for the reduction afterwards (the two never overlap in time)
+  extern __shared__ float red[];
+  __shared__ int last_arriver;
+  constexpr int NJG = 4 / JBW;                  // j-block groups per row tile
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int S = a.splits;
+  const int unit = blockIdx.x / S, s = blockIdx.x - (blockIdx.x / S) * S;
+  const int r = unit / NJG, jb0 = (unit - (unit / NJG) * NJG) * JBW;
+  const int arow = lane & 15, akq = lane >> 4;
+  const int rbase = r * a.n_tc;
+
+  v4f acc[JBW][TB];
+#pragma unroll
+  for (int j = 0; j < JBW; ++j)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[j][tb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int lo8r = a.rp8[r], hi8r = a.rp8[r + 1];
+  const int n8r = hi8r - lo8r;
+  const int lo8 = lo8r + (n8r * s) / S, hi8 = lo8r + (n8r * (s + 1)) / S;
+  const int n8 = hi8 - lo8;
+
+  // ---------------- INT8 tiles: wave takes positions lo8 + wave + i*W ----------------
+  // Batches of U tiles: ids and weights of a batch are all in flight before
+  // the first wait; the load phases are branch-free (positions past the
+  // batch re-read the last valid tile, an L2 hit, and are never used).
+  int cs[U];
+  float sw[U];
+  v4i bw[U][JBW];
+  auto load_batch = [&](int p0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int pu = min(p0 + u * W, hi8 - 1);
+      cs[u] = col_of(a.ids8[pu], rbase, a.n_tc);
+      sw[u] = a.sw8[pu];
+#pragma unroll
+      for (int j = 0; j < JBW; ++j) bw[u][j] = load_w8(a, pu, jb0 + j, lane);
+    }
+  };
+  const int first_p = lo8 + wave;
+  if (first_p < hi8) load_batch(first_p);        // the first batch streams during the prologue
+
+  const int ldc = a.n_tc * 64;                    // FUSED: LDS code row stride
+  int8_t* codes = reinterpret_cast<int8_t*>(red);
+  float* sxl = reinterpret_cast<float*>(codes + ((a.n * ldc + 15) & ~15));
+  if constexpr (FUSED) {
+    // Prologue: the waves quantize column tiles c = wave, wave + W, ... of the
+    // activation into LDS (closed form of tq_act_quant), QB tiles per pass
+    // with all their loads issued first, while the weights are in flight.
+    constexpr int QB = 4;
+    for (int c0 = wave; c0 < a.n_tc; c0 += QB * W) {
+      XSlice<NPOW, XVEC> xs[QB];
+#pragma unroll
+      for (int q = 0; q < QB; ++q) xs[q].load(a, min(c0 + q * W, a.n_tc - 1), lane);
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        const int c = c0 + q * W;
+        if (c < a.n_tc) {
+          const float sxc = quant_col_tile<XT, NPOW, XVEC>(a, xs[q], c, lane, codes + c * 64, ldc);
+          if (lane == 0) sxl[c] = sxc;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  for (int p0 = first_p; p0 < hi8; p0 += U * W) {
+    if (p0 != first_p) load_batch(p0);
+    const int nu = min(U, (hi8 - p0 + W - 1) / W);   // valid tiles in this batch (uniform)
+    v4i ax[U][TB];
+    float sxs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if constexpr (FUSED) {
+        sxs[u] = sxl[cs[u]];
+        ax[u][0] = (arow < a.n) ? *reinterpret_cast<const v4i*>(codes + arow * ldc + cs[u] * 64 + akq * 16)
+                                : v4i{0, 0, 0, 0};
+      } else {
+        sxs[u] = a.sx[cs[u]];
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+          ax[u][tb] = load_xq<XVEC ? 1 : 0>(a, tb * 16 + arow, cs[u] * 64 + akq * 16);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (u < nu) {
+        const float sc = sxs[u] * sw[u];
+#pragma unroll
+        for (int j = 0; j < JBW; ++j)
+#pragma unroll
+          for (int tb = 0; tb < TB; ++tb) {
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[u][tb], bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
+          }
+      }
+  }
+
+  // ---------------- 16-bit tiles: rotation continues after the INT8 ones ----------------
+  if (a.w16 != nullptr) {
+    const int lo16r = a.rp16[r], hi16r = a.rp16[r + 1];
+    const int n16r = hi16r - lo16r;
+    const int lo16 = lo16r + (n16r * s) / S, hi16 = lo16r + (n16r * (s + 1)) / S;
+    const int first = (wave - (n8 % W) + W) % W;
+    for (int q = lo16 + first; q < hi16; q += W) {
+      const int c = col_of(a.ids16[q], rbase, a.n_tc);
+      v4i bw[JBW][2];
+#pragma unroll
+      for (int j = 0; j < JBW; ++j) {
+        bw[j][0] = load_w16(a, q, jb0 + j, 0, lane);
+        bw[j][1] = load_w16(a, q, jb0 + j, 1, lane);
+      }
+      v4i ax[TB][2];
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ax[tb][h] = load_xf<XVEC ? 1 : 0>(a, tb * 16 + arow, c * 64 + h * 32 + akq * 8);
+#pragma unroll
+      for (int j = 0; j < JBW; ++j)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          acc[j][tb] = mfma16<XT>(ax[tb][0], bw[j][0], acc[j][tb]);
+          acc[j][tb] = mfma16<XT>(ax[tb][1], bw[j][1], acc[j][tb]);
+        }
+    }
+  }
+
+  // ---------------- waves -> LDS -> one partial per workgroup ----------------
+  constexpr int E = JBW * TB * 4 * 64;   // (j, tb, v, lane)
+  if constexpr (FUSED) __syncthreads();   // every wave is done reading the codes
+#pragma unroll
+  for (int j = 0; j < JBW; ++j)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave * E + ((j * TB + tb) * 4 + v) * 64 + lane] = acc[j][tb][v];
+  __syncthreads();
+
+  // element e -> (row, column within the row tile); rows >= n are padding
+  auto coords = [&](int e, int& row, int& jcol) {
+    const int ln = e & 63, t = e >> 6, v = t & 3, tb = (t >> 2) % TB, j = (t >> 2) / TB;
+    row = tb * 16 + 4 * (ln >> 4) + v;
+    jcol = (jb0 + j) * 16 + (ln & 15);
+  };
+  auto store = [&](int row, int jcol, float sum) {
+    const int col = r * 64 + jcol;
+    if (col >= a.m) return;
+    uint16_t y;
+    if (a.out_bf16) {
+      y = Bf16::from_f32(sum);
+      if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+    } else {
+      y = Fp16::from_f32(sum);
+      if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+    }
+    a.out[(int64_t)row * a.ldo + col] = y;
+  };
+
+  if (S == 1) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      int row, jcol;
+      coords(e, row, jcol);
+      if (row >= a.n) continue;
+      float sum = red[e];
+      for (int w = 1; w < W; ++w) sum += red[w * E + e];
+      store(row, jcol, sum);
+    }
+    return;
+  }
+
+  // Cross-workgroup hand-off without cache-wide maintenance: partials are
+  // written with agent-scope (sc1, write-through) stores, every thread waits
+  // for its stores to complete, then one thread bumps the counter; the last
+  // arriver reads the partials with agent-scope loads that bypass the
+  // non-coherent L1/L2 copies.  (A device-scope __threadfence() would instead
+  // write back and invalidate the whole L2 of the XCD.)
+  float* part = a.partials + ((int64_t)unit * S + s) * a.n * 64;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int row, jcol;
+    coords(e, row, jcol);
+    if (row >= a.n) continue;
+    float sum = red[e];
+    for (int w = 1; w < W; ++w) sum += red[w * E + e];
+    __hip_atomic_store(part + row * 64 + jcol, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // every thread's stores must be complete (acknowledged at the coherence
+  // point) before the counter moves: on gfx9 stores count in vmcnt
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_arriver = (prev == S - 1);
+  }
+  __syncthreads();
+  if (!last_arriver) return;
+  const float* unitp = a.partials + (int64_t)unit * S * a.n * 64;
+  for (int e = threadIdx.x; e < a.n * JBW * 16; e += blockDim.x) {
+    const int row = e / (JBW * 16), jcol = jb0 * 16 + e % (JBW * 16);
+    const int off = row * 64 + jcol;
+    float sum = __hip_atomic_load(unitp + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = 1; t < S; ++t)
+      sum += __hip_atomic_load(unitp + (int64_t)t * a.n * 64 + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    store(row, jcol, sum);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side -----------------------------------------------------------
@@ -319,13 +677,129 @@ static bool xvec_ok(const GemmArgs& a) {
          (a.xf == nullptr || ((a.ldx % 8) == 0 && aligned16(a.xf)));
 }
 
+// Decode schedule.  Cross-workgroup reduction costs several microseconds of
+// serial latency on MI355X (write-through stores, a counter RMW, coherent
+// reads), more than the data time of a small GEMM, so the automatic plan
+// never splits: whole-tile workgroups (JBW 4) when the row tiles alone give
+// enough workgroups, else one 16-feature j-block per workgroup (JBW 1), and
+// W waves so each wave keeps a batch of U tiles in flight.  An explicit
+// split_k > 1 runs S = split_k splits with the reduction.
+constexpr int kWideRowTiles = 192;   // row tiles from which whole-tile workgroups fill the GPU
+
+// The arrival counters occupy a FIXED region at the head of the workspace so
+// that calls with different shapes never see another call's partials as
+// counters; shapes with more units than the cap run with one split.
+constexpr int kCounterCap = 4096;
+static int64_t counter_elems(int units) { (void)units; return kCounterCap; }
+
+struct SplitPlan {
+  int S, W, tb, jbw;
+};
+
+static int plan_u(int jbw, int tb) { return jbw == 1 ? (tb == 1 ? 8 : (tb == 2 ? 4 : 2)) : (tb == 1 ? 4 : (tb == 2 ? 2 : 1)); }
+
+static int plan_max_waves(int jbw, int tb) {
+  // LDS for the reduction: W * jbw * tb * 1 KiB <= 64 KiB; launch bound 16 / 8 waves
+  int w = 64 / (jbw * tb);
+  const int bound = jbw == 4 ? 8 : 16;
+  return w < bound ? w : bound;
+}
+
+static SplitPlan plan_split(int n, int n_tr, int n_tc, int split_k) {
+  SplitPlan p;
+  p.tb = pick_tb(n);
+  p.jbw = n_tr >= kWideRowTiles ? 4 : 1;
+  p.S = split_k > 1 ? split_k : 1;
+  const int units = n_tr * (4 / p.jbw);
+  if (p.S > 1 && units > kCounterCap) p.S = 1;
+  const int per_split = (n_tc + p.S - 1) / p.S;
+  const int U = plan_u(p.jbw, p.tb);
+  int W = (per_split + U - 1) / U;
+  const int wmax = plan_max_waves(p.jbw, p.tb);
+  if (W > wmax) W = wmax;
+  p.W = W < 1 ? 1 : W;
+  return p;
+}
+
+static int64_t split_workspace_elems(const SplitPlan& p, int n, int n_tr) {
+  const int64_t units = (int64_t)n_tr * (4 / p.jbw);
+  return p.S > 1 ? counter_elems((int)units) + units * p.S * n * 64 : 0;
+}
+
+template <class XT, bool FUSED, bool XVEC, int JBW>
+static void launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 grid, dim3 block, size_t lds,
+                           hipStream_t s) {
+  constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 2 : 1;
+  if constexpr (FUSED) {
+    const int n = a.n;
+    if (n <= 1) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>), grid, block, lds, s, a);
+    else if (n <= 2) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>), grid, block, lds, s, a);
+    else if (n <= 4) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>), grid, block, lds, s, a);
+    else if (n <= 8) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>), grid, block, lds, s, a);
+  } else {
+    switch (p.tb) {
+      case 1: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
+      case 2: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
+      default: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
+    }
+  }
+}
+
+// LDS of the fused prologue: codes [n][64 * n_tc] (16-byte aligned) + sx[n_tc].
+static size_t fused_lds_bytes(int n, int n_tc) {
+  return (((size_t)n * n_tc * 64 + 15) & ~(size_t)15) + (size_t)n_tc * sizeof(float);
+}
+
+template <class XT, bool FUSED>
+static hipError_t launch_split(GemmArgs a, const SplitPlan& p, float* ws, hipStream_t s) {
+  a.splits = p.S;
+  const int units = a.n_tr * (4 / p.jbw);
+  a.counters = reinterpret_cast<int32_t*>(ws);
+  a.partials = ws ? ws + counter_elems(units) : nullptr;
+  dim3 grid(units * p.S), block(p.W * kWave);
+  size_t lds = (size_t)p.W * p.jbw * p.tb * 4 * 64 * sizeof(float);
+  if (FUSED && fused_lds_bytes(a.n, a.n_tc) > lds) lds = fused_lds_bytes(a.n, a.n_tc);
+  if (p.jbw == 4) {
+    if (a.xvec) launch_split_v<XT, FUSED, true, 4>(a, p, grid, block, lds, s);
+    else launch_split_v<XT, FUSED, false, 4>(a, p, grid, block, lds, s);
+  } else {
+    if (a.xvec) launch_split_v<XT, FUSED, true, 1>(a, p, grid, block, lds, s);
+    else launch_split_v<XT, FUSED, false, 1>(a, p, grid, block, lds, s);
+  }
+  return hipGetLastError();
+}
+
+// Chooses the split plan and checks the workspace; without a (large enough)
+// workspace an automatic plan falls back to S = 1, an explicit split_k > 1 is
+// an error.
+static int resolve_plan(SplitPlan& p, int n, int n_tr, int split_k, float* ws, int64_t ws_elems) {
+  const int64_t need = split_workspace_elems(p, n, n_tr);
+  if (need == 0) return TQ_OK;
+  if (ws != nullptr && ws_elems >= need && ((uintptr_t)ws & 3u) == 0) return TQ_OK;
+  if (split_k > 1) return TQ_ERR_WORKSPACE;
+  p.S = 1;
+  return TQ_OK;
+}
+
 }  // namespace tq
 
 using namespace tq;
 
 extern "C" int64_t tq_gemm_workspace_elems(int n, int m, int n_tr, int n_tc, int split_k) {
-  (void)n; (void)m; (void)n_tr; (void)n_tc; (void)split_k;
-  return 0;  // the row-owned schedule reduces inside the workgroup
+  (void)m;
+  if (n <= 0 || n_tr <= 0 || n > kDecodeMaxTokens) return 0;   // larger n: no workspace
+  return split_workspace_elems(plan_split(n, n_tr, n_tc, split_k), n, n_tr);
+}
+
+static int check_gemm_common(int n, int m, int k, int n_tr, int n_tc, int x_dtype, int out_dtype,
+                             int tile_layout) {
+  if (n < 0 || m < 0 || k < 0 || n_tr < 0 || n_tc < 0) return TQ_ERR_ARG;
+  if ((int64_t)n_tr * 64 < m || (int64_t)n_tc * 64 < k) return TQ_ERR_ARG;
+  if (x_dtype != TQ_DTYPE_BF16 && x_dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (out_dtype != TQ_DTYPE_BF16 && out_dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (tile_layout != TQ_LAYOUT_ROW_MAJOR && tile_layout != TQ_LAYOUT_MFMA) return TQ_ERR_DTYPE;
+  return TQ_OK;
 }
 
 extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
@@ -337,12 +811,8 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                   int out_dtype, const void* bias, int n, int m, int k, int n_tr,
                                   int n_tc, int split_k, int tile_layout, float* workspace,
                                   int64_t workspace_elems, void* stream) {
-  (void)workspace; (void)workspace_elems;
-  if (n < 0 || m < 0 || k < 0 || n_tr < 0 || n_tc < 0) return TQ_ERR_ARG;
-  if ((int64_t)n_tr * 64 < m || (int64_t)n_tc * 64 < k) return TQ_ERR_ARG;
-  if (x_dtype != TQ_DTYPE_BF16 && x_dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
-  if (out_dtype != TQ_DTYPE_BF16 && out_dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
-  if (tile_layout != TQ_LAYOUT_ROW_MAJOR && tile_layout != TQ_LAYOUT_MFMA) return TQ_ERR_DTYPE;
+  int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
+  if (rc) return rc;
   if (n == 0 || m == 0) return TQ_OK;
   if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_int8 == nullptr || sx == nullptr)
     return TQ_ERR_ARG;
@@ -358,15 +828,66 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
   a.ids16 = fp16_tile_ids; a.rp16 = fp16_row_ptr;
   a.out = static_cast<uint16_t*>(out); a.ldo = out_stride_n;
   a.bias = static_cast<const uint16_t*>(bias);
-  a.dump = nullptr;
   a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
   a.xvec = xvec_ok(a);
-  const int tb = pick_tb(n);
-  const int W = pick_waves(n_tr, n_tc, (n + 16 * tb - 1) / (16 * tb), split_k);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = (x_dtype == TQ_DTYPE_BF16) ? launch<Bf16, false>(a, W, s) : launch<Fp16, false>(a, W, s);
+  hipError_t e;
+  if (n <= kDecodeMaxTokens) {
+    SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
+    rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
+    if (rc) return rc;
+    e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, false>(a, p, workspace, s)
+                                   : launch_split<Fp16, false>(a, p, workspace, s);
+  } else {
+    const int tb = pick_tb(n);
+    const int W = pick_waves(n_tr, n_tc, (n + 16 * tb - 1) / (16 * tb), split_k);
+    e = (x_dtype == TQ_DTYPE_BF16) ? launch<Bf16, false>(a, W, s) : launch<Fp16, false>(a, W, s);
+  }
+  return (int)e;
+}
+
+extern "C" int tq_linear_mixed_fused_max_tokens(int k) {
+  const int n_tc = (k + 63) / 64;
+  int n = kFusedMaxTokens;
+  while (n > 0 && fused_lds_bytes(n, n_tc) > kFusedMaxLds) --n;
+  return n;
+}
+
+extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                                     const int8_t* int8_tiles, const float* int8_scales,
+                                     const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                                     const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                                     const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                                     int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                                     int n_tc, int split_k, int tile_layout, float* workspace,
+                                     int64_t workspace_elems, void* stream) {
+  int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
+  if (rc) return rc;
+  if (n > kFusedMaxTokens || fused_lds_bytes(n, n_tc) > kFusedMaxLds) return TQ_ERR_ARG;
+  if (n == 0 || m == 0) return TQ_OK;
+  if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_fp == nullptr || x_fp_stride_n < k)
+    return TQ_ERR_ARG;
+  const bool has16 = fp16_tiles != nullptr && fp16_tile_ids != nullptr && fp16_row_ptr != nullptr;
+  if (!aligned16(int8_tiles) || (has16 && !aligned16(fp16_tiles))) return TQ_ERR_ALIGN;
+  GemmArgs a{};
+  a.w8 = int8_tiles; a.sw8 = int8_scales; a.ids8 = int8_tile_ids; a.rp8 = int8_row_ptr;
+  a.xf = static_cast<const uint16_t*>(x_fp); a.ldx = x_fp_stride_n;
+  a.w16 = has16 ? static_cast<const uint16_t*>(fp16_tiles) : nullptr;
+  a.ids16 = fp16_tile_ids; a.rp16 = fp16_row_ptr;
+  a.out = static_cast<uint16_t*>(out); a.ldo = out_stride_n;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
+  a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
+  a.layout = tile_layout;
+  a.xvec = (k == n_tc * 64 && (x_fp_stride_n % 8) == 0 && aligned16(x_fp)) ? 1 : 0;
+  SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
+  rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, true>(a, p, workspace, s)
+                                            : launch_split<Fp16, true>(a, p, workspace, s);
   return (int)e;
 }
 

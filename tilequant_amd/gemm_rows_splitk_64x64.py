@@ -9,11 +9,56 @@ or ``"mfma"`` (the operand-major order this build's packer writes).
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
 from . import _native as nat
+
+# Largest token count the fused quantize + GEMM launch takes (kFusedMaxTokens);
+# wide inputs allow fewer (fused_max_tokens).
+FUSED_MAX_TOKENS = 16
+
+
+def fused_max_tokens(K: int) -> int:
+    """Largest row count linear_mixed_fused accepts for input width K."""
+    return int(nat.lib().tq_linear_mixed_fused_max_tokens(int(K)))
+
+
+class _SplitKWorkspace:
+    """Per (device, stream) zero-initialised fp32 buffer for the split-K
+    partials and arrival counters (the analogue of the reference's
+    _SplitKWorkspace, gemm_rows_splitk_64x64.py:193-215).  Kernels on one
+    stream run in order and leave the counters at zero, so the buffer is
+    reused without re-initialisation, also across HIP graph replays.  It only
+    grows, and a replaced buffer is kept alive: a captured graph may still
+    hold its address."""
+
+    def __init__(self) -> None:
+        self.buffers: Dict[Tuple[int, int], torch.Tensor] = {}
+        self.retired: List[torch.Tensor] = []
+
+    def get(self, device: torch.device, elems: int) -> Optional[torch.Tensor]:
+        if elems <= 0:
+            return None
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        key = (index, nat.stream_handle(device))
+        buf = self.buffers.get(key)
+        if buf is None or buf.numel() < elems:
+            if buf is not None:
+                self.retired.append(buf)
+            buf = torch.zeros((max(elems, 1 << 16),), device=device, dtype=torch.float32)
+            self.buffers[key] = buf
+        return buf
+
+
+_WORKSPACE = _SplitKWorkspace()
+
+
+def _workspace(device, n, M, n_tr, n_tc, split_k):
+    elems = int(nat.lib().tq_gemm_workspace_elems(int(n), int(M), int(n_tr), int(n_tc), int(split_k or 0)))
+    ws = _WORKSPACE.get(device, elems)
+    return (nat.ptr(ws), ws.numel()) if ws is not None else (None, 0)
 
 
 def _check_tiles(name: str, t: torch.Tensor, dtype) -> None:
@@ -83,6 +128,7 @@ def gemm_mixed_rows_splitk(
             raise ValueError(f"{name} must be a contiguous int32 tensor")
     if n == 0 or M == 0:
         return out
+    ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
     rc = nat.lib().tq_gemm_mixed_rows(
         nat.ptr(x_int8), x_int8.stride(0), nat.ptr(sx),
         nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
@@ -90,9 +136,67 @@ def gemm_mixed_rows_splitk(
         nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
         nat.ptr(fp16_row_ptr) if has16 else None,
         nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
-        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], None, 0,
+        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems,
         nat.stream_handle(x_fp.device))
     nat.check(rc, "tq_gemm_mixed_rows")
+    return out
+
+
+def linear_mixed_fused(
+    *,
+    x_fp: torch.Tensor,
+    int8_tiles: torch.Tensor,
+    int8_scales: torch.Tensor,
+    int8_tile_ids: torch.Tensor,
+    int8_row_ptr: torch.Tensor,
+    fp16_tiles: torch.Tensor,
+    fp16_tile_ids: torch.Tensor,
+    fp16_row_ptr: torch.Tensor,
+    M: int,
+    K: int,
+    n_tr: int,
+    n_tc: int,
+    out_dtype: torch.dtype,
+    bias: Optional[torch.Tensor] = None,
+    split_k: Optional[int] = None,
+    out: Optional[torch.Tensor] = None,
+    tile_layout: str = "row_major",
+) -> torch.Tensor:
+    """Activation quantization + mixed tile GEMM in ONE launch (decode sizes,
+    at most FUSED_MAX_TOKENS rows).  Same result, bit for bit, as
+    ``quantize_activation_tile_absmax`` followed by ``gemm_mixed_rows_splitk``
+    with the same ``split_k``; no reference counterpart (the reference always
+    launches the two kernels, mixed_linear.py:233-239)."""
+    nat.require_device(x_fp, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr, fp16_tiles, fp16_tile_ids,
+                       fp16_row_ptr, bias, out)
+    n = int(x_fp.shape[0])
+    M, K, n_tr, n_tc = int(M), int(K), int(n_tr), int(n_tc)
+    if n > fused_max_tokens(K):
+        raise ValueError(f"linear_mixed_fused takes at most {fused_max_tokens(K)} rows for K={K}, got {n}")
+    if x_fp.dim() != 2 or x_fp.shape[1] < K or x_fp.stride(1) != 1:
+        raise ValueError("x_fp must be an (N, >=K) tensor with unit column stride")
+    if out is None:
+        out = torch.empty((n, M), device=x_fp.device, dtype=out_dtype)
+    elif tuple(out.shape) != (n, M) or out.dtype != out_dtype or out.stride(1) != 1:
+        raise ValueError("out must be an (N, M) tensor of out_dtype with unit column stride")
+    _check_tiles("int8_tiles", int8_tiles, torch.int8)
+    has16 = fp16_tiles.numel() != 0
+    if has16:
+        _check_tiles("fp16_tiles", fp16_tiles, x_fp.dtype)
+    if bias is not None and (bias.dtype != out_dtype or not bias.is_contiguous() or bias.numel() < M):
+        raise ValueError("bias must be a contiguous tensor of out_dtype with M entries")
+    if n == 0 or M == 0:
+        return out
+    ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
+    rc = nat.lib().tq_linear_mixed_fused(
+        nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
+        nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
+        nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
+        nat.ptr(fp16_row_ptr) if has16 else None,
+        nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
+        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems,
+        nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_linear_mixed_fused")
     return out
 
 

@@ -12,6 +12,12 @@ projection groups and sibling-activation cache as the reference
 * Q/K/V and Gate/Up siblings can be stacked into one ``MixedLinearGroup``
   (one quantization + one GEMM per group), each member served a column slice.
 
+With ``cfg.fused_decode = True``, decode-sized inputs (at most 16 rows,
+fewer for very wide inputs) run quantization and GEMM as one launch
+(``linear_mixed_fused``), bit-identical to the two-launch path.  It is off
+by default: every GEMM workgroup then re-quantizes all column tiles of the
+activation, which on MI355X costs more than the separate quantize launch.
+
 The extra state records the packed tiles' storage order (``tile_layout``) so a
 ``state_dict`` round trip keeps it.
 """
@@ -24,7 +30,7 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 import torch.nn as nn
 
-from .gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+from .gemm_rows_splitk_64x64 import fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused
 from .pack import Pack, concat_packs_along_rows
 from .quant_utils import (
     activation_tile_absmax_scales,
@@ -160,6 +166,22 @@ class MixedLinear(nn.Module):
             out_dtype=out_dtype, bias=self._out_bias(out_dtype), out=out, tile_layout=self.tile_layout,
         )
 
+    def _fused_limit(self) -> int:
+        limit = getattr(self, "_fused_rows", None)
+        if limit is None:
+            limit = self._fused_rows = fused_max_tokens(self.K_orig)
+        return limit
+
+    def _fused_decode(self, x_fp: torch.Tensor) -> torch.Tensor:
+        out_dtype = self._out_dtype()
+        return linear_mixed_fused(
+            x_fp=x_fp, int8_tiles=self.int8_tiles, int8_scales=self.int8_scales,
+            int8_tile_ids=self.int8_tile_ids, int8_row_ptr=self.int8_row_ptr, fp16_tiles=self.fp16_tiles,
+            fp16_tile_ids=self.fp16_tile_ids, fp16_row_ptr=self.fp16_row_ptr, M=self.M_orig, K=self.K_orig,
+            n_tr=self.n_tr, n_tc=self.n_tc, out_dtype=out_dtype, bias=self._out_bias(out_dtype),
+            tile_layout=self.tile_layout,
+        )
+
     def _forward_chunk(self, x_chunk: torch.Tensor, sx: torch.Tensor, out: torch.Tensor) -> None:
         x_int8 = quantize_activation_tile_with_scales(x_chunk, sx=sx, tile_n=self.tile_n)
         self._gemm_bias(x_fp=x_chunk, x_int8=x_int8, sx=sx, out=out)
@@ -177,7 +199,9 @@ class MixedLinear(nn.Module):
             raise ValueError(f"Input K mismatch: got {k_in}, expected {self.K_orig}")
         x_work = x2d.contiguous()
         chunk = self._activation_row_chunk_size()
-        if n_rows <= chunk:
+        if 0 < n_rows <= min(self._fused_limit(), chunk) and bool(_cfg_get(self.cfg, "fused_decode", False)):
+            y = self._fused_decode(x_work)
+        elif n_rows <= chunk:
             x_int8, sx = _quantize_shared_activation(source=x, x_work=x_work, tile_n=self.tile_n,
                                                      consumer_id=id(self))
             y = self._gemm_bias(x_fp=x_work, x_int8=x_int8, sx=sx)
