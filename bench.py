@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU work timed for the baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense bf16 context measurement")
+    ap.add_argument("--prefill-tokens", type=int, default=8192, help="prefill measurement rows (0 = skip)")
+    ap.add_argument("--prefill-keep", type=float, default=0.05)
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
 
@@ -115,6 +117,47 @@ def make_inputs(args, device):
         x[:, ch] *= 20
         xs[name] = x.to(torch.bfloat16).to(device)
     return xs
+
+
+INT8_PEAK_TOPS = 5030.0   # dense INT8 MFMA, 256 CU x 2.4 GHz x 8192 ops/clk
+
+
+def prefill_measure(args, device):
+    """one Llama-3.2-3B layer's QKV/O/GateUp/Down at
+    prefill_tokens rows (MixedLinear: whole-input scales, 4096-row chunks),
+    keep05 uniform masks.  Compute-bound: reported against INT8 MFMA peak."""
+    import numpy as np
+    import torch
+
+    a2 = argparse.Namespace(**vars(args))
+    a2.layers, a2.keep, a2.tokens = 1, args.prefill_keep, args.prefill_tokens
+    layers, info = build_layers(a2, device)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(args.seed + 7)
+    xs = {name: torch.randn((args.prefill_tokens, k), generator=g).to(torch.bfloat16).to(device)
+          for name, _, k in GROUPS}
+    mods = layers[0]
+    for name, _, _ in GROUPS:
+        mods[name](xs[name])
+    torch.cuda.synchronize()
+    per = {}
+    for name, _, _ in GROUPS:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(5):
+            e0.record()
+            mods[name](xs[name])
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        per[name] = statistics.median(times)
+    total_ms = sum(per.values())
+    return {"tokens": args.prefill_tokens, "keep": args.prefill_keep, "layer_ms": total_ms,
+            "tops": info["ops"] / (total_ms / 1e3) / 1e12,
+            "frac_int8_peak": info["ops"] / (total_ms / 1e3) / 1e12 / INT8_PEAK_TOPS,
+            "group_ms": per, "ops_per_layer": info["ops"], "bf16_tiles": info["t16"],
+            "note": "MixedLinear forward per group (scales over all rows, 2 x 4096-row chunks of quantize + "
+                    "GEMM), HIP events, median of 5"}
 
 
 def cpu_baseline(args, layers, xs):
@@ -304,6 +347,8 @@ def main():
         del ws
 
     cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
+    del layers
+    prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
 
     result = {
         "metric": "mixed tile GEMM TOPS + % roofline (M=4 decode, M=8192 prefill); TPOT",
@@ -336,6 +381,7 @@ def main():
                      "timing": "HIP events around each of the step's 112 GEMM launches, enqueued behind a "
                                "spin kernel so they run back to back on the launch stream"},
         "dense_bf16": dense,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

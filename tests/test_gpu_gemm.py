@@ -323,3 +323,22 @@ def test_fused_quantization_handles_exact_ties():
     xq, sx = quantize_activation_tile_absmax(xt)
     assert torch.equal(xq.cpu(), torch.from_numpy(nm.act_quant(x)[0]))
     assert torch.equal(_fused(pack, xt), _gemm(pack, xt, xq, sx))
+
+
+@pytest.mark.parametrize("n,m,k,frac", [(512, 3072, 3072, 0.05), (300, 1024, 8192, 0.05), (4096, 256, 3072, 0.2)])
+def test_prefill_kernel_shapes(n, m, k, frac):
+    """BASELINE configs[2]-style prefill (N > 64: LDS-staged MFMA kernel) vs the oracle."""
+    W, pack, ids16 = _case(m, k, frac, seed=n + m)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=n - m)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    y = _gemm(pack, xd, xq, sx)
+    rows = np.unique(np.r_[0:5, n // 2:n // 2 + 5, n - 5:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc)
+    assert torch.equal(_gemm(pack, xd, xq, sx), y)
+    rm = relayout_pack(pack, "row_major")
+    assert torch.equal(_gemm(rm, xd, xq, sx), y)
