@@ -342,3 +342,33 @@ def test_prefill_kernel_shapes(n, m, k, frac):
     assert torch.equal(_gemm(pack, xd, xq, sx), y)
     rm = relayout_pack(pack, "row_major")
     assert torch.equal(_gemm(rm, xd, xq, sx), y)
+
+
+@pytest.mark.parametrize("n,m,k,frac", [(300, 512, 3072, 0.05), (257, 256, 1024, 0.0)])
+def test_prefill_dma_and_register_paths_agree_bitwise(n, m, k, frac):
+    """Aligned activation rows take the DMA-pipelined prefill kernel; a row
+    stride that is not a multiple of 16 bytes takes the register-staged one.
+    Both apply the same fp32 operations in the same tile order."""
+    W, pack, _ = _case(m, k, frac, seed=n + 7)
+    x = make_x(n, k, seed=n + 8)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_odd = torch.zeros((n, k + 8), dtype=torch.int8, device="cuda")[:, :k]
+    xq_odd.copy_(xq)
+    xf_odd = torch.zeros((n, k + 4), dtype=xd.dtype, device="cuda")[:, :k]
+    xf_odd.copy_(xd)
+    assert torch.equal(_gemm(pack, xd, xq, sx), _gemm(pack, xf_odd, xq_odd, sx))
+
+
+def test_prefill_rows_longer_than_one_metadata_chunk():
+    # 1100 tiles per row tile: the DMA kernel stages tile metadata in chunks of 512
+    n, m, k = 80, 128, 64 * 1100
+    W, pack, ids16 = _case(m, k, 0.01, seed=901)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=902)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    assert_gemm_close(y, acc, sab, pack.n_tc)

@@ -781,6 +781,200 @@ gemm_prefill_kernel(GemmArgs a) {
       }
 }
 
+// ---- prefill kernel, asynchronous LDS pipeline ------------------------------
+//
+// Same workgroup decomposition and arithmetic as gemm_prefill_kernel, with
+// the K-step operands moved by global_load_lds_dwordx4 (gfx950: each lane's
+// 16 bytes land at LDS base + lane*16, no VGPRs) through a P-stage ring of
+// 20 KiB stages.  Per stage each wave issues five DMA loads: its 1 KiB j-block
+// of the weight tile and 4 KiB (four 16-token blocks) of the activation
+// slice, with per-lane source addresses chosen so the data lands in MFMA
+// operand order.  Loop step p: wait for stage p (the P-2 younger stages stay
+// in flight: vmcnt = 5*(P-2)), one barrier, issue tile p+P-1 into the stage
+// consumed at step p-1, then 16 MFMA + the fp32 epilogue on stage p.  Tail
+// steps re-issue the last tile so the vmcnt arithmetic stays constant.  Rows
+// past n read a clamped valid row: they only feed output rows >= n, which are
+// never stored.  Needs 16-byte aligned activation rows and k == 64 * n_tc.
+
+constexpr int kPfStage = 4096 + kPfXBytes;
+constexpr int kPfStages = 3;
+constexpr int kPfMeta = 512;
+
+// LDS byte address of a __shared__ object
+__device__ inline uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+__device__ inline int lds_read_i32(uint32_t addr) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+template <int V>
+__device__ inline void wait_vmcnt() {
+  // s_waitcnt with vmcnt = V (gfx9 split field) and expcnt / lgkmcnt at their maxima
+  __builtin_amdgcn_s_waitcnt((V & 0xF) | ((V >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <class XT, int P>
+__global__ void __launch_bounds__(kPfThreads)
+gemm_prefill_async_kernel(GemmArgs a) {
+  __shared__ __align__(16) int8_t smem[P * kPfStage];
+  __shared__ int meta_x[kPfMeta];
+  __shared__ float meta_s[kPfMeta];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = blockIdx.x;
+  const int n0 = blockIdx.y * kPfTokens;
+  const int rbase = r * a.n_tc;
+  const int arow = lane & 15, akq = lane >> 4;
+
+  v4f acc[4][4];   // [token block][j-block]
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int lo8 = a.rp8[r], hi8 = a.rp8[r + 1];
+  // this lane's weight chunk offset inside a tile: j-block `wave`, lane slot `lane`
+  const int w_off = (a.layout == TQ_LAYOUT_MFMA) ? wave * 1024 + lane * 16
+                                                 : (wave * 16 + (lane & 15)) * 64 + (lane >> 4) * 16;
+  // this lane's activation rows for token blocks wave*4 + i
+  int64_t x_row[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    x_row[i] = (int64_t)min(n0 + (wave * 4 + i) * 16 + arow, a.n - 1) * a.ldq + akq * 16;
+
+  auto issue = [&](int p, int xoff, int stage) {
+    int8_t* st = smem + stage * kPfStage;
+    __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)p * 4096 + w_off, st + wave * 1024, 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(a.xq + x_row[i] + xoff, st + 4096 + (wave * 4 + i) * 1024, 16, 0, 0);
+  };
+
+  // LDS reads inside the pipeline are inline asm: the compiler cannot tell
+  // which LDS bytes an in-flight DMA load writes, so it would put a full
+  // vmcnt(0) before every ordinary LDS read and drain the pipeline.  The
+  // explicit vmcnt wait + barrier at the top of each step orders them instead.
+  const uint32_t smem_lds = lds_addr(smem);
+  const uint32_t mx_lds = lds_addr(meta_x), ms_lds = lds_addr(meta_s);
+  const uint32_t w_rd = smem_lds + lane * 16;
+  const uint32_t x_rd = smem_lds + 4096 + wave * 4096 + lane * 16;
+
+  // Tile metadata (activation byte offset, combined scale) is staged through
+  // LDS per chunk of kPfMeta tiles: loading it from global inside the loop
+  // would share the in-order vmcnt with the DMA loads and drain the pipeline.
+  for (int base = lo8; base < hi8; base += kPfMeta) {
+    const int end = min(base + kPfMeta, hi8);
+    __syncthreads();   // the previous chunk's readers are done with meta and stages
+    for (int t = base + (int)threadIdx.x; t < end; t += kPfThreads) {
+      const int c = col_of(a.ids8[t], rbase, a.n_tc);
+      meta_x[t - base] = c * 64;
+      meta_s[t - base] = a.sx[c] * a.sw8[t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < P - 1; ++s) {
+      const int p = min(base + s, end - 1);
+      issue(p, __builtin_amdgcn_readfirstlane(lds_read_i32(mx_lds + 4 * (p - base))), s);
+    }
+    for (int p = base; p < end; ++p) {
+      const int stage = (p - base) % P;
+      wait_vmcnt<5 * (P - 2)>();
+      // s_barrier without __syncthreads' release fence: that fence waits for
+      // every outstanding load (vmcnt(0)), in-flight DMA included.  The DMA
+      // writes are ordered by the vmcnt wait above; the asm LDS reads below
+      // complete (lgkmcnt(0)) before their step ends.
+      asm volatile("s_barrier" ::: "memory");
+      const int pn = min(p + P - 1, end - 1);
+      int xo;
+      float sc;
+      asm volatile(
+          "ds_read_b32 %0, %2\n\t"
+          "ds_read_b32 %1, %3\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(xo), "=&v"(sc)
+          : "v"(mx_lds + 4 * (pn - base)), "v"(ms_lds + 4 * (p - base))
+          : "memory");
+      issue(pn, __builtin_amdgcn_readfirstlane(xo), (stage + P - 1) % P);
+      v4i bw[4], ax[4];
+      const uint32_t so = stage * kPfStage;
+      asm volatile(
+          "ds_read_b128 %0, %8\n\t"
+          "ds_read_b128 %1, %8 offset:1024\n\t"
+          "ds_read_b128 %2, %8 offset:2048\n\t"
+          "ds_read_b128 %3, %8 offset:3072\n\t"
+          "ds_read_b128 %4, %9\n\t"
+          "ds_read_b128 %5, %9 offset:1024\n\t"
+          "ds_read_b128 %6, %9 offset:2048\n\t"
+          "ds_read_b128 %7, %9 offset:3072\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+            "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
+          : "v"(w_rd + so), "v"(x_rd + so)
+          : "memory");
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], sc, acc[tb][jb][v]);
+        }
+    }
+    wait_vmcnt<0>();   // drain the re-issued tail loads before the stages are reused
+  }
+
+  // ---- 16-bit tiles (straight from global; rare by construction)
+  if (a.w16 != nullptr) {
+    const int lo16 = a.rp16[r], hi16 = a.rp16[r + 1];
+    for (int q = lo16; q < hi16; ++q) {
+      const int c = col_of(a.ids16[q], rbase, a.n_tc);
+      v4i bw[4][2];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        bw[jb][0] = load_w16(a, q, jb, 0, lane);
+        bw[jb][1] = load_w16(a, q, jb, 1, lane);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int row = n0 + wave * 64 + tb * 16 + arow;
+        const v4i a0 = load_xf<1>(a, row, c * 64 + akq * 8);
+        const v4i a1 = load_xf<1>(a, row, c * 64 + 32 + akq * 8);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          acc[tb][jb] = mfma16<XT>(a0, bw[jb][0], acc[tb][jb]);
+          acc[tb][jb] = mfma16<XT>(a1, bw[jb][1], acc[tb][jb]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = n0 + wave * 64 + tb * 16 + 4 * akq + v;
+        const int col = r * 64 + jb * 16 + arow;
+        if (row < a.n && col < a.m) {
+          const float sum = acc[tb][jb][v];
+          uint16_t y;
+          if (a.out_bf16) {
+            y = Bf16::from_f32(sum);
+            if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+          } else {
+            y = Fp16::from_f32(sum);
+            if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+          }
+          a.out[(int64_t)row * a.ldo + col] = y;
+        }
+      }
+}
+
 // ---- host side -----------------------------------------------------------
 
 static int pick_tb(int n) { return n <= 16 ? 1 : (n <= 32 ? 2 : 4); }
@@ -963,8 +1157,13 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                    : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
-    if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_kernel<Bf16>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(gemm_prefill_kernel<Fp16>, grid, block, 0, s, a);
+    if (a.xvec) {   // DMA path: whole 16-byte activation chunks, aligned rows
+      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL((gemm_prefill_async_kernel<Bf16, kPfStages>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((gemm_prefill_async_kernel<Fp16, kPfStages>), grid, block, 0, s, a);
+    } else {
+      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_kernel<Bf16>, grid, block, 0, s, a);
+      else hipLaunchKernelGGL(gemm_prefill_kernel<Fp16>, grid, block, 0, s, a);
+    }
     e = hipGetLastError();
   }
   return (int)e;
