@@ -107,8 +107,8 @@ def test_config1_packer_products_and_output():
     assert torch.equal(back.int8_tiles, pack.int8_tiles) and torch.equal(back.fp16_tiles, pack.fp16_tiles)
 
 
-@pytest.mark.parametrize("m,k", [(1024, 3072), (8192, 3072), (3072, 8192), (5120, 3072)])
-@pytest.mark.parametrize("n", [1, 4, 16, 64])
+@pytest.mark.parametrize("m,k", [(1024, 3072), (8192, 3072), (3072, 8192), (5120, 3072), (16384, 3072)])
+@pytest.mark.parametrize("n", [1, 4, 16, 24, 64])
 def test_llama_decode_shapes(m, k, n):
     """BASELINE configs[1] shapes (k/v, gate/up, down, fused QKV) at decode token counts."""
     W, pack, ids16 = _case(m, k, 0.01, seed=m + k + n)
@@ -242,6 +242,21 @@ def test_fused_equals_two_launch_path_bitwise(n):
         y2 = _gemm(pack, xd, xq, sx, split_k=split_k)
         y1 = _fused(pack, xd, split_k=split_k)
         assert torch.equal(y1, y2), f"split_k={split_k}"
+    op = oracle_pack(W, ids16)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y1, acc, sab, 48)
+
+
+@pytest.mark.parametrize("n", [1, 4, 8, 16])
+def test_fused_equals_two_launch_path_on_whole_tile_schedule(n):
+    """Stacked gate/up width (256 row tiles): whole-tile workgroups."""
+    W, pack, ids16 = _case(16384, 3072, 0.01, seed=950 + n)
+    x = make_x(n, 3072, seed=951 + n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y2 = _gemm(pack, xd, xq, sx)
+    y1 = _fused(pack, xd)
+    assert torch.equal(y1, y2)
     op = oracle_pack(W, ids16)
     acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
     assert_gemm_close(y1, acc, sab, 48)

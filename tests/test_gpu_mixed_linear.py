@@ -153,10 +153,13 @@ def test_iaa_packing_matches_torch_restatement():
 
 
 def test_fused_decode_option_is_bitwise_identical():
-    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16", fused_decode=False)
     lin, W, ids16, _ = _linear(1024, 3072, 0.01, 80, cfg, bias=True)
-    fused_cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16", fused_decode=True)
-    lin_f = MixedLinear(lin.to_pack(), lin.bias.detach(), fused_cfg)
-    for n in (1, 4, 16):
+    lin_f = MixedLinear(lin.to_pack(), lin.bias.detach(), SimpleNamespace(quant_style="gi", dtype_out="bf16",
+                                                                           fused_decode=True))
+    lin_a = MixedLinear(lin.to_pack(), lin.bias.detach(), SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    for n in (1, 2, 3, 4, 16):
         x = make_x(n, 3072, seed=81 + n).cuda()
-        assert torch.equal(lin_f(x), lin(x))
+        y = lin(x)
+        assert torch.equal(lin_f(x), y)
+        assert torch.equal(lin_a(x), y)   # "auto": fused up to FUSED_AUTO_MAX_ROWS rows

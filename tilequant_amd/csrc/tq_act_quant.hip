@@ -41,34 +41,6 @@ __device__ inline u32x4 load8(const XView& v, int row, int col) {
   return *reinterpret_cast<const u32x4*>(v.x + (int64_t)row * v.sn + col);
 }
 
-template <class T>
-__device__ inline float max8(u32x4 w, float m) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] & 0xffffu))));
-    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] >> 16))));
-  }
-  return m;
-}
-
-template <class T>
-__device__ inline u32x2 codes8(u32x4 w, const CodeScale& s) {
-  u32x2 out;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t word = w[h * 2 + i];
-      uint32_t lo = (uint32_t)(s.code(T::to_f32((uint16_t)(word & 0xffffu))) & 0xff);
-      uint32_t hi = (uint32_t)(s.code(T::to_f32((uint16_t)(word >> 16))) & 0xff);
-      packed |= (lo | (hi << 8)) << (16 * i);
-    }
-    out[h] = packed;
-  }
-  return out;
-}
-
 // Vector path is legal for tile c when rows are 16-byte aligned, the column
 // stride is 1 and the tile lies fully inside k.
 __device__ inline bool tile_vec_ok(const XView& v, int c) {

@@ -84,15 +84,56 @@ struct CodeScale {
   bool exact_div;
   __device__ explicit CodeScale(float scale)
       : s(scale), rcp(1.0f / scale), exact_div(!(scale >= 1.1754943508222875e-38f)) {}
-  __device__ inline int code(float v) const {
-    if (exact_div) return quant_code(v, s);
+  // with rcp == 1.0f / scale computed elsewhere (IEEE divide)
+  __device__ CodeScale(float scale, float recip)
+      : s(scale), rcp(recip), exact_div(!(scale >= 1.1754943508222875e-38f)) {}
+  // Normal scales only (!exact_div).  q is never NaN here, so the clamp is
+  // a single v_med3_f32.
+  __device__ inline int code_fast(float v) const {
     const float t = v * rcp;
     const float h = __builtin_floorf(t) + 0.5f;
-    float q = (__builtin_fmaf(-h, s, v) == 0.0f) ? __builtin_rintf(h) : __builtin_rintf(t);
-    q = fmaxf(fminf(q, 127.0f), -127.0f);
-    return (int)q;
+    const float q = (__builtin_fmaf(-h, s, v) == 0.0f) ? __builtin_rintf(h) : __builtin_rintf(t);
+    return (int)__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
   }
+  __device__ inline int code(float v) const { return exact_div ? quant_code(v, s) : code_fast(v); }
 };
+
+// 8 consecutive 16-bit values packed in a 16-byte word: absmax and codes.
+template <class T>
+__device__ inline float max8(u32x4 w, float m) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] & 0xffffu))));
+    m = fmaxf(m, fabsf(T::to_f32((uint16_t)(w[i] >> 16))));
+  }
+  return m;
+}
+
+template <class T, bool EXACT>
+__device__ inline u32x2 codes8_impl(u32x4 w, const CodeScale& s) {
+  u32x2 out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t word = w[h * 2 + i];
+      const float a = T::to_f32((uint16_t)(word & 0xffffu)), b = T::to_f32((uint16_t)(word >> 16));
+      const uint32_t lo = (uint32_t)((EXACT ? quant_code(a, s.s) : s.code_fast(a)) & 0xff);
+      const uint32_t hi = (uint32_t)((EXACT ? quant_code(b, s.s) : s.code_fast(b)) & 0xff);
+      packed |= (lo | (hi << 8)) << (16 * i);
+    }
+    out[h] = packed;
+  }
+  return out;
+}
+
+// One branch per 8 values (the scale is shared): the IEEE-divide path only for
+// subnormal scales.
+template <class T>
+__device__ inline u32x2 codes8(u32x4 w, const CodeScale& s) {
+  return s.exact_div ? codes8_impl<T, true>(w, s) : codes8_impl<T, false>(w, s);
+}
 
 // ---- wave reductions ----------------------------------------------------
 
@@ -129,6 +170,17 @@ __device__ inline float block_max(float v, float* red, int nwaves) {
 }
 
 __host__ __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Workgroup barrier for LDS hand-offs that leaves outstanding global loads in
+// flight: waits only for this wave's LDS operations (lgkmcnt(0); vmcnt and
+// expcnt at their maxima in the gfx9 s_waitcnt encoding), then s_barrier.
+// __syncthreads() would also wait for every outstanding global load
+// (vmcnt(0)), serialising prefetched weight streams behind the barrier.  The
+// "memory" clobber keeps the compiler from moving memory operations across.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+}
 
 }  // namespace tq
 

@@ -635,6 +635,275 @@ gemm_splitk_kernel(GemmArgs a) {
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- decode kernel with the activation staged in LDS ------------------------
+//
+// Same unit decomposition as gemm_splitk_kernel with one split: workgroup =
+// (row tile r, group of JBW j-blocks), W waves taking the row's tiles
+// round-robin.  A decode GEMM lasts a few microseconds, so its duration is set
+// by the number of DEPENDENT memory round trips, not by arithmetic.  This
+// kernel has two: the row's tile range (row_ptr), then everything else.
+//   1. At entry every thread issues its share of the activation -- int8 codes
+//      and sx, or (QUANT) the raw 16-bit values -- which depends on nothing.
+//   2. Each wave issues all of its tiles (up to UMAX per batch; one 16-byte
+//      load per lane per j-block) with their ids and scales.
+//   3. While the weights stream, the activation goes to LDS.  QUANT computes
+//      the codes there first, by the closed form of tq_act_quant: an LDS
+//      atomic max per column tile over all n rows, the scale rounded to the
+//      input dtype, IEEE-exact codes -- bit for bit the separate kernel's.
+//      The hand-offs use lds_barrier(), which leaves the weight loads in
+//      flight.
+//   4. MFMAs read their A operand from LDS at the tile's column: no global
+//      load waits for a tile id.
+// Codes live in LDS as [n][k + 16] (16-byte row padding spreads the rows of one
+// A-operand read over different banks); the reduction buffer reuses the area
+// afterwards.  Needs k == 64 * n_tc, 16-byte aligned activation rows, S == 1.
+
+constexpr int kDecCodesMax = 96 * 1024;   // LDS bytes for staged codes
+
+// Raw buffer resource over `bytes` bytes at p (stride 0): loads at offsets >=
+// bytes return 0 and touch no memory.  Word 3 = 0x00020000 is the gfx9-family
+// descriptor format (32-bit data format, no swizzle).
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+// Byte offset of this lane's 16-byte B-operand chunk of j-block jb, k-half h
+// inside a 16-bit tile (the element offsets of load_w16, times two).
+__device__ inline int w16_lane_offset(int layout, int jb, int h, int lane) {
+  return layout == TQ_LAYOUT_MFMA ? (jb * 2 + h) * 1024 + lane * 16
+                                  : jb * 2048 + (lane & 15) * 128 + h * 64 + (lane >> 4) * 16;
+}
+
+// Byte offset of this lane's 16-byte B-operand chunk of j-block 0 inside an
+// INT8 tile (add jb * 1024 in the MFMA layout; the row-major layout places
+// j-block jb at rows 16 jb .. 16 jb + 15, i.e. also + jb * 1024).
+__device__ inline int w8_lane_offset(int layout, int lane) {
+  return layout == TQ_LAYOUT_MFMA ? lane * 16 : (lane & 15) * 64 + (lane >> 4) * 16;
+}
+
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
+__global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
+gemm_decode_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) int8_t dsm[];
+  constexpr int NJG = 4 / JBW;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = blockDim.x, W = T >> 6;
+  const int unit = blockIdx.x;
+  const int r = unit / NJG, jb0 = (unit - (unit / NJG) * NJG) * JBW;
+  const int arow = lane & 15, akq = lane >> 4;
+  const int rbase = r * a.n_tc;
+  const int n_tc = a.n_tc;
+  const int ldc = a.k + 16;
+  int8_t* codes = dsm;                                                  // [n][ldc]
+  float* sxl = reinterpret_cast<float*>(dsm + a.n * ldc);               // [n_tc] scales
+  float* rcpl = sxl + n_tc;                                             // QUANT: [n_tc] 1 / scale
+  uint32_t* amax = reinterpret_cast<uint32_t*>(rcpl + n_tc);            // QUANT: [n_tc] absmax bits
+
+  // ---- 1. activation share (16-byte chunks; duplicates past the end rewrite
+  //         the last chunk with identical data, so the phase is branch-free)
+  const int cpr = QUANT ? (a.k >> 3) : (a.k >> 4);   // chunks per row
+  const int total = a.n * cpr;
+  u32x4 xr[CMAX];
+#pragma unroll
+  for (int j = 0; j < CMAX; ++j) {
+    const int i = min((int)threadIdx.x + j * T, total - 1);
+    const int row = i / cpr, ch = i - row * cpr;
+    if constexpr (QUANT) xr[j] = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
+    else xr[j] = *reinterpret_cast<const u32x4*>(a.xq + (int64_t)row * a.ldq + ch * 16);
+  }
+  float sxr[2] = {0.0f, 0.0f};
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sxr[h] = a.sx[min((int)threadIdx.x + h * T, n_tc - 1)];
+  }
+
+  // ---- 2. this wave's first batch of INT8 tiles, issued unconditionally:
+  //         buffer loads bounded to the row's own tiles return 0 past its end
+  //         instead of faulting, so no branch guards them and the waits below
+  //         count exactly the loads issued before the weights.  Lane u < UMAX
+  //         fetches the id and scale of batch tile u with a VECTOR load (read
+  //         back with v_readlane): scalar loads would share lgkmcnt with the
+  //         LDS traffic, so every lds_barrier() below would wait for them.
+  const int lo8 = a.rp8[r], hi8 = a.rp8[r + 1];
+  const int n8 = hi8 - lo8;
+  const __amdgpu_buffer_rsrc_t wrs = row_rsrc(a.w8 + (int64_t)lo8 * 4096, n8 * 4096);
+  const __amdgpu_buffer_rsrc_t irs = row_rsrc(a.ids8 + lo8, n8 * 4);
+  const __amdgpu_buffer_rsrc_t srs = row_rsrc(a.sw8 + lo8, n8 * 4);
+  const int woff = w8_lane_offset(a.layout, lane);
+  int idl;
+  float swl;
+  v4i bw[UMAX][JBW];
+  auto load_batch = [&](int q0) {   // q0: position relative to lo8
+    const int ql = (q0 + min(lane, UMAX - 1) * W) * 4;
+    idl = __builtin_amdgcn_raw_buffer_load_b32(irs, ql, 0, 0);
+    swl = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, ql, 0, 0));
+#pragma unroll
+    for (int u = 0; u < UMAX; ++u)
+#pragma unroll
+      for (int j = 0; j < JBW; ++j)
+        bw[u][j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                               wrs, (q0 + u * W) * 4096 + woff + (jb0 + j) * 1024, 0, 0));
+  };
+  const int first_q = wave;
+  load_batch(first_q);
+
+  // The first U16 16-bit tiles of this wave (their rotation continues after
+  // the INT8 tiles), prefetched the same way.  Without 16-bit tiles the
+  // ranges are empty and these loads touch no memory.
+  constexpr int U16 = JBW == 1 ? 2 : 1;
+  const bool has16 = a.w16 != nullptr;
+  const int32_t* rp16p = has16 ? a.rp16 : a.rp8;
+  const int lo16 = rp16p[r];
+  const int n16 = has16 ? rp16p[r + 1] - lo16 : 0;
+  const __amdgpu_buffer_rsrc_t w16rs =
+      row_rsrc(has16 ? (const void*)(a.w16 + (int64_t)lo16 * 4096) : (const void*)a.rp8, n16 * 8192);
+  const __amdgpu_buffer_rsrc_t i16rs = row_rsrc(has16 ? (const void*)(a.ids16 + lo16) : (const void*)a.rp8, n16 * 4);
+  const int first16 = (wave - (n8 % W) + W) % W;
+  const int id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + min(lane, U16 - 1) * W) * 4, 0, 0);
+  v4i b16p[U16][JBW][2];
+  auto load_w16_at = [&](v4i (&dst)[JBW][2], int q) {
+#pragma unroll
+    for (int j = 0; j < JBW; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        dst[j][h] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                w16rs, q * 8192 + w16_lane_offset(a.layout, jb0 + j, h, lane), 0, 0));
+  };
+#pragma unroll
+  for (int u = 0; u < U16; ++u) load_w16_at(b16p[u], first16 + u * W);
+
+  // ---- 3. activation -> LDS
+  if constexpr (QUANT) {
+    for (int c = threadIdx.x; c < n_tc; c += T) amax[c] = 0u;
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < CMAX; ++j) {
+      const int i = min((int)threadIdx.x + j * T, total - 1);
+      const int c = (i - (i / cpr) * cpr) >> 3;   // 8 chunks of 8 values per column tile
+      // The 8 chunks of one (row, column tile) sit in 8 aligned consecutive
+      // lanes (cpr and T are multiples of 8; clamped tail chunks form whole
+      // groups): reduce them with DPP, then one LDS atomic per group.
+      // Absolute values are non-negative, so their bit patterns order like the floats.
+      uint32_t m = __float_as_uint(max8<XT>(xr[j], 0.0f));
+      m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+      m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+      m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));  // row_half_mirror
+      if ((lane & 7) == 0) __hip_atomic_fetch_max(amax + c, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    lds_barrier();
+    for (int c = threadIdx.x; c < n_tc; c += T) {
+      const float s = act_scale_from_absmax<XT>(__uint_as_float(amax[c]));
+      sxl[c] = s;
+      rcpl[c] = 1.0f / s;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < CMAX; ++j) {
+      const int i = min((int)threadIdx.x + j * T, total - 1);
+      const int row = i / cpr, ch = i - row * cpr;
+      const int c = ch >> 3;
+      const CodeScale cq(sxl[c], rcpl[c]);
+      *reinterpret_cast<u32x2*>(codes + row * ldc + ch * 8) = codes8<XT>(xr[j], cq);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < CMAX; ++j) {
+      const int i = min((int)threadIdx.x + j * T, total - 1);
+      const int row = i / cpr, ch = i - row * cpr;
+      *reinterpret_cast<u32x4*>(codes + row * ldc + ch * 16) = xr[j];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if ((int)threadIdx.x + h * T < n_tc) sxl[threadIdx.x + h * T] = sxr[h];
+  }
+  lds_barrier();
+
+  v4f acc[JBW][TB];
+#pragma unroll
+  for (int j = 0; j < JBW; ++j)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[j][tb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // ---- 4. INT8 tiles: A operand from LDS
+  for (int q0 = first_q; q0 < n8; q0 += UMAX * W) {
+    if (q0 != first_q) load_batch(q0);
+    const int nu = min(UMAX, (n8 - q0 + W - 1) / W);   // valid tiles in this batch (wave-uniform)
+#pragma unroll
+    for (int u = 0; u < UMAX; ++u)
+      if (u < nu) {
+        const int c = col_of(__builtin_amdgcn_readlane(idl, u), rbase, n_tc);
+        const float sc = sxl[c] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), u));
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          const int row = tb * 16 + arow;   // rows >= n: zero operand (clamped read stays in the buffer)
+          const v4i xv = *reinterpret_cast<const v4i*>(codes + min(row, a.n - 1) * ldc + c * 64 + akq * 16);
+          const v4i ax = row < a.n ? xv : v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int j = 0; j < JBW; ++j) {
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
+          }
+        }
+      }
+  }
+
+  // ---- 16-bit tiles (positions first16 + i*W, ascending); A from global
+  auto tile16 = [&](const v4i (&b16)[JBW][2], int id) {
+    const int c = col_of(id, rbase, n_tc);
+    v4i ax[TB][2];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) ax[tb][h] = load_xf<1>(a, tb * 16 + arow, c * 64 + h * 32 + akq * 8);
+#pragma unroll
+    for (int j = 0; j < JBW; ++j)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        acc[j][tb] = mfma16<XT>(ax[tb][0], b16[j][0], acc[j][tb]);
+        acc[j][tb] = mfma16<XT>(ax[tb][1], b16[j][1], acc[j][tb]);
+      }
+  };
+#pragma unroll
+  for (int u = 0; u < U16; ++u)
+    if (first16 + u * W < n16) tile16(b16p[u], __builtin_amdgcn_readlane(id16l, u));
+  for (int q = first16 + U16 * W; q < n16; q += W) {
+    v4i b16[JBW][2];
+    load_w16_at(b16, q);
+    tile16(b16, __builtin_amdgcn_raw_buffer_load_b32(i16rs, q * 4, 0, 0));
+  }
+
+  // ---- waves -> LDS (reusing the code area) -> sum in wave order -> store
+  constexpr int E = JBW * TB * 4 * 64;   // (j, tb, v, lane)
+  float* red = reinterpret_cast<float*>(dsm);
+  lds_barrier();   // every wave is done reading codes and scales
+#pragma unroll
+  for (int j = 0; j < JBW; ++j)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave * E + ((j * TB + tb) * 4 + v) * 64 + lane] = acc[j][tb][v];
+  lds_barrier();
+  for (int e = threadIdx.x; e < E; e += T) {
+    const int ln = e & 63, t = e >> 6, v = t & 3, tb = (t >> 2) % TB, j = (t >> 2) / TB;
+    const int row = tb * 16 + 4 * (ln >> 4) + v;
+    const int col = r * 64 + (jb0 + j) * 16 + (ln & 15);
+    if (row >= a.n || col >= a.m) continue;
+    float sum = red[e];
+    for (int w = 1; w < W; ++w) sum += red[w * E + e];
+    uint16_t y;
+    if (a.out_bf16) {
+      y = Bf16::from_f32(sum);
+      if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+    } else {
+      y = Fp16::from_f32(sum);
+      if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+    }
+    a.out[(int64_t)row * a.ldo + col] = y;
+  }
+}
+
 // ---- prefill kernel (N > 64 tokens) ----------------------------------------
 //
 // Compute-bound schedule.  Workgroup (row tile r, token block of BN = 256)
@@ -999,7 +1268,14 @@ static bool xvec_ok(const GemmArgs& a) {
 // enough workgroups, else one 16-feature j-block per workgroup (JBW 1), and
 // W waves so each wave keeps a batch of U tiles in flight.  An explicit
 // split_k > 1 runs S = split_k splits with the reduction.
-constexpr int kWideRowTiles = 192;   // row tiles from which whole-tile workgroups fill the GPU
+// Whole-tile workgroups (JBW 4) only where one-j-block workgroups would each
+// stage a large activation: with many row tiles and more than 8 tokens.  Below
+// that, four workgroups per row tile (one 16-feature j-block each) give 4x the
+// workgroups, which streams the weights faster (measured on MI355X: the stacked
+// gate/up projection at 1-4 tokens runs ~13% faster).
+constexpr int kWideRowTiles = 192;
+constexpr int kWideMinTokens = 9;
+static int pick_jbw(int n, int n_tr) { return (n_tr >= kWideRowTiles && n >= kWideMinTokens) ? 4 : 1; }
 
 // The arrival counters occupy a FIXED region at the head of the workspace so
 // that calls with different shapes never see another call's partials as
@@ -1020,16 +1296,36 @@ static int plan_max_waves(int jbw, int tb) {
   return w < bound ? w : bound;
 }
 
+// Waves per workgroup of the unsplit decode schedules.  gemm_decode_kernel and
+// gemm_splitk_kernel both take a row tile's tiles round-robin over W waves and
+// sum the wave partials in wave order, so with the same W they add the same
+// terms in the same order: their outputs are bitwise equal (the fused path
+// falls back to gemm_splitk_kernel where gemm_decode_kernel cannot stage the
+// activation).  About UMAX tiles per wave; at most 8 waves for whole-tile
+// (JBW 4) workgroups.
+#ifndef TQ_DEC_UMAX_JB1
+#define TQ_DEC_UMAX_JB1 8
+#endif
+#ifndef TQ_DEC_UMAX_JB4
+#define TQ_DEC_UMAX_JB4 6
+#endif
+static int decode_waves(int jbw, int n_tc) {
+  const int umax = jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+  const int wmax = jbw == 1 ? 16 : 8;
+  int W = (n_tc + umax - 1) / umax;
+  return W < 4 ? 4 : (W > wmax ? wmax : W);
+}
+
 static SplitPlan plan_split(int n, int n_tr, int n_tc, int split_k) {
   SplitPlan p;
   p.tb = pick_tb(n);
-  p.jbw = n_tr >= kWideRowTiles ? 4 : 1;
+  p.jbw = pick_jbw(n, n_tr);
   p.S = split_k > 1 ? split_k : 1;
   const int units = n_tr * (4 / p.jbw);
   if (p.S > 1 && units > kCounterCap) p.S = 1;
   const int per_split = (n_tc + p.S - 1) / p.S;
   const int U = plan_u(p.jbw, p.tb);
-  int W = (per_split + U - 1) / U;
+  int W = p.S == 1 ? decode_waves(p.jbw, n_tc) : (per_split + U - 1) / U;
   const int wmax = plan_max_waves(p.jbw, p.tb);
   if (W > wmax) W = wmax;
   p.W = W < 1 ? 1 : W;
@@ -1097,6 +1393,80 @@ static int resolve_plan(SplitPlan& p, int n, int n_tr, int split_k, float* ws, i
   return TQ_OK;
 }
 
+// Plan of gemm_decode_kernel: wave count, batch size, activation chunks per
+// thread, LDS bytes.  ok == false when the activation does not fit LDS or a
+// size limit is exceeded; the caller then uses gemm_splitk_kernel.
+struct DecodePlan {
+  int W, tb, jbw, umax, cmax;
+  size_t lds;
+  bool ok;
+};
+
+static DecodePlan plan_decode(int n, int k, int n_tr, int n_tc, bool quant) {
+  DecodePlan p{};
+  p.ok = false;
+  p.tb = pick_tb(n);
+  p.jbw = pick_jbw(n, n_tr);
+  p.umax = p.jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+  if (n < 1 || n > kDecodeMaxTokens || k != n_tc * 64 || (quant && n > kFusedMaxTokens)) return p;
+  const int W = decode_waves(p.jbw, n_tc);
+  p.W = W;
+  const int64_t T = (int64_t)W * kWave;
+  const int64_t codes = (int64_t)n * (k + 16);
+  const int64_t meta = (int64_t)n_tc * 4 * (quant ? 3 : 1);
+  const int64_t red = (int64_t)W * p.jbw * p.tb * 1024;
+  const int64_t chunks = quant ? (int64_t)n * k / 8 : (int64_t)n * k / 16;
+  const int64_t per = (chunks + T - 1) / T;
+  p.cmax = per <= 1 ? 1 : (per <= 2 ? 2 : (per <= 4 ? 4 : 8));
+  p.lds = (size_t)(codes + meta > red ? codes + meta : red);
+  // 16-token blocks: one or two (more than 32 rows use gemm_splitk_kernel)
+  p.ok = p.tb <= 2 && per <= (quant ? 4 : 8) && codes <= kDecCodesMax && n_tc <= 2 * T && p.lds <= 160 * 1024;
+  return p;
+}
+
+// Launches one instantiation; dynamic LDS above 64 KiB needs the kernel's
+// limit raised once (gfx950 has 160 KiB per workgroup).
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
+static void launch_decode_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX>;
+  if (p.lds > 64 * 1024) {
+    static bool raised = false;
+    if (!raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024) != hipSuccess)
+        return;   // the launch below is skipped; hipGetLastError reports the failure
+      raised = true;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(a.n_tr * (4 / JBW)), dim3(p.W * kWave), p.lds, s, a);
+}
+
+template <class XT, int TB, int JBW, int UMAX, bool QUANT>
+static void launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  switch (p.cmax) {
+    case 1: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 1>(a, p, s); break;
+    case 2: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 2>(a, p, s); break;
+    case 4: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 4>(a, p, s); break;
+    default:
+      if constexpr (!QUANT) launch_decode_one<XT, TB, JBW, UMAX, QUANT, 8>(a, p, s);   // QUANT plans stop at 4
+      break;
+  }
+}
+
+template <class XT, bool QUANT>
+static hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  if (p.jbw == 4) {
+    if constexpr (QUANT) launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, true>(a, p, s);
+    else if (p.tb == 1) launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
+    else launch_decode_c<XT, 2, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
+  } else {
+    if constexpr (QUANT) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
+    else if (p.tb == 1) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
+    else launch_decode_c<XT, 2, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -1149,6 +1519,12 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
   a.xvec = xvec_ok(a);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
+  if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec) {
+    const DecodePlan d = plan_decode(n, k, n_tr, n_tc, false);
+    if (d.ok)
+      return (int)((x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, false>(a, d, s)
+                                              : launch_decode<Fp16, false>(a, d, s));
+  }
   if (n <= kDecodeMaxTokens) {
     SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
     rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
@@ -1203,10 +1579,16 @@ extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, in
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
   a.xvec = (k == n_tc * 64 && (x_fp_stride_n % 8) == 0 && aligned16(x_fp)) ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (split_k <= 1 && a.xvec) {
+    const DecodePlan d = plan_decode(n, k, n_tr, n_tc, true);
+    if (d.ok)
+      return (int)((x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, true>(a, d, s)
+                                              : launch_decode<Fp16, true>(a, d, s));
+  }
   SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
   rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
   if (rc) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, true>(a, p, workspace, s)
                                             : launch_split<Fp16, true>(a, p, workspace, s);
   return (int)e;

@@ -12,11 +12,14 @@ projection groups and sibling-activation cache as the reference
 * Q/K/V and Gate/Up siblings can be stacked into one ``MixedLinearGroup``
   (one quantization + one GEMM per group), each member served a column slice.
 
-With ``cfg.fused_decode = True``, decode-sized inputs (at most 16 rows,
-fewer for very wide inputs) run quantization and GEMM as one launch
-(``linear_mixed_fused``), bit-identical to the two-launch path.  It is off
-by default: every GEMM workgroup then re-quantizes all column tiles of the
-activation, which on MI355X costs more than the separate quantize launch.
+Decode-sized inputs can run quantization and GEMM as one launch
+(``linear_mixed_fused``), bit-identical to the two-launch path: every GEMM
+workgroup quantizes the whole activation into LDS while its weights stream
+in.  That saves a launch (~2.5 us on MI355X) but repeats the quantization in
+every workgroup, so it pays off only for very few rows.  ``cfg.fused_decode``
+selects it: ``None`` / ``"auto"`` (default) for inputs of at most
+``FUSED_AUTO_MAX_ROWS`` rows, ``True`` for every size the fused launch takes
+(at most 16 rows, fewer for very wide inputs), ``False`` never.
 
 The extra state records the packed tiles' storage order (``tile_layout``) so a
 ``state_dict`` round trip keeps it.
@@ -39,6 +42,9 @@ from .quant_utils import (
 )
 
 DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 4096
+# Rows up to which cfg.fused_decode = "auto" fuses quantization into the GEMM
+# (measured on MI355X: 1 row saves ~2 us per projection, 4 rows break even).
+FUSED_AUTO_MAX_ROWS = 2
 # Sibling projections reuse one activation quantization for inputs of at least
 # this many rows (mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
@@ -172,6 +178,14 @@ class MixedLinear(nn.Module):
             limit = self._fused_rows = fused_max_tokens(self.K_orig)
         return limit
 
+    def _fused_rows_for_cfg(self) -> int:
+        mode = _cfg_get(self.cfg, "fused_decode", None)
+        if mode is False:
+            return 0
+        if mode is None or mode == "auto":
+            return min(FUSED_AUTO_MAX_ROWS, self._fused_limit())
+        return self._fused_limit()
+
     def _fused_decode(self, x_fp: torch.Tensor) -> torch.Tensor:
         out_dtype = self._out_dtype()
         return linear_mixed_fused(
@@ -199,7 +213,7 @@ class MixedLinear(nn.Module):
             raise ValueError(f"Input K mismatch: got {k_in}, expected {self.K_orig}")
         x_work = x2d.contiguous()
         chunk = self._activation_row_chunk_size()
-        if 0 < n_rows <= min(self._fused_limit(), chunk) and bool(_cfg_get(self.cfg, "fused_decode", False)):
+        if 0 < n_rows <= min(self._fused_rows_for_cfg(), chunk):
             y = self._fused_decode(x_work)
         elif n_rows <= chunk:
             x_int8, sx = _quantize_shared_activation(source=x, x_work=x_work, tile_n=self.tile_n,
