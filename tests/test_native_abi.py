@@ -68,6 +68,9 @@ def test_workspace_sizing(lib):
     # (unit, split, row, 64 cols); units = 4 j-block groups per row tile below
     # 192 row tiles, whole row tiles from there on
     assert lib.tq_gemm_workspace_elems(16, 3072, 48, 48, 8) == 4096 + 48 * 4 * 8 * 16 * 64
-    assert lib.tq_gemm_workspace_elems(4, 16384, 256, 48, 8) == 4096 + 256 * 8 * 4 * 64
+    # up to 8 tokens every row tile has four one-j-block workgroups (units)
+    assert lib.tq_gemm_workspace_elems(4, 16384, 256, 48, 8) == 4096 + 256 * 4 * 8 * 4 * 64
+    # whole-tile workgroups (one unit per row tile) from 9 tokens on 192+ row tiles
+    assert lib.tq_gemm_workspace_elems(16, 16384, 256, 48, 8) == 4096 + 256 * 8 * 16 * 64
     assert lib.tq_gemm_workspace_elems(4, 1 << 20, 1 << 14, 48, 8) == 0   # beyond the counter cap
     assert lib.tq_gemm_workspace_elems(100, 3072, 48, 48, 0) == 0     # general kernel: none
