@@ -12,7 +12,8 @@ Infinity Cache.  The step is captured once as a HIP graph and replayed.
 
 Prints ONE JSON line: value = whole-job TOPS (2*tokens*M*K summed over the
 step / step time); roofline = the GEMM kernel's packed-weight GB/s against
-8 TB/s HBM, from HIP events bracketing every GEMM launch; cpu_baseline = the
+8 TB/s HBM, from HIP events around a graph of the step's GEMM launches run
+back to back (per-launch average); cpu_baseline = the
 CPU oracle (oracle/tq_oracle.c, the reference's arithmetic) on a bounded
 sample of the same workload.
 """
@@ -281,39 +282,51 @@ def main():
     for item in launches:
         gemm(*item)
     torch.cuda.synchronize()
-    # Event pairs around every GEMM launch.  A calibrated spin kernel at the
-    # head of the stream keeps the GPU busy while the host enqueues all the
-    # pairs, so the GPU then runs them back to back and the events measure the
-    # kernels, not host launch overhead.
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    torch.cuda._sleep(1_000_000)
-    e1.record()
-    torch.cuda.synchronize()
-    cycles_per_ms = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
-    per_group = {name: [] for name, _, _ in GROUPS}
-    reps = max(3, min(args.steps, 10))
-    total_ms, n_launch = 0.0, 0
-    gemm_graph_ms = []
-    for _ in range(reps):
-        pairs = [(item[1], torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                 for item in launches]
-        torch.cuda._sleep(int(cycles_per_ms * 30))
-        for item, (_, a, b) in zip(launches, pairs):
-            a.record()
+    # GEMM kernel duration: the step's 112 GEMM launches (activations quantized
+    # beforehand) captured back to back in one HIP graph on stream s; HIP events
+    # on that stream bracket the replays, so the per-launch average covers the
+    # kernels and the gaps between them, nothing else.
+    with torch.cuda.stream(s):
+        for item in launches:
             gemm(*item)
-            b.record()
+    torch.cuda.synchronize()
+    ggraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ggraph, stream=s):
+        for item in launches:
+            gemm(*item)
+    reps = max(3, args.steps)
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            ggraph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            ggraph.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    total_ms = e0.elapsed_time(e1)
+    n_launch = reps * len(launches)
+    # per-group durations: one graph per projection group (28 launches each)
+    group_us = {}
+    for gname, _, _ in GROUPS:
+        sub = [item for item in launches if item[1] == gname]
+        gg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gg, stream=s):
+            for item in sub:
+                gemm(*item)
+        with torch.cuda.stream(s):
+            gg.replay()
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record(s)
+            for _ in range(reps):
+                gg.replay()
+            a1.record(s)
         torch.cuda.synchronize()
-        gemm_graph_ms.append(pairs[0][1].elapsed_time(pairs[-1][2]))
-        for name, a, b in pairs:
-            ms = a.elapsed_time(b)
-            per_group[name].append(ms)
-            total_ms += ms
-            n_launch += 1
+        group_us[gname] = a0.elapsed_time(a1) * 1e3 / (reps * len(sub))
+        del gg
     gemm_avg_s = total_ms / n_launch / 1e3
     bytes_per_launch = info["packed_bytes"] / len(launches)
     achieved = bytes_per_launch / gemm_avg_s / 1e9
-    group_us = {name: statistics.median(v) * 1e3 for name, v in per_group.items()}
 
     # dense bf16 context: the same linear set through torch.nn.functional.linear (hipBLASLt)
     dense = None
@@ -374,12 +387,12 @@ def main():
         "eager_ms_per_step": eager_s * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "tq::gemm_rows_kernel", "avg_launch_us": gemm_avg_s * 1e6,
+                     "kernel": "tq::gemm_decode_kernel", "avg_launch_us": gemm_avg_s * 1e6,
                      "bytes_per_launch": bytes_per_launch, "launches_per_step": len(launches),
-                     "group_median_us": group_us,
-                     "gemm_back_to_back_ms": statistics.median(gemm_graph_ms),
-                     "timing": "HIP events around each of the step's 112 GEMM launches, enqueued behind a "
-                               "spin kernel so they run back to back on the launch stream"},
+                     "group_avg_us": group_us,
+                     "timing": "HIP events on the launch stream around replays of one HIP graph holding the "
+                               "step's 112 GEMM launches back to back (activations quantized beforehand); "
+                               "per-launch average includes the inter-kernel gaps"},
         "dense_bf16": dense,
         "prefill": prefill,
         "cpu_baseline": cpu,
