@@ -138,6 +138,25 @@ int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
                               const int32_t* int8_row_ptr, int n, int k, int n_tr, int n_tc,
                               int tile_layout, int32_t* products, void* stream);
 
+/* ---- decode attention ----------------------------------------------------
+ * One query token per sequence over a static KV cache read up to a length
+ * held on the device (so a captured graph serves every position):
+ *   out[b, h, :] = softmax_t(scale * q[b, h, :] . k[b, t, h / G, :]) v[b, t, h / G, :]
+ *   for t < min(seq_used[b], max_len), G = q_heads / kv_heads (<= 8), head_dim 128.
+ * q, out: [batch, q_heads, head_dim] with strides (elements) per batch / head;
+ * k, v: caches sharing strides per batch / position / kv head, unit stride
+ * inside a head.  16-byte aligned pointers, strides multiples of 8.  fp32
+ * accumulation; workspace = tq_decode_attention_workspace_elems() fp32 elements
+ * (split partials; no initialisation needed).
+ * Replaces the torch.ops.aten._flash_attention_forward(..., seqused_k=...)
+ * call of _cuda_graph_attention (src/runtime/graph_decode.py:56-71). */
+int64_t tq_decode_attention_workspace_elems(int batch, int q_heads, int max_len);
+int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                        const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
+                        const int32_t* seq_used, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                        int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
+                        float scale, float* workspace, int64_t workspace_elems, void* stream);
+
 /* ---- load-time packing -------------------------------------------------
  * w [m, k] (x_dtype, row stride w_stride_m) is read as if zero-padded to
  * multiples of 64.  tile_ids are flat ids r * n_tc + c.                  */

@@ -1,0 +1,223 @@
+"""GPU: decode attention kernel, load-time packing driver and the HIP-graph
+greedy decoder (mirrors of src/quantization/api.py and src/runtime/graph_decode.py).
+
+Bars: attention output within 2 bf16 ulp of a float64 reference (fp32
+accumulation); loaded models bitwise equal to models packed directly from the
+same weights; decoder logits equal to the eager forward within bf16 rounding
+noise, identical across replays."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from e2e_models import tiny_llama_config, tiny_qwen2_config, write_checkpoint, write_tile_maps
+from tilequant_amd import api
+from tilequant_amd.attention import decode_attention, decode_attention_workspace
+from tilequant_amd.mixed_linear import MixedLinear
+from tilequant_amd.pack import pack_weight_from_tile_ids
+from tilequant_amd.rules import iter_target_linears
+from tilequant_amd.types import ApplyConfig
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _attention_reference(q, k, v, lens, scale):
+    """float64 softmax attention of each sequence over its first lens[b] keys."""
+    q, k, v = (t.double().cpu() for t in (q, k, v))
+    B, Hq, D = q.shape
+    G = Hq // k.shape[1]
+    out = torch.zeros((B, Hq, D), dtype=torch.float64)
+    for b in range(B):
+        n = int(lens[b])
+        if n == 0:
+            continue
+        kk = k[b, :, :n].repeat_interleave(G, dim=0)      # [Hq, n, D]
+        vv = v[b, :, :n].repeat_interleave(G, dim=0)
+        s = torch.einsum("hd,hnd->hn", q[b], kk) * scale
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.einsum("hn,hnd->hd", p, vv)
+    return out
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L", [(4, 24, 8, 2304), (2, 7, 1, 300), (1, 8, 1, 64), (3, 40, 8, 513)])
+@pytest.mark.parametrize("token_major", [False, True])
+def test_decode_attention_matches_reference(B, Hq, Hkv, L, token_major):
+    g = torch.Generator().manual_seed(B * 1000 + L)
+    D = 128
+    q = torch.randn((B, Hq, D), generator=g).to(torch.bfloat16)
+    if token_major:   # [B, L, Hkv, D] storage viewed as [B, Hkv, L, D]
+        k = torch.randn((B, L, Hkv, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+        v = torch.randn((B, L, Hkv, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    else:
+        k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16)
+        v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16)
+    lens = [L, 1, 256, 257][:B] if B > 1 else [L // 2 + 3]
+    lens = [min(x, L) for x in lens]
+    scale = D ** -0.5
+    kd, vd = k.to(DEV), v.to(DEV)
+    out = decode_attention(q.to(DEV), kd, vd, torch.tensor(lens, dtype=torch.int32, device=DEV), scale=scale)
+    ref = _attention_reference(q, k, v, lens, scale)
+    got = out.double().cpu()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -126))) - 7)
+    assert bool(((got - ref).abs() <= 2 * ulp + 1e-6).all()), float(((got - ref).abs() / ulp).max())
+    # bitwise reproducible
+    assert torch.equal(decode_attention(q.to(DEV), kd, vd, torch.tensor(lens, dtype=torch.int32, device=DEV),
+                                        scale=scale), out)
+
+
+def test_decode_attention_graph_replays_follow_device_length():
+    B, Hq, Hkv, L, D = 2, 24, 8, 600, 128
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((B, Hq, D), generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    seq = torch.ones((B,), dtype=torch.int32, device=DEV)
+    ws = decode_attention_workspace(B, Hq, L, DEV)
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        decode_attention(q, k, v, seq, scale=D ** -0.5, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        decode_attention(q, k, v, seq, scale=D ** -0.5, out=out, workspace=ws)
+    for n in (1, 255, 256, 257, 599, 600, 17):
+        seq.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = decode_attention(q, k, v, torch.full((B,), n, dtype=torch.int32, device=DEV), scale=D ** -0.5)
+        assert torch.equal(out, want), n
+
+
+def test_decode_attention_argument_errors():
+    q = torch.zeros((1, 4, 64), dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros((1, 2, 8, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):   # head_dim 64 is not served
+        decode_attention(q, k, k, torch.ones(1, dtype=torch.int32, device=DEV), scale=1.0)
+    q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros((1, 2, 8, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        decode_attention(q, k, k, torch.ones(1, dtype=torch.int64, device=DEV), scale=1.0)
+
+
+def _direct_model(model_dir, keep_dir, apply_cfg):
+    """Dense checkpoint model with every target swapped for a directly packed MixedLinear (no groups)."""
+    from transformers import AutoModelForCausalLM
+
+    model = AutoModelForCausalLM.from_pretrained(model_dir, dtype=torch.bfloat16, attn_implementation="sdpa").to(DEV)
+    cfg = api._make_cfg(apply_cfg)
+    maps = api.validate_fp16_ids_coverage_and_shapes(model, keep_dir, apply_cfg)
+    for parent, attr, name, lin in iter_target_linears(model, cfg, apply_cfg.model_type):
+        f16, i8, n_tr, n_tc = maps[name]
+        pack = pack_weight_from_tile_ids(lin.weight.detach(), n_tr=n_tr, n_tc=n_tc, int8_tile_ids=i8,
+                                         fp16_tile_ids=f16, cfg=cfg)
+        bias = lin.bias.detach() if lin.bias is not None else None
+        setattr(parent, attr, MixedLinear(pack, bias, cfg).to(DEV))
+    return model.eval()
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen"])
+def test_loader_equals_direct_packing_bitwise(tmp_path, family):
+    config = tiny_llama_config() if family == "llama" else tiny_qwen2_config()
+    sd = write_checkpoint(config, tmp_path / "ckpt", seed=11, shards=2)
+    write_tile_maps(config, tmp_path / "keep10", frac=0.1, seed=12, model_type=family)
+    apply_cfg = ApplyConfig(model_type=family, dtype_out="bf16")
+    model, stats = api.load_mixed_precision_model_from_masks(tmp_path / "ckpt", tmp_path / "keep10", apply_cfg,
+                                                             torch.bfloat16, DEV, attn_implementation="sdpa")
+    assert stats["num_targets"] == 14 and stats["num_replaced_during_load"] == 14
+    assert stats["fused_projection_groups"] == 4          # QKV and Gate/Up per layer
+    emb = model.get_input_embeddings().weight
+    assert torch.equal(emb.cpu(), sd["model.embed_tokens.weight"])
+    ref = _direct_model(tmp_path / "ckpt", tmp_path / "keep10", apply_cfg)
+    ids = torch.randint(0, config.vocab_size, (2, 40), generator=torch.Generator().manual_seed(1)).to(DEV)
+    with torch.inference_mode():
+        a = model(input_ids=ids).logits
+        b = ref(input_ids=ids).logits
+    assert torch.equal(a, b)   # stacked groups == members, same packing, same kernels
+
+
+def test_random_init_builder_packs_every_target():
+    config = tiny_llama_config()
+    apply_cfg = ApplyConfig(model_type="llama", dtype_out="bf16")
+    model, stats = api.build_mixed_precision_model(config, apply_cfg, DEV, keep_frac=0.05, seed=3)
+    assert stats["num_targets"] == 14 and stats["fused_projection_groups"] == 4
+    assert all(p.device.type == "cuda" for p in model.parameters())
+    ids = torch.randint(0, config.vocab_size, (1, 8)).to(DEV)
+    with torch.inference_mode():
+        logits = model(input_ids=ids).logits
+    assert logits.shape == (1, 8, config.vocab_size) and bool(torch.isfinite(logits).all())
+
+
+def _eager_teacher_forced(model, prompt, tokens):
+    """Eager forward with a DynamicCache on fused SDPA, fed the given tokens:
+    last-position logits of the prompt and of every following step."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    outs = []
+    with torch.inference_mode(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        o = model(input_ids=prompt, use_cache=True, logits_to_keep=1)
+        outs.append(o.logits[:, -1].float())
+        cache = o.past_key_values
+        for t in range(tokens.shape[1]):
+            o = model(input_ids=tokens[:, t:t + 1], past_key_values=cache, use_cache=True, logits_to_keep=1)
+            outs.append(o.logits[:, -1].float())
+            cache = o.past_key_values
+    return outs
+
+
+def test_graph_decoder_matches_eager_and_replays_independently():
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+
+    config = tiny_llama_config(layers=2)
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), DEV,
+                                               keep_frac=0.05, seed=21)
+    B, P, O = 2, 96, 12
+    g = torch.Generator().manual_seed(22)
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=g)
+    dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV)
+    assert dec.prefill_captured
+    first = dec.prefill(prompt).clone()   # the returned token buffer is reused by decode
+    prefill_logits = dec.last_logits[:, -1].float().clone()
+    ids = dec.decode(O - 1).clone()
+    assert ids.shape == (B, O) and torch.equal(ids[:, :1], first)
+    # every generated token is the argmax of the decoder's own logits; compare with
+    # the eager model fed the same tokens
+    other = torch.randint(0, config.vocab_size, (B, P), generator=g)
+    ids_other = dec.generate(other).clone()
+    again = dec.generate(prompt).clone()
+    assert torch.equal(again, ids)                 # reset-and-prefill makes replays independent
+    dec.close()
+    ref = _eager_teacher_forced(model, prompt.to(DEV), ids[:, :-1])
+    scale = max(float(r.abs().max()) for r in ref)
+    assert float((prefill_logits - ref[0]).abs().max()) <= 2e-2 * scale
+    # the decode graph's argmax agrees with the eager logits wherever the eager
+    # margin between the best two logits exceeds the rounding noise
+    for t in range(1, O):
+        r = ref[t]
+        top2 = r.topk(2, dim=-1).values
+        clear = (top2[:, 0] - top2[:, 1]) > 2e-2 * scale
+        assert torch.equal(r.argmax(-1)[clear], ids[:, t][clear]), t
+    assert not torch.equal(ids_other, ids)
+
+
+def test_decoder_argument_errors():
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+
+    config = tiny_llama_config(layers=1)
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), DEV,
+                                               keep_frac=0.05, seed=1)
+    with pytest.raises(ValueError):
+        CudaGraphGreedyDecoder(model, prompt_tokens=0, max_new_tokens=4, device=DEV)
+    dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=8, max_new_tokens=3, batch_size=1, device=DEV)
+    with pytest.raises(ValueError):
+        dec.prefill(torch.zeros((1, 9), dtype=torch.long))
+    with pytest.raises(ValueError):
+        dec.decode(5)
+    with pytest.raises(RuntimeError, match="already has"):
+        CudaGraphGreedyDecoder(model, prompt_tokens=8, max_new_tokens=3, device=DEV)
+    dec.close()

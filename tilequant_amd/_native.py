@@ -50,6 +50,9 @@ _SIGNATURES = {
                                    _i, _i, _i, _i, _i,
                                    _i, _i, _p, _i64, _p]),
     "tq_gemm_tile_products_i32": (_i, [_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
+    "tq_decode_attention_workspace_elems": (_i64, [_i, _i, _i]),
+    "tq_decode_attention": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+                                 _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
     "tq_pack_int8_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
     "tq_pack_16bit_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p]),
     "tq_tiles_relayout": (_i, [_p, _p, _i64, _i, _i, _i, _p]),
