@@ -53,6 +53,15 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=8192, help="prefill measurement rows (0 = skip)")
     ap.add_argument("--prefill-keep", type=float, default=0.05)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--e2e", type=int, default=1, help="end-to-end generation section (BASELINE configs[4]); 0 = skip")
+    ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end section (profiling)")
+    ap.add_argument("--e2e-batch", type=int, default=4)
+    ap.add_argument("--e2e-prompt", type=int, default=2048)
+    ap.add_argument("--e2e-output", type=int, default=256)
+    ap.add_argument("--e2e-warmup", type=int, default=2)
+    ap.add_argument("--e2e-repeats", type=int, default=5)
+    ap.add_argument("--e2e-dense-eager", type=int, default=1)
+    ap.add_argument("--e2e-dense", type=int, default=1, help="also run the dense bf16 baseline model")
     return ap.parse_args()
 
 
@@ -161,6 +170,134 @@ def prefill_measure(args, device):
                     "GEMM), HIP events, median of 5"}
 
 
+LLAMA32_3B = dict(vocab_size=128256, hidden_size=HIDDEN, intermediate_size=MLP, num_hidden_layers=LAYERS,
+                  num_attention_heads=24, num_key_value_heads=8, head_dim=128, rope_theta=5e5, rms_norm_eps=1e-5,
+                  max_position_embeddings=131072, tie_word_embeddings=True)
+
+
+def _dense_model(config, device, seed, dtype):
+    """Random-init dense bf16 model of the same architecture (the baseline), materialised on the device."""
+    import torch
+    from accelerate import init_empty_weights
+    from transformers import AutoModelForCausalLM
+
+    with init_empty_weights():
+        model = AutoModelForCausalLM.from_config(config, dtype=dtype, attn_implementation="sdpa")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    for name, p in list(model.named_parameters()):
+        mod_name, _, leaf = name.rpartition(".")
+        owner = model.get_submodule(mod_name) if mod_name else model
+        if "norm" in mod_name.lower():
+            value = torch.ones(p.shape, device=device, dtype=dtype)
+        else:
+            value = (torch.randn(p.shape, generator=gen, device=device, dtype=torch.float32) * 0.02).to(dtype)
+        owner._parameters[leaf] = torch.nn.Parameter(value, requires_grad=False)
+    for mod in model.modules():
+        for bname, buf in list(mod._buffers.items()):
+            if buf is not None and buf.device != device:
+                mod._buffers[bname] = buf.to(device)
+    model.tie_weights()
+    return model.eval()
+
+
+def e2e_measure(args, device):
+    """BASELINE configs[4] / the reference's benchmark protocol
+    (examples/benchmark_generation.py:74-155): random-init Llama-3.2-3B
+    architecture, every decoder linear a MixedLinear with a seeded uniform
+    keep01 tile map, greedy generation through the HIP-graph decoder; batch 4,
+    2048 seeded uniform prompt ids, 256 output tokens.  TTFT = request start to
+    first token (host prompt copy included), TPOT = (end - first) / (O - 1),
+    tok/s = B * O / (end - start); medians over the timed requests.  The dense
+    bf16 model of the same architecture runs the reference's eager loop and the
+    same graph decoder."""
+    import gc
+
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from transformers import LlamaConfig
+    from tilequant_amd.api import build_mixed_precision_model
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+    from tilequant_amd.types import ApplyConfig
+
+    B, P, O = args.e2e_batch, args.e2e_prompt, args.e2e_output
+    config = LlamaConfig(**LLAMA32_3B, attn_implementation="sdpa")
+    g = torch.Generator().manual_seed(args.seed + 99)
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=g)
+
+    def graph_request(dec):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompt)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dec.decode(O - 1)
+        torch.cuda.synchronize()
+        return t0, t1, time.perf_counter()
+
+    @torch.inference_mode()
+    def eager_request(model):
+        # the reference's dense loop (benchmark_generation.py:74-88), fused SDPA backends only
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = model(input_ids=prompt.to(device), use_cache=True, logits_to_keep=1)
+            cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(O - 1):
+                out = model(input_ids=cur, past_key_values=cache, use_cache=True, logits_to_keep=1)
+                cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
+            torch.cuda.synchronize()
+            return t0, t1, time.perf_counter()
+
+    def summarize(rows):
+        ttft = statistics.median((t1 - t0) * 1e3 for t0, t1, _ in rows)
+        tpot = statistics.median((t2 - t1) * 1e3 / max(O - 1, 1) for _, t1, t2 in rows)
+        tps = statistics.median(B * O / (t2 - t0) for t0, _, t2 in rows)
+        return {"ttft_ms": ttft, "tpot_ms": tpot, "output_tok_s": tps, "requests": len(rows)}
+
+    def run(fn, target):
+        for _ in range(args.e2e_warmup):
+            fn(target)
+        return summarize([fn(target) for _ in range(args.e2e_repeats)])
+
+    res = {"batch": B, "prompt": P, "output": O, "keep": args.keep, "data": "random-init weights, seeded uniform "
+           "prompt ids, seeded uniform tile maps"}
+    t0 = time.perf_counter()
+    model, stats = build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), device,
+                                               keep_frac=args.keep, seed=args.seed)
+    res["build_s"] = time.perf_counter() - t0
+    torch.cuda.reset_peak_memory_stats()
+    dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
+    res["tilequant_graph"] = run(graph_request, dec)
+    res["tilequant_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
+    dec.close()
+    del dec, model
+    gc.collect()
+    torch.cuda.empty_cache()
+    if not args.e2e_dense:
+        return res
+    dense = _dense_model(config, device, args.seed, torch.bfloat16)
+    torch.cuda.reset_peak_memory_stats()
+    dec = CudaGraphGreedyDecoder.prepare(dense, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
+    res["dense_bf16_graph"] = run(graph_request, dec)
+    res["dense_bf16_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
+    dec.close()
+    del dec
+    if args.e2e_dense_eager:
+        res["dense_bf16_eager"] = run(eager_request, dense)
+    del dense
+    gc.collect()
+    torch.cuda.empty_cache()
+    tq, dg = res["tilequant_graph"], res["dense_bf16_graph"]
+    res["tpot_speedup_vs_dense_graph"] = dg["tpot_ms"] / tq["tpot_ms"]
+    res["ttft_speedup_vs_dense_graph"] = dg["ttft_ms"] / tq["ttft_ms"]
+    if "dense_bf16_eager" in res:
+        res["tpot_speedup_vs_dense_eager"] = res["dense_bf16_eager"]["tpot_ms"] / tq["tpot_ms"]
+    return res
+
+
 def cpu_baseline(args, layers, xs):
     """Time the CPU oracle (reference arithmetic, OpenMP) on the first cpu_layers layers."""
     import numpy as np
@@ -221,6 +358,9 @@ def main():
     _native.load()
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.e2e_only:
+        print(json.dumps({"e2e": e2e_measure(args, device)}), flush=True)
+        return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)
 
@@ -362,6 +502,8 @@ def main():
     cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
+    torch.cuda.empty_cache()
+    e2e = e2e_measure(args, device) if args.e2e else None
 
     result = {
         "metric": "mixed tile GEMM TOPS + % roofline (M=4 decode, M=8192 prefill); TPOT",
@@ -395,6 +537,7 @@ def main():
                                "per-launch average includes the inter-kernel gaps"},
         "dense_bf16": dense,
         "prefill": prefill,
+        "e2e": e2e,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
