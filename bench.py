@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--e2e-repeats", type=int, default=5)
     ap.add_argument("--e2e-dense-eager", type=int, default=1)
     ap.add_argument("--e2e-dense", type=int, default=1, help="also run the dense bf16 baseline model")
+    ap.add_argument("--e2e-module-path", type=int, default=1,
+                    help="also time both models with the modules' own forward in the decode graph")
     return ap.parse_args()
 
 
@@ -272,8 +274,17 @@ def e2e_measure(args, device):
     dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
     res["tilequant_graph"] = run(graph_request, dec)
     res["tilequant_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
+    res["tilequant_graph"]["decode_step"] = "fused (10 launches per layer)" if dec._fused else "model forward"
     dec.close()
-    del dec, model
+    del dec
+    if args.e2e_module_path:
+        # the reference's structure: the model's own modules replayed in the decode graph
+        dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device,
+                                             fused_decode=False)
+        res["tilequant_graph_module_step"] = run(graph_request, dec)
+        dec.close()
+        del dec
+    del model
     gc.collect()
     torch.cuda.empty_cache()
     if not args.e2e_dense:
@@ -283,8 +294,16 @@ def e2e_measure(args, device):
     dec = CudaGraphGreedyDecoder.prepare(dense, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
     res["dense_bf16_graph"] = run(graph_request, dec)
     res["dense_bf16_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
+    res["dense_bf16_graph"]["decode_step"] = "fused glue, hipBLASLt GEMMs on stacked weights" if dec._fused \
+        else "model forward"
     dec.close()
     del dec
+    if args.e2e_module_path:
+        dec = CudaGraphGreedyDecoder.prepare(dense, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device,
+                                             fused_decode=False)
+        res["dense_bf16_graph_module_step"] = run(graph_request, dec)
+        dec.close()
+        del dec
     if args.e2e_dense_eager:
         res["dense_bf16_eager"] = run(eager_request, dense)
     del dense
@@ -295,6 +314,8 @@ def e2e_measure(args, device):
     res["ttft_speedup_vs_dense_graph"] = dg["ttft_ms"] / tq["ttft_ms"]
     if "dense_bf16_eager" in res:
         res["tpot_speedup_vs_dense_eager"] = res["dense_bf16_eager"]["tpot_ms"] / tq["tpot_ms"]
+    if "dense_bf16_graph_module_step" in res:
+        res["tpot_speedup_vs_dense_graph_module_step"] = res["dense_bf16_graph_module_step"]["tpot_ms"] / tq["tpot_ms"]
     return res
 
 

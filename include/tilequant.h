@@ -157,6 +157,50 @@ int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, c
                         int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
                         float scale, float* workspace, int64_t workspace_elems, void* stream);
 
+/* As tq_decode_attention, and the attention output (the [batch, q_heads *
+ * head_dim] input of the next projection) is also quantized like
+ * tq_act_quant_fused: q_out int8 with row stride q_out_stride_b, sx_out
+ * [q_heads * head_dim / 64].  batch <= 16.  No reference counterpart (the
+ * reference quantizes the projection input in a separate launch,
+ * src/models/mixed_linear.py:233-239). */
+int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                              const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
+                              const int32_t* seq_used, void* out, int64_t out_stride_b,
+                              int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b, float* sx_out,
+                              int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
+                              float scale, float* workspace, int64_t workspace_elems, void* stream);
+
+/* ---- decode-step producers fused with the activation quantization ---------
+ * Each computes a decoder-layer step that feeds a mixed tile GEMM and, when
+ * q_out is non-null, quantizes its output like tq_act_quant_fused (scales over
+ * ALL n rows, sx_out[k / 64]).  Rounding follows the Hugging Face module code
+ * op by op.  n <= 64 rows; widths multiples of 64; 16-bit rows 16-byte
+ * aligned.  No reference counterparts: the reference runs the model's own
+ * modules and quantizes inside every MixedLinear call
+ * (src/models/mixed_linear.py:233-239); these replace those chains inside a
+ * captured decode step (src/runtime/graph_decode.py:350-385). */
+
+/* h = x + delta (rounded; skipped when delta is NULL, then h = x and h_out is
+ * unused), y = weight * round(h * rsqrt(mean(h^2) + eps)) (LlamaRMSNorm). */
+int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                         const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out,
+                         int64_t y_stride, int8_t* q_out, int64_t q_stride, float* sx_out, int dtype, int n,
+                         int k, void* stream);
+
+/* y = round(round(silu(gate)) * up) for gate_up = [gate | up] of width 2 * inter. */
+int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride, int8_t* q_out,
+                      int64_t q_stride, float* sx_out, int dtype, int n, int inter, void* stream);
+
+/* RoPE (q * cos + rotate_half(q) * sin, head_dim 128) on the q and k heads of
+ * a stacked [n, (q_heads + 2 kv_heads) * 128] q/k/v projection output; rotated
+ * q to q_out [n, q_heads, 128]; rotated k and v written to the caches at
+ * index *position (device int64; no write when outside [0, max_len)).
+ * cos / sin: the 128 values at the position. */
+int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin, const int64_t* position,
+                  void* q_out, int64_t q_stride_b, int64_t q_stride_h, void* k_cache, void* v_cache,
+                  int64_t cache_stride_b, int64_t cache_stride_h, int64_t cache_stride_l, int dtype, int n,
+                  int q_heads, int kv_heads, int head_dim, int max_len, void* stream);
+
 /* ---- load-time packing -------------------------------------------------
  * w [m, k] (x_dtype, row stride w_stride_m) is read as if zero-padded to
  * multiples of 64.  tile_ids are flat ids r * n_tc + c.                  */

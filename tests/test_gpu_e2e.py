@@ -221,3 +221,152 @@ def test_decoder_argument_errors():
     with pytest.raises(RuntimeError, match="already has"):
         CudaGraphGreedyDecoder(model, prompt_tokens=8, max_new_tokens=3, device=DEV)
     dec.close()
+
+
+# ---- fused decode-step kernels -------------------------------------------------------------------
+from tilequant_amd import _native as nat                               # noqa: E402
+from tilequant_amd.quant_utils import quantize_activation_tile_absmax   # noqa: E402
+
+
+def _ulp_close(a: torch.Tensor, b: torch.Tensor, ulps: float = 1.0) -> bool:
+    a, b = a.float(), b.float()
+    ulp = torch.exp2(torch.floor(torch.log2(b.abs().clamp_min(2.0 ** -126))) - 7)
+    return bool(((a - b).abs() <= ulps * ulp).all())
+
+
+@pytest.mark.parametrize("n,k,with_delta", [(4, 3072, True), (1, 3072, False), (16, 512, True), (3, 8192, True)])
+def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    g = torch.Generator().manual_seed(n * 7 + k)
+    x = (torch.randn((n, k), generator=g) * 3).to(torch.bfloat16).to(DEV)
+    d = (torch.randn((n, k), generator=g) * 2).to(torch.bfloat16).to(DEV)
+    norm = LlamaRMSNorm(k, eps=1e-5).to(DEV).to(torch.bfloat16)
+    norm.weight.data = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16).to(DEV)
+    h_ref = (x + d) if with_delta else x
+    with torch.inference_mode():
+        y_ref = norm(h_ref)
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    q = torch.empty((n, k), dtype=torch.int8, device=DEV)
+    sx = torch.empty((k // 64,), dtype=torch.float32, device=DEV)
+    rc = nat.lib().tq_add_rmsnorm_quant(x.data_ptr(), k, d.data_ptr() if with_delta else None, k,
+                                        norm.weight.data_ptr(), 1e-5, h.data_ptr(), k, y.data_ptr(), k,
+                                        q.data_ptr(), k, sx.data_ptr(), 0, n, k,
+                                        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    if with_delta:
+        assert torch.equal(h, h_ref)                       # the residual add rounds exactly like torch
+    assert _ulp_close(y, y_ref, 1.0)                        # only the sum-of-squares order differs
+    q_ref, sx_ref = quantize_activation_tile_absmax(y)
+    assert torch.equal(q, q_ref) and torch.equal(sx, sx_ref)   # same closed form as the quantizer, bitwise
+
+
+@pytest.mark.parametrize("n,inter", [(4, 8192), (1, 1024), (16, 512)])
+def test_silu_mul_quant_matches_module_and_quantizer(n, inter):
+    g = torch.Generator().manual_seed(n + inter)
+    gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        y_ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+    y = torch.empty((n, inter), dtype=torch.bfloat16, device=DEV)
+    q = torch.empty((n, inter), dtype=torch.int8, device=DEV)
+    sx = torch.empty((inter // 64,), dtype=torch.float32, device=DEV)
+    rc = nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y.data_ptr(), inter, q.data_ptr(), inter,
+                                     sx.data_ptr(), 0, n, inter, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert _ulp_close(y, y_ref, 1.0)
+    q_ref, sx_ref = quantize_activation_tile_absmax(y)
+    assert torch.equal(q, q_ref) and torch.equal(sx, sx_ref)
+
+
+def test_rope_cache_matches_module_ops():
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    B, hq, hkv, D, L, pos = 4, 24, 8, 128, 300, 137
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(DEV)
+    ang = torch.randn(D, generator=g)
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    kc = torch.zeros((B, hkv, L, D), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty((B, hq, D), dtype=torch.bfloat16, device=DEV)
+    position = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    rc = nat.lib().tq_rope_cache(qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), position.data_ptr(),
+                                 q_out.data_ptr(), q_out.stride(0), q_out.stride(1), kc.data_ptr(), vc.data_ptr(),
+                                 kc.stride(0), kc.stride(1), kc.stride(2), 0, B, hq, hkv, D, L,
+                                 torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    q = qkv[:, :hq * D].view(B, 1, hq, D).transpose(1, 2)
+    k = qkv[:, hq * D:(hq + hkv) * D].view(B, 1, hkv, D).transpose(1, 2)
+    v = qkv[:, (hq + hkv) * D:].view(B, 1, hkv, D).transpose(1, 2)
+    q_ref, k_ref = apply_rotary_pos_emb(q, k, cos.view(1, 1, D), sin.view(1, 1, D))
+    torch.cuda.synchronize()
+    assert torch.equal(q_out, q_ref[:, :, 0])
+    assert torch.equal(kc[:, :, pos], k_ref[:, :, 0]) and torch.equal(vc[:, :, pos], v[:, :, 0])
+    assert int(kc[:, :, :pos].abs().sum()) == 0 and int(vc[:, :, pos + 1:].abs().sum()) == 0
+
+
+def test_attention_quant_equals_attention_then_quantizer():
+    B, Hq, Hkv, L, D = 4, 24, 8, 700, 128
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn((B, Hq, D), generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    seq = torch.tensor([700, 1, 129, 400], dtype=torch.int32, device=DEV)
+    ref = decode_attention(q, k, v, seq, scale=D ** -0.5)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=DEV)
+    qo = torch.empty((B, Hq * D), dtype=torch.int8, device=DEV)
+    sx = torch.empty((Hq * D // 64,), dtype=torch.float32, device=DEV)
+    ws = decode_attention_workspace(B, Hq, L, DEV)
+    rc = nat.lib().tq_decode_attention_quant(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+                                             k.stride(0), k.stride(2), k.stride(1), seq.data_ptr(), out.data_ptr(),
+                                             out.stride(0), D, qo.data_ptr(), qo.stride(0), sx.data_ptr(), 0, B, Hq,
+                                             Hkv, D, L, D ** -0.5, ws.data_ptr(), ws.numel(),
+                                             torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(B, Hq, D), ref)
+    q_ref, sx_ref = quantize_activation_tile_absmax(out)
+    assert torch.equal(qo, q_ref) and torch.equal(sx, sx_ref)
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen"])
+def test_fused_decode_step_matches_module_forward(family):
+    """The fused one-token step against the model's own forward in the same
+    captured decoder (fused_decode=False): same tokens fed, logits within
+    bf16 rounding noise, argmax equal wherever the margin is clear."""
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+
+    config = tiny_llama_config(layers=2) if family == "llama" else tiny_qwen2_config(layers=2)
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out="bf16"), DEV,
+                                               keep_frac=0.05, seed=31)
+    B, P, O = 4, 80, 10
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(32))
+    dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV)
+    assert dec._fused is not None
+    dec.prefill(prompt)
+    steps = []
+    for _ in range(O - 1):
+        dec._graph.replay()
+        steps.append((dec._decode_logits[:, -1].float().clone(), dec._token.clone()))
+    ids_fused = dec._generated.clone()
+    dec.close()
+    ref = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV,
+                                         fused_decode=False)
+    assert ref._fused is None
+    ref.prefill(prompt)
+    # feed the fused run's tokens to the module path and compare logits step by step
+    for t in range(O - 1):
+        with torch.inference_mode():
+            ref._token.copy_(ids_fused[:, t:t + 1])
+        ref._graph.replay()
+        r = ref._decode_logits[:, -1].float()
+        f = steps[t][0]
+        scale = float(r.abs().max())
+        assert float((f - r).abs().max()) <= 3e-2 * scale, t
+        top2 = r.topk(2, dim=-1).values
+        clear = (top2[:, 0] - top2[:, 1]) > 3e-2 * scale
+        assert torch.equal(f.argmax(-1)[clear], r.argmax(-1)[clear]), t
+    ref.close()

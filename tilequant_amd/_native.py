@@ -53,6 +53,13 @@ _SIGNATURES = {
     "tq_decode_attention_workspace_elems": (_i64, [_i, _i, _i]),
     "tq_decode_attention": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                  _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
+    "tq_decode_attention_quant": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+                                       _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
+    "tq_add_rmsnorm_quant": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _p, _i64, _p,
+                                  _i, _i, _i, _p]),
+    "tq_silu_mul_quant": (_i, [_p, _i64, _p, _i64, _p, _i64, _p, _i, _i, _i, _p]),
+    "tq_rope_cache": (_i, [_p, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i, _i, _i, _i, _i,
+                           _i, _p]),
     "tq_pack_int8_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
     "tq_pack_16bit_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p]),
     "tq_tiles_relayout": (_i, [_p, _p, _i64, _i, _i, _i, _p]),

@@ -12,21 +12,24 @@
 // kv head kvh and writes a partial (running max m, sum l, unnormalised o[D])
 // per query head; a second kernel merges the splits of each (b, h) in split
 // order.  Splits past seq_used write m = -inf, l = 0.
+//   loads: all K and V rows of a wave's keys are issued at entry (8 + 8
+//       16-byte loads per lane), so the chunk costs one memory round trip.
 //   QK: a wave covers 4 keys per step, 16 lanes per key row (16 bytes = 8
 //       elements each, so each row is one coalesced 256-byte read); the 8-wide
 //       partial dots are summed across the 16 lanes with DPP.
-//   softmax: scores (pre-multiplied by scale * log2 e) in LDS, workgroup
-//       max / exp2 / sum.
-//   PV: same lane mapping over V; per-lane accumulators for G heads x 8
-//       dimensions, reduced across the wave with ds_swizzle-free xor shuffles,
-//       then across the 4 waves through LDS in wave order.
+//   softmax: scores (pre-multiplied by scale * log2 e) in LDS; after one
+//       barrier every wave derives the chunk's max and sum itself.
+//   PV: same lane mapping over V, probabilities recomputed from the scores;
+//       per-lane accumulators for G heads x 8 dimensions, reduced across the
+//       wave with xor shuffles, then across the 4 waves through LDS in wave
+//       order.
 // Everything accumulates in fp32; results are bitwise reproducible.
 #include "tq_common.h"
 
 namespace tq {
 
 constexpr int kAttnD = 128;        // head dimension served
-constexpr int kAttnChunk = 256;    // keys per split
+constexpr int kAttnChunk = 128;    // keys per split
 constexpr int kAttnThreads = 256;  // 4 waves
 constexpr int kAttnMaxG = 8;       // query heads per kv head
 constexpr float kLog2e = 1.4426950408889634f;
@@ -63,138 +66,113 @@ __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
   }
 }
 
-template <class XT>
+template <class XT, int G>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_split_kernel(AttnArgs a) {
-  __shared__ float sc[kAttnMaxG][kAttnChunk];        // scores, then probabilities
-  __shared__ float wred[kAttnThreads / kWave][kAttnMaxG];
-  __shared__ float opart[kAttnThreads / kWave][kAttnMaxG][kAttnD];
+  __shared__ float sc[G][kAttnChunk];                               // scaled scores (log2 units)
+  __shared__ float opart[kAttnThreads / kWave][G][kAttnD];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int s = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads, kvh = blockIdx.y - (blockIdx.y / a.kv_heads) * a.kv_heads;
-  const int G = a.G;
   const int len = min(max(a.seq_used[b], 0), a.max_len);
   const int key0 = s * kAttnChunk;
   const int kl = lane >> 4, ch = lane & 15;   // key within a step of 4, 8-element chunk
+  constexpr int kSteps = kAttnChunk / (kAttnThreads / kWave) / 4;   // 4-key steps per wave
 
-  // this lane's 8 query values of each head of the group
-  float qv[kAttnMaxG][8];
+  // ---- every load of the workgroup is issued up front: q, then all K and V
+  //      rows of this wave's keys (keys past the valid length are not read)
+  u32x4 qw[G];
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
-      const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8;
-      unpack8<XT>(*reinterpret_cast<const u32x4*>(qp), qv[g]);
-    }
-  }
-
+  for (int g = 0; g < G; ++g)
+    qw[g] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8);
   const int64_t kv_base = (int64_t)b * a.kv_sb + (int64_t)kvh * a.kv_sh + ch * 8;
-  // ---- QK: wave covers keys key0 + wave*64 + 4*i + kl
-#pragma unroll 4
-  for (int i = 0; i < 16; ++i) {
-    const int kloc = wave * 64 + 4 * i + kl;
-    const int key = key0 + kloc;
-    const bool valid = key < len;
-    u32x4 kw = u32x4{0, 0, 0, 0};
-    if (valid) kw = *reinterpret_cast<const u32x4*>(a.k + kv_base + (int64_t)key * a.kv_sl);
+  u32x4 kw[kSteps], vw[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
+    kw[i] = vw[i] = u32x4{0, 0, 0, 0};
+    if (key < len) {
+      kw[i] = *reinterpret_cast<const u32x4*>(a.k + kv_base + (int64_t)key * a.kv_sl);
+      vw[i] = *reinterpret_cast<const u32x4*>(a.v + kv_base + (int64_t)key * a.kv_sl);
+    }
+  }
+  float qv[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) unpack8<XT>(qw[g], qv[g]);
+
+  // ---- QK: 16 lanes per key row, partial dots summed across the row with DPP
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int kloc = wave * (4 * kSteps) + 4 * i + kl;
+    const bool valid = key0 + kloc < len;
     float kf[8];
-    unpack8<XT>(kw, kf);
+    unpack8<XT>(kw[i], kf);
 #pragma unroll
-    for (int g = 0; g < kAttnMaxG; ++g) {
-      if (g < G) {
-        float d = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      float d = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
-        d = row16_sum(d);
-        if (ch == 0) sc[g][kloc] = valid ? d * a.scale_log2 : -INFINITY;
-      }
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
+      d = row16_sum(d);
+      if (ch == 0) sc[g][kloc] = valid ? d * a.scale_log2 : -INFINITY;
     }
   }
   __syncthreads();
 
-  // ---- softmax over the chunk: thread t owns key t
-  float mloc[kAttnMaxG], lsum[kAttnMaxG];
+  // ---- softmax statistics of the chunk, computed redundantly by every wave
+  //      (no further barrier): each lane reads kAttnChunk / 64 scores per head
+  float mloc[G], lsum[G];
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
-      float m = sc[g][t];
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-      if (lane == 0) wred[wave][g] = m;
-    }
-  }
-  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
-      float m = wred[0][g];
-      for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, wred[w][g]);
-      mloc[g] = m;
-    }
-  }
-  __syncthreads();   // wred is reused for the sums
+    for (int j = 0; j < kAttnChunk / kWave; ++j) m = fmaxf(m, sc[g][lane + 64 * j]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float l = 0.0f;
+    if (m != -INFINITY) {
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
-      const float p = (mloc[g] == -INFINITY) ? 0.0f : exp2f(sc[g][t] - mloc[g]);
-      sc[g][t] = p;
-      float l = p;
-      for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-      if (lane == 0) wred[wave][g] = l;
+      for (int j = 0; j < kAttnChunk / kWave; ++j) l += exp2f(sc[g][lane + 64 * j] - m);
     }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
-      float l = wred[0][g];
-      for (int w = 1; w < kAttnThreads / kWave; ++w) l += wred[w][g];
-      lsum[g] = l;
-    }
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+    mloc[g] = m;
+    lsum[g] = l;
   }
 
-  // ---- PV: same lane mapping, accumulate G heads x 8 dims per lane
-  float o[kAttnMaxG][8];
+  // ---- PV with the probabilities recomputed from the scores
+  float o[G][8];
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < 16; ++i) {
-    const int kloc = wave * 64 + 4 * i + kl;
-    const int key = key0 + kloc;
-    u32x4 vw = u32x4{0, 0, 0, 0};
-    if (key < len) vw = *reinterpret_cast<const u32x4*>(a.v + kv_base + (int64_t)key * a.kv_sl);
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int kloc = wave * (4 * kSteps) + 4 * i + kl;
     float vf[8];
-    unpack8<XT>(vw, vf);
+    unpack8<XT>(vw[i], vf);
 #pragma unroll
-    for (int g = 0; g < kAttnMaxG; ++g) {
-      if (g < G) {
-        const float p = sc[g][kloc];
+    for (int g = 0; g < G; ++g) {
+      const float p = mloc[g] == -INFINITY ? 0.0f : exp2f(sc[g][kloc] - mloc[g]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vf[e], o[g][e]);
-      }
+      for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vf[e], o[g][e]);
     }
   }
   // reduce the 4 keys-per-step lanes (lane, lane^16, lane^32, lane^48) in a fixed order
 #pragma unroll
-  for (int g = 0; g < kAttnMaxG; ++g) {
-    if (g < G) {
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = o[g][e];
-        x += __shfl_xor(x, 16);
-        x += __shfl_xor(x, 32);
-        if (kl == 0) opart[wave][g][ch * 8 + e] = x;
-      }
+    for (int e = 0; e < 8; ++e) {
+      float x = o[g][e];
+      x += __shfl_xor(x, 16);
+      x += __shfl_xor(x, 32);
+      if (kl == 0) opart[wave][g][ch * 8 + e] = x;
     }
-  }
   __syncthreads();
   // partial record per query head: o[D], m, l (m in log2 units of the scaled score)
   for (int e = t; e < G * kAttnD; e += kAttnThreads) {
     const int g = e / kAttnD, d = e - g * kAttnD;
     float x = opart[0][g][d];
+#pragma unroll
     for (int w = 1; w < kAttnThreads / kWave; ++w) x += opart[w][g][d];
-    const int h = kvh * G + g;
-    float* rec = a.part + ((int64_t)(b * a.q_heads + h) * a.n_splits + s) * (kAttnD + 2);
+    float* rec = a.part + ((int64_t)(b * a.q_heads + kvh * G + g) * a.n_splits + s) * (kAttnD + 2);
     rec[d] = x;
     if (d == 0) {
       rec[kAttnD] = mloc[g];
@@ -203,28 +181,116 @@ attn_split_kernel(AttnArgs a) {
   }
 }
 
+// Merge of the split partials of one (b, h) for dimension d: online over
+// batches of kMergeBatch splits, every load of a batch issued before its
+// first use.  With at most kMergeBatch splits this is the plain two-pass
+// formula (global max, then the weighted sums in split order).
+constexpr int kMergeBatch = 16;
+
+__device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d) {
+  float M = -INFINITY, L = 0.0f, acc = 0.0f;
+  for (int s0 = 0; s0 < a.n_splits; s0 += kMergeBatch) {
+    float m[kMergeBatch], l[kMergeBatch], o[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const int sj = min(s0 + j, a.n_splits - 1);
+      const float* r = rec + (int64_t)sj * (kAttnD + 2);
+      m[j] = r[kAttnD];
+      l[j] = r[kAttnD + 1];
+      o[j] = r[d];
+      if (s0 + j >= a.n_splits) m[j] = -INFINITY;
+    }
+    float Mb = M;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, m[j]);
+    if (Mb == -INFINITY) continue;
+    const float r = exp2f(M - Mb);   // 0 while nothing has been accumulated (M = -inf)
+    L *= r;
+    acc *= r;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      if (m[j] == -INFINITY) continue;
+      const float w = exp2f(m[j] - Mb);
+      L = fmaf(w, l[j], L);
+      acc = fmaf(w, o[j], acc);
+    }
+    M = Mb;
+  }
+  return L > 0.0f ? acc / L : 0.0f;
+}
+
 template <class XT>
 __global__ void __launch_bounds__(kAttnD)
 attn_merge_kernel(AttnArgs a) {
   const int bh = blockIdx.x, d = threadIdx.x;
   const int b = bh / a.q_heads, h = bh - (bh / a.q_heads) * a.q_heads;
   const float* rec = a.part + (int64_t)bh * a.n_splits * (kAttnD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, rec[(int64_t)s * (kAttnD + 2) + kAttnD]);
-  float L = 0.0f, acc = 0.0f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const float* r = rec + (int64_t)s * (kAttnD + 2);
-    const float m = r[kAttnD];
-    if (m == -INFINITY) continue;
-    const float w = exp2f(m - M);
-    L = fmaf(w, r[kAttnD + 1], L);
-    acc = fmaf(w, r[d], acc);
+  a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(merge_splits(a, rec, d));
+}
+
+// Merge + INT8 quantization of the attention output for the next projection:
+// workgroup h = query head h for ALL batch rows (b < batch <= 16), 4 row
+// groups x 128 dimensions.  Dimensions 0..63 / 64..127 of the head are column
+// tiles 2h / 2h + 1 of the [batch, q_heads * 128] projection input, so both
+// tiles are whole inside the workgroup: absmax over the batch rows, scale,
+// codes -- the closed form of tq_act_quant, bit for bit.
+constexpr int kMergeQuantMaxRows = 16;
+constexpr int kMergeQuantThreads = 512;   // 4 row groups x 128 dimensions
+
+template <class XT>
+__global__ void __launch_bounds__(kMergeQuantThreads)
+attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
+  __shared__ float red[kMergeQuantThreads / kWave];
+  const int h = blockIdx.x, t = threadIdx.x, d = t & (kAttnD - 1), rg = t / kAttnD;   // row group rg
+  constexpr int kGroups = kMergeQuantThreads / kAttnD;
+  constexpr int kPer = kMergeQuantMaxRows / kGroups;
+  float y[kPer];
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = rg + kGroups * i;
+    y[i] = 0.0f;
+    if (b < a.batch) {
+      const float* rec = a.part + (int64_t)(b * a.q_heads + h) * a.n_splits * (kAttnD + 2);
+      const uint16_t o = XT::from_f32(merge_splits(a, rec, d));
+      a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = o;
+      y[i] = XT::to_f32(o);
+      am = fmaxf(am, fabsf(y[i]));
+    }
   }
-  const float y = L > 0.0f ? acc / L : 0.0f;
-  a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(y);
+  // column tile 2h + (d >= 64): waves with the same parity hold the same half
+  const float wm = wave_max_nonneg(am);
+  const int wave = t >> 6, lane = t & 63;
+  if (lane == 0) red[wave] = wm;
+  __syncthreads();
+  float tm = 0.0f;
+  for (int w = (wave & 1); w < kMergeQuantThreads / kWave; w += 2) tm = fmaxf(tm, red[w]);
+  const float s = act_scale_from_absmax<XT>(tm);
+  const CodeScale cs(s);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = rg + kGroups * i;
+    if (b < a.batch) q[(int64_t)b * ldq + h * kAttnD + d] = (int8_t)cs.code(y[i]);
+  }
+  if (t < kAttnD && (d & 63) == 0) sx[2 * h + (d >> 6)] = s;
 }
 
 static int attn_splits(int max_len) { return (max_len + kAttnChunk - 1) / kAttnChunk; }
+
+template <class XT>
+static void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(kAttnThreads);
+  switch (a.G) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<XT, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<XT, 2>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((attn_split_kernel<XT, 3>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<XT, 4>), grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((attn_split_kernel<XT, 5>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((attn_split_kernel<XT, 6>), grid, block, 0, s, a); break;
+    case 7: hipLaunchKernelGGL((attn_split_kernel<XT, 7>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<XT, 8>), grid, block, 0, s, a); break;
+  }
+}
 
 }  // namespace tq
 
@@ -235,12 +301,11 @@ extern "C" int64_t tq_decode_attention_workspace_elems(int batch, int q_heads, i
   return (int64_t)batch * q_heads * attn_splits(max_len) * (kAttnD + 2);
 }
 
-extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
-                                   const void* v, int64_t kv_stride_b, int64_t kv_stride_l,
-                                   int64_t kv_stride_h, const int32_t* seq_used, void* out,
-                                   int64_t out_stride_b, int64_t out_stride_h, int dtype, int batch,
-                                   int q_heads, int kv_heads, int head_dim, int max_len, float scale,
-                                   float* workspace, int64_t workspace_elems, void* stream) {
+static int attn_setup(AttnArgs& a, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                      const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
+                      const int32_t* seq_used, void* out, int64_t out_stride_b, int64_t out_stride_h, int dtype,
+                      int batch, int q_heads, int kv_heads, int head_dim, int max_len, float scale,
+                      float* workspace, int64_t workspace_elems) {
   if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || max_len < 0) return TQ_ERR_ARG;
   if (head_dim != kAttnD || q_heads % kv_heads != 0 || q_heads / kv_heads > kAttnMaxG) return TQ_ERR_ARG;
@@ -251,7 +316,6 @@ extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
     return TQ_ERR_ALIGN;
   if (workspace == nullptr || workspace_elems < tq_decode_attention_workspace_elems(batch, q_heads, max_len))
     return TQ_ERR_WORKSPACE;
-  AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
   a.k = static_cast<const uint16_t*>(k); a.v = static_cast<const uint16_t*>(v);
   a.kv_sb = kv_stride_b; a.kv_sl = kv_stride_l; a.kv_sh = kv_stride_h;
@@ -261,14 +325,53 @@ extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
   a.batch = batch; a.q_heads = q_heads; a.kv_heads = kv_heads; a.G = q_heads / kv_heads;
   a.max_len = max_len; a.n_splits = attn_splits(max_len);
   a.scale_log2 = scale * kLog2e;
+  return 1;   // ready to launch
+}
+
+extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                                   const void* v, int64_t kv_stride_b, int64_t kv_stride_l,
+                                   int64_t kv_stride_h, const int32_t* seq_used, void* out,
+                                   int64_t out_stride_b, int64_t out_stride_h, int dtype, int batch,
+                                   int q_heads, int kv_heads, int head_dim, int max_len, float scale,
+                                   float* workspace, int64_t workspace_elems, void* stream) {
+  AttnArgs a{};
+  const int rc = attn_setup(a, q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_l, kv_stride_h, seq_used,
+                            out, out_stride_b, out_stride_h, dtype, batch, q_heads, kv_heads, head_dim, max_len,
+                            scale, workspace, workspace_elems);
+  if (rc != 1) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 g1(a.n_splits, batch * kv_heads), g2(batch * q_heads);
   if (dtype == TQ_DTYPE_BF16) {
-    hipLaunchKernelGGL(attn_split_kernel<Bf16>, g1, dim3(kAttnThreads), 0, s, a);
+    launch_split<Bf16>(a, g1, s);
     hipLaunchKernelGGL(attn_merge_kernel<Bf16>, g2, dim3(kAttnD), 0, s, a);
   } else {
-    hipLaunchKernelGGL(attn_split_kernel<Fp16>, g1, dim3(kAttnThreads), 0, s, a);
+    launch_split<Fp16>(a, g1, s);
     hipLaunchKernelGGL(attn_merge_kernel<Fp16>, g2, dim3(kAttnD), 0, s, a);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                                         const void* v, int64_t kv_stride_b, int64_t kv_stride_l,
+                                         int64_t kv_stride_h, const int32_t* seq_used, void* out,
+                                         int64_t out_stride_b, int64_t out_stride_h, int8_t* q_out,
+                                         int64_t q_out_stride_b, float* sx_out, int dtype, int batch, int q_heads,
+                                         int kv_heads, int head_dim, int max_len, float scale, float* workspace,
+                                         int64_t workspace_elems, void* stream) {
+  if (batch > kMergeQuantMaxRows || (batch > 0 && (!q_out || !sx_out))) return TQ_ERR_ARG;
+  AttnArgs a{};
+  const int rc = attn_setup(a, q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_l, kv_stride_h, seq_used,
+                            out, out_stride_b, out_stride_h, dtype, batch, q_heads, kv_heads, head_dim, max_len,
+                            scale, workspace, workspace_elems);
+  if (rc != 1) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g1(a.n_splits, batch * kv_heads), g2(q_heads);
+  if (dtype == TQ_DTYPE_BF16) {
+    launch_split<Bf16>(a, g1, s);
+    hipLaunchKernelGGL(attn_merge_quant_kernel<Bf16>, g2, dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+  } else {
+    launch_split<Fp16>(a, g1, s);
+    hipLaunchKernelGGL(attn_merge_quant_kernel<Fp16>, g2, dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
   }
   return (int)hipGetLastError();
 }

@@ -1,0 +1,283 @@
+// tq_fused.hip -- decode-step glue kernels that feed the mixed tile GEMMs
+// their INT8 activations directly, for gfx950.
+//
+// A Llama / Qwen2 decoder layer at decode runs, between its GEMMs, a residual
+// add, an RMSNorm, RoPE, a KV-cache write, SiLU * up, and the activation
+// quantization of every GEMM input -- each a separate small launch in the
+// Hugging Face modules.  These kernels do each producer and the quantization
+// of its output in one launch:
+//   add_rmsnorm_quant  h = x + delta (rounded to the 16-bit type), y = w * rmsnorm(h),
+//                      and y's per-64-column-tile INT8 codes and scales;
+//   silu_mul_quant     y = silu(gate) * up of a stacked gate/up output, and its codes;
+//   rope_cache         RoPE on the q/k heads of a stacked q/k/v output, k and v
+//                      written into the static cache at the device-held position.
+// Rounding follows the module code op by op (every intermediate the modules
+// materialise in the 16-bit type is rounded to it here too); only the order
+// of the fp32 sum of squares differs.  The quantization is the closed form of
+// tq_act_quant (scale over ALL rows of the call), bit for bit.
+//
+// Quantizing kernels run one workgroup per 64-column tile, so the tile's
+// absmax over all rows is local to the workgroup.
+#include "tq_common.h"
+
+namespace tq {
+
+constexpr int kFuseThreads = 256;
+
+// Max over the workgroup of a non-negative value (all threads receive it).
+__device__ inline float wg_max_nonneg(float v, float* red) {
+  v = wave_max_nonneg(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// Sum over a wave (every lane receives it), fixed xor-butterfly order.
+__device__ inline float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+struct NormArgs {
+  const uint16_t* x;      // [n, k], row stride ldx
+  const uint16_t* delta;  // nullable, row stride ldd
+  const uint16_t* w;      // [k]
+  uint16_t* h;            // nullable: h = x + delta, row stride ldh
+  uint16_t* y;            // [n, k], row stride ldy
+  int8_t* q;              // nullable: codes [n, k], row stride ldq
+  float* sx;              // [n_tc] when q
+  int64_t ldx, ldd, ldh, ldy, ldq;
+  int n, k;
+  float eps;
+};
+
+// workgroup c: every row's sum of squares over all k columns (each wave takes
+// rows wave, wave + 4, ...), then the 64 columns of tile c for every row.
+template <class XT>
+__global__ void __launch_bounds__(kFuseThreads)
+add_rmsnorm_quant_kernel(NormArgs a) {
+  __shared__ float rinv[64];          // 1 / sqrt(mean(h^2) + eps) per row (n <= 64)
+  __shared__ float red[kFuseThreads / kWave];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int c = blockIdx.x;
+  const int cpr = a.k >> 3;           // 8-element chunks per row
+  // Passes of kNormBatch chunks per lane: all loads of a pass are issued
+  // before the first use (one memory round trip per pass, not per chunk).
+  constexpr int kNormBatch = 8;
+  for (int row = wave; row < a.n; row += kFuseThreads / kWave) {
+    float ss = 0.0f;
+    for (int c0 = 0; c0 < cpr; c0 += kNormBatch * kWave) {
+      u32x4 xv[kNormBatch], dv[kNormBatch];
+#pragma unroll
+      for (int j = 0; j < kNormBatch; ++j) {
+        const int ch = min(c0 + j * kWave + lane, cpr - 1);
+        xv[j] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.ldx + ch * 8);
+        dv[j] = u32x4{0, 0, 0, 0};
+        if (a.delta) dv[j] = *reinterpret_cast<const u32x4*>(a.delta + (int64_t)row * a.ldd + ch * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < kNormBatch; ++j) {
+        if (c0 + j * kWave + lane >= cpr) continue;   // clamped duplicate: not summed
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float hv = XT::to_f32((uint16_t)(xv[j][i >> 1] >> (16 * (i & 1))));
+          if (a.delta) hv = XT::round(hv + XT::to_f32((uint16_t)(dv[j][i >> 1] >> (16 * (i & 1)))));
+          ss = fmaf(hv, hv, ss);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) rinv[row] = rsqrtf(ss / (float)a.k + a.eps);
+  }
+  __syncthreads();
+  // tile c: thread t -> row t / 64 (+4 per pass), column c*64 + t%64
+  const int col = c * 64 + lane;
+  float am = 0.0f;
+  float yv[16];
+  const float wv = XT::to_f32(a.w[col]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = wave + 4 * i;
+    yv[i] = 0.0f;
+    if (row < a.n) {
+      float hv = XT::to_f32(a.x[(int64_t)row * a.ldx + col]);
+      if (a.delta) {
+        hv = XT::round(hv + XT::to_f32(a.delta[(int64_t)row * a.ldd + col]));
+        if (a.h) a.h[(int64_t)row * a.ldh + col] = XT::from_f32(hv);
+      }
+      const float nrm = XT::round(hv * rinv[row]);   // hidden_states.to(input_dtype)
+      const float y = XT::round(wv * nrm);           // weight * hidden_states
+      a.y[(int64_t)row * a.ldy + col] = XT::from_f32(y);
+      yv[i] = y;
+      am = fmaxf(am, fabsf(y));
+    }
+  }
+  if (a.q == nullptr) return;
+  const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
+  const CodeScale cs(s);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = wave + 4 * i;
+    if (row < a.n) a.q[(int64_t)row * a.ldq + col] = (int8_t)cs.code(yv[i]);
+  }
+  if (t == 0) a.sx[c] = s;
+}
+
+struct SiluArgs {
+  const uint16_t* gu;   // [n, 2 * inter]: gate columns [0, inter), up [inter, 2 inter)
+  uint16_t* y;          // [n, inter]
+  int8_t* q;            // nullable codes [n, inter]
+  float* sx;
+  int64_t ldg, ldy, ldq;
+  int n, inter;
+};
+
+// y = silu(gate) * up with the module's roundings: silu in fp32 rounded to the
+// 16-bit type, the product rounded again.  Workgroup c = 64-column tile c.
+template <class XT>
+__global__ void __launch_bounds__(kFuseThreads)
+silu_mul_quant_kernel(SiluArgs a) {
+  __shared__ float red[kFuseThreads / kWave];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float am = 0.0f;
+  float yv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = wave + 4 * i;
+    yv[i] = 0.0f;
+    if (row < a.n) {
+      const float g = XT::to_f32(a.gu[(int64_t)row * a.ldg + col]);
+      const float u = XT::to_f32(a.gu[(int64_t)row * a.ldg + a.inter + col]);
+      const float sg = XT::round(g / (1.0f + expf(-g)));
+      const float y = XT::round(sg * u);
+      a.y[(int64_t)row * a.ldy + col] = XT::from_f32(y);
+      yv[i] = y;
+      am = fmaxf(am, fabsf(y));
+    }
+  }
+  if (a.q == nullptr) return;
+  const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
+  const CodeScale cs(s);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = wave + 4 * i;
+    if (row < a.n) a.q[(int64_t)row * a.ldq + col] = (int8_t)cs.code(yv[i]);
+  }
+  if (t == 0) a.sx[blockIdx.x] = s;
+}
+
+struct RopeArgs {
+  const uint16_t* qkv;   // [n, (hq + 2 hkv) * 128], row stride ldqkv
+  const uint16_t* cos;   // [128] at the decode position
+  const uint16_t* sin;
+  const int64_t* pos;    // device position (cache index)
+  uint16_t* q_out;       // [n, hq, 128] rotated queries, strides q_sb, q_sh
+  uint16_t* k_cache;     // [n, hkv, L, 128] with strides c_sb, c_sh, c_sl (shared by v)
+  uint16_t* v_cache;
+  int64_t ldqkv, q_sb, q_sh, c_sb, c_sh, c_sl;
+  int n, hq, hkv, max_len;
+};
+
+// Workgroup (row b, head slot j < hq + 2 hkv), 64 threads, lane d rotates the
+// pair (d, d + 64): out[d] = q[d] cos[d] - q[d+64] sin[d],
+// out[d+64] = q[d+64] cos[d+64] + q[d] sin[d+64], each product and the sum
+// rounded to the 16-bit type as the modules do (q * cos + rotate_half(q) * sin).
+template <class XT>
+__global__ void __launch_bounds__(64)
+rope_cache_kernel(RopeArgs a) {
+  const int b = blockIdx.x, j = blockIdx.y, d = threadIdx.x;
+  const int64_t p = a.pos[0];
+  if (p < 0 || p >= a.max_len) return;   // never indexes outside the cache
+  const uint16_t* src = a.qkv + (int64_t)b * a.ldqkv + (int64_t)j * 128;
+  const float lo = XT::to_f32(src[d]), hi = XT::to_f32(src[d + 64]);
+  if (j >= a.hq + a.hkv) {   // v head: copy into the cache
+    uint16_t* dst = a.v_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq - a.hkv) * a.c_sh + p * a.c_sl;
+    dst[d] = src[d];
+    dst[d + 64] = src[d + 64];
+    return;
+  }
+  const float c0 = XT::to_f32(a.cos[d]), c1 = XT::to_f32(a.cos[d + 64]);
+  const float s0 = XT::to_f32(a.sin[d]), s1 = XT::to_f32(a.sin[d + 64]);
+  const float o0 = XT::round(XT::round(lo * c0) + XT::round(-hi * s0));
+  const float o1 = XT::round(XT::round(hi * c1) + XT::round(lo * s1));
+  uint16_t* dst = (j < a.hq) ? a.q_out + (int64_t)b * a.q_sb + (int64_t)j * a.q_sh
+                             : a.k_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq) * a.c_sh + p * a.c_sl;
+  dst[d] = XT::from_f32(o0);
+  dst[d + 64] = XT::from_f32(o1);
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                                    const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out,
+                                    int64_t y_stride, int8_t* q_out, int64_t q_stride, float* sx_out, int dtype,
+                                    int n, int k, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (n < 0 || k < 0 || n > 64 || (k % 64) != 0) return TQ_ERR_ARG;
+  if (n == 0 || k == 0) return TQ_OK;
+  if (!x || !weight || !y_out || (q_out && !sx_out) || (delta && !h_out)) return TQ_ERR_ARG;
+  if (!al16(x) || (x_stride % 8) || (delta && (!al16(delta) || (delta_stride % 8)))) return TQ_ERR_ALIGN;
+  NormArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.delta = static_cast<const uint16_t*>(delta);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.h = static_cast<uint16_t*>(h_out); a.y = static_cast<uint16_t*>(y_out); a.q = q_out; a.sx = sx_out;
+  a.ldx = x_stride; a.ldd = delta_stride; a.ldh = h_stride; a.ldy = y_stride; a.ldq = q_stride;
+  a.n = n; a.k = k; a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Bf16>, dim3(k / 64), dim3(kFuseThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Fp16>, dim3(k / 64), dim3(kFuseThreads), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride,
+                                 int8_t* q_out, int64_t q_stride, float* sx_out, int dtype, int n, int inter,
+                                 void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (n < 0 || inter < 0 || n > 64 || (inter % 64) != 0) return TQ_ERR_ARG;
+  if (n == 0 || inter == 0) return TQ_OK;
+  if (!gate_up || !y_out || (q_out && !sx_out)) return TQ_ERR_ARG;
+  SiluArgs a{};
+  a.gu = static_cast<const uint16_t*>(gate_up); a.y = static_cast<uint16_t*>(y_out); a.q = q_out; a.sx = sx_out;
+  a.ldg = gu_stride; a.ldy = y_stride; a.ldq = q_stride; a.n = n; a.inter = inter;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(silu_mul_quant_kernel<Bf16>, dim3(inter / 64), dim3(kFuseThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(silu_mul_quant_kernel<Fp16>, dim3(inter / 64), dim3(kFuseThreads), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+                             const int64_t* position, void* q_out, int64_t q_stride_b, int64_t q_stride_h,
+                             void* k_cache, void* v_cache, int64_t cache_stride_b, int64_t cache_stride_h,
+                             int64_t cache_stride_l, int dtype, int n, int q_heads, int kv_heads, int head_dim,
+                             int max_len, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (head_dim != 128 || n < 0 || q_heads <= 0 || kv_heads <= 0 || max_len <= 0) return TQ_ERR_ARG;
+  if (n == 0) return TQ_OK;
+  if (!qkv || !cos || !sin || !position || !q_out || !k_cache || !v_cache) return TQ_ERR_ARG;
+  RopeArgs a{};
+  a.qkv = static_cast<const uint16_t*>(qkv); a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin); a.pos = position;
+  a.q_out = static_cast<uint16_t*>(q_out); a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.ldqkv = qkv_stride; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
+  a.c_sb = cache_stride_b; a.c_sh = cache_stride_h; a.c_sl = cache_stride_l;
+  a.n = n; a.hq = q_heads; a.hkv = kv_heads; a.max_len = max_len;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(n, q_heads + 2 * kv_heads);
+  if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(rope_cache_kernel<Bf16>, grid, dim3(64), 0, s, a);
+  else hipLaunchKernelGGL(rope_cache_kernel<Fp16>, grid, dim3(64), 0, s, a);
+  return (int)hipGetLastError();
+}

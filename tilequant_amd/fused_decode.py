@@ -1,0 +1,200 @@
+"""One-token decode step of a Llama / Qwen2 model from fused kernels.
+
+``FusedDecodeStep`` computes what the model's own forward computes for one
+new token per sequence over a ``StaticCache`` -- embedding, 28-ish decoder
+layers, final norm, LM head -- with per layer:
+
+  add_rmsnorm_quant  residual add + input RMSNorm + INT8 codes of the result
+  QKV GEMM           stacked Q/K/V MixedLinear on the codes (or F.linear)
+  rope_cache         RoPE on q/k, k/v written into the cache at the position
+  decode attention   split kernel + merge that also quantizes for O
+  O GEMM
+  add_rmsnorm_quant  residual add + post-attention RMSNorm + codes
+  Gate/Up GEMM       stacked
+  silu_mul_quant     SiLU(gate) * up + codes
+  Down GEMM
+
+i.e. 10 launches per layer where the modules issue ~40 (norm, RoPE, cache
+update, residual and activation elementwise kernels, one quantization per
+GEMM).  The arithmetic follows the modules op by op (see csrc/tq_fused.hip);
+the GEMMs are exactly the MixedLinear kernels on exactly the activation
+codes MixedLinear would compute.  Dense ``nn.Linear`` projections (the bf16
+baseline) run through ``F.linear`` on stacked weights, with the same fused
+glue, so both models are timed with the same non-GEMM work.
+
+This is the decode-latency step of the ranked "fewer launches per layer" item
+of the reference's hot path (activation quantization fused into its producer,
+src/models/mixed_linear.py:233-239 -> quant_utils.py:119-134); the reference
+runs the Hugging Face modules inside its captured decode graph
+(src/runtime/graph_decode.py:350-385).
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _native as nat
+from .attention import decode_attention_workspace
+from .gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+from .mixed_linear import MixedLinear
+
+
+def _stacked(parent: nn.Module, group_attr: str, names) -> nn.Module:
+    """The stacked projection of a group: a MixedLinear (grouped by
+    fuse_projection_groups) or a dense nn.Linear built from the members."""
+    group = getattr(parent, group_attr, None)
+    if group is not None:
+        return group.linear
+    members = [getattr(parent, n) for n in names]
+    if not all(isinstance(m, nn.Linear) for m in members):
+        raise ValueError(f"cannot stack {names}: expected a projection group or nn.Linear members")
+    w = torch.cat([m.weight.detach() for m in members], dim=0)
+    lin = nn.Linear(w.shape[1], w.shape[0], bias=members[0].bias is not None, device=w.device, dtype=w.dtype)
+    lin.weight = nn.Parameter(w, requires_grad=False)
+    if lin.bias is not None:
+        lin.bias = nn.Parameter(torch.cat([m.bias.detach() for m in members]), requires_grad=False)
+    return lin
+
+
+class _Layer:
+    def __init__(self, layer: nn.Module) -> None:
+        attn, mlp = layer.self_attn, layer.mlp
+        self.qkv = _stacked(attn, "tilequant_qkv", ("q_proj", "k_proj", "v_proj"))
+        self.o = attn.o_proj
+        self.gate_up = _stacked(mlp, "tilequant_gate_up", ("gate_proj", "up_proj"))
+        self.down = mlp.down_proj
+        self.ln1, self.ln2 = layer.input_layernorm, layer.post_attention_layernorm
+        act = getattr(getattr(mlp, "config", None), "hidden_act", "silu")
+        if act not in ("silu", "swish"):
+            raise ValueError(f"fused decode supports SiLU MLPs, got {act}")
+
+
+class FusedDecodeStep:
+    """Decode forward for a bound model and static cache (batch fixed)."""
+
+    def __init__(self, model: nn.Module, cache, batch: int, max_cache_len: int, device: torch.device) -> None:
+        cfg = model.config.get_text_config(decoder=True)
+        self.model = model
+        self.text = model.model
+        self.cache = cache
+        self.B = int(batch)
+        self.L = int(max_cache_len)
+        self.device = device
+        self.hidden = int(cfg.hidden_size)
+        self.hq, self.hkv = int(cfg.num_attention_heads), int(cfg.num_key_value_heads)
+        self.head_dim = int(getattr(cfg, "head_dim", None) or self.hidden // self.hq)
+        if self.head_dim != 128:
+            raise ValueError("fused decode serves head_dim 128")
+        if self.B > 16:
+            raise ValueError("fused decode serves at most 16 sequences")
+        self.inter = int(cfg.intermediate_size)
+        self.layers: List[_Layer] = [_Layer(l) for l in self.text.layers]
+        self.dtype = self.text.embed_tokens.weight.dtype
+        self.code = nat.dtype_code(self.dtype)
+        self.scale = float(self.text.layers[0].self_attn.scaling)
+        B, H, dt, dev = self.B, self.hidden, self.dtype, device
+        qkv_w = (self.hq + 2 * self.hkv) * self.head_dim
+        e = lambda *s, d=dt: torch.empty(s, device=dev, dtype=d)   # noqa: E731
+        # static activations (graph-stable addresses)
+        self.h = [e(B, H), e(B, H)]            # residual stream, ping-pong
+        self.y = e(B, H)
+        self.yq, self.ysx = e(B, H, d=torch.int8), e(H // 64, d=torch.float32)
+        self.qkv_out = e(B, qkv_w)
+        self.q_rot = e(B, self.hq, self.head_dim)
+        self.attn = e(B, self.hq * self.head_dim)
+        self.aq = e(B, self.hq * self.head_dim, d=torch.int8)
+        self.asx = e(self.hq * self.head_dim // 64, d=torch.float32)
+        self.o_out = e(B, H)
+        self.gu = e(B, 2 * self.inter)
+        self.m = e(B, self.inter)
+        self.mq, self.msx = e(B, self.inter, d=torch.int8), e(self.inter // 64, d=torch.float32)
+        self.d_out = e(B, H)
+        self.final = e(B, H)
+        self.attn_ws = decode_attention_workspace(B, self.hq, self.L, dev)
+
+    # -- kernels -------------------------------------------------------------
+    def _norm(self, x, delta, ln, h_out, y_out, q_out, sx_out) -> None:
+        rc = nat.lib().tq_add_rmsnorm_quant(
+            nat.ptr(x), x.stride(0), nat.ptr(delta), delta.stride(0) if delta is not None else 0,
+            nat.ptr(ln.weight), float(ln.variance_epsilon), nat.ptr(h_out), h_out.stride(0) if h_out is not None else 0,
+            nat.ptr(y_out), y_out.stride(0), nat.ptr(q_out), q_out.stride(0) if q_out is not None else 0,
+            nat.ptr(sx_out), self.code, self.B, self.hidden, nat.stream_handle(self.device))
+        nat.check(rc, "tq_add_rmsnorm_quant")
+
+    def _linear(self, lin: nn.Module, x, xq, sx, out) -> None:
+        if isinstance(lin, MixedLinear):
+            gemm_mixed_rows_splitk(x_fp=x, x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles, int8_scales=lin.int8_scales,
+                                   int8_tile_ids=lin.int8_tile_ids, int8_row_ptr=lin.int8_row_ptr,
+                                   fp16_tiles=lin.fp16_tiles, fp16_tile_ids=lin.fp16_tile_ids,
+                                   fp16_row_ptr=lin.fp16_row_ptr, M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr,
+                                   n_tc=lin.n_tc, out_dtype=out.dtype, bias=lin._out_bias(out.dtype), out=out,
+                                   tile_layout=lin.tile_layout)
+        else:
+            torch.matmul(x, lin.weight.t(), out=out)
+            if lin.bias is not None:
+                out.add_(lin.bias)
+
+    @staticmethod
+    def _quantized(lin: nn.Module) -> bool:
+        return isinstance(lin, MixedLinear)
+
+    # -- step -----------------------------------------------------------------
+    @torch.inference_mode()
+    def __call__(self, token: torch.Tensor, position: torch.Tensor, seq_used: torch.Tensor) -> torch.Tensor:
+        """token [B, 1] int64, position [1] int64 (cache index of the token),
+        seq_used [B] int32 (= position + 1).  Returns logits [B, 1, V]."""
+        B, dev = self.B, self.device
+        stream = nat.stream_handle(dev)
+        x = self.text.embed_tokens(token).view(B, self.hidden)
+        cos, sin = self.text.rotary_emb(x.view(B, 1, self.hidden), position.view(1, 1))
+        cos, sin = cos.reshape(-1), sin.reshape(-1)
+        cur, delta = x, None
+        k = 0
+        for li, ly in enumerate(self.layers):
+            h_new = self.h[k]
+            q8 = self._quantized(ly.qkv)
+            self._norm(cur, delta, ly.ln1, h_new if delta is not None else None, self.y,
+                       self.yq if q8 else None, self.ysx if q8 else None)
+            resid = h_new if delta is not None else cur
+            self._linear(ly.qkv, self.y, self.yq, self.ysx, self.qkv_out)
+            layer_cache = self.cache.layers[li]
+            kc, vc = layer_cache.keys, layer_cache.values
+            rc = nat.lib().tq_rope_cache(
+                nat.ptr(self.qkv_out), self.qkv_out.stride(0), nat.ptr(cos), nat.ptr(sin), nat.ptr(position),
+                nat.ptr(self.q_rot), self.q_rot.stride(0), self.q_rot.stride(1), nat.ptr(kc), nat.ptr(vc),
+                kc.stride(0), kc.stride(1), kc.stride(2), self.code, B, self.hq, self.hkv, self.head_dim, self.L,
+                stream)
+            nat.check(rc, "tq_rope_cache")
+            q8o = self._quantized(ly.o)
+            args = (nat.ptr(self.q_rot), self.q_rot.stride(0), self.q_rot.stride(1), nat.ptr(kc), nat.ptr(vc),
+                    kc.stride(0), kc.stride(2), kc.stride(1), nat.ptr(seq_used), nat.ptr(self.attn),
+                    self.attn.stride(0), self.head_dim)
+            tail = (self.code, B, self.hq, self.hkv, self.head_dim, self.L, self.scale, nat.ptr(self.attn_ws),
+                    self.attn_ws.numel(), stream)
+            if q8o:
+                rc = nat.lib().tq_decode_attention_quant(*args, nat.ptr(self.aq), self.aq.stride(0),
+                                                         nat.ptr(self.asx), *tail)
+            else:
+                rc = nat.lib().tq_decode_attention(*args, *tail)
+            nat.check(rc, "tq_decode_attention")
+            self._linear(ly.o, self.attn, self.aq, self.asx, self.o_out)
+            k ^= 1
+            h2 = self.h[k]
+            q8g = self._quantized(ly.gate_up)
+            self._norm(resid, self.o_out, ly.ln2, h2, self.y, self.yq if q8g else None, self.ysx if q8g else None)
+            self._linear(ly.gate_up, self.y, self.yq, self.ysx, self.gu)
+            q8d = self._quantized(ly.down)
+            rc = nat.lib().tq_silu_mul_quant(nat.ptr(self.gu), self.gu.stride(0), nat.ptr(self.m), self.m.stride(0),
+                                             nat.ptr(self.mq) if q8d else None, self.mq.stride(0),
+                                             nat.ptr(self.msx) if q8d else None, self.code, B, self.inter, stream)
+            nat.check(rc, "tq_silu_mul_quant")
+            self._linear(ly.down, self.m, self.mq, self.msx, self.d_out)
+            cur, delta = h2, self.d_out
+            k ^= 1
+        norm = self.text.norm
+        self._norm(cur, delta, norm, self.h[k], self.final, None, None)
+        logits = self.model.lm_head(self.final.view(B, 1, self.hidden))
+        return logits

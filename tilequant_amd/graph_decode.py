@@ -17,6 +17,12 @@ ROCm specifics (this build's own design):
   token-major re-layout is needed.
 * Prefill attention is SDPA restricted to the fused flash / memory-efficient
   backends (causal, grouped-query); the unfused math backend is never used.
+* The one-token step runs ``FusedDecodeStep`` (10 launches per decoder layer:
+  residual + RMSNorm + INT8 quantization, RoPE + cache write, attention whose
+  merge quantizes for O, SiLU * up + quantization, four GEMMs) for Llama /
+  Qwen2 layouts with head_dim 128 and up to 16 sequences; ``fused_decode=False``
+  (or any other architecture) replays the model's own forward as the reference
+  does.
 * Argmax, token feedback and the position counter stay on the device, as in
   the reference (graph_decode.py:347-385): no scalar leaves the GPU between
   replays.
@@ -115,7 +121,7 @@ class CudaGraphGreedyDecoder:
     prefill graph; ``decode`` replays the one-token graph."""
 
     def __init__(self, model: torch.nn.Module, *, prompt_tokens: int, max_new_tokens: int, batch_size: int = 1,
-                 device="cuda", prefill_only: bool = False) -> None:
+                 device="cuda", prefill_only: bool = False, fused_decode: bool = True) -> None:
         if prompt_tokens < 1:
             raise ValueError("prompt_tokens must be positive")
         if batch_size < 1:
@@ -168,6 +174,16 @@ class CudaGraphGreedyDecoder:
             self._generated = torch.empty((self.batch_size, self.max_new_tokens), dtype=torch.long, device=dev)
             self._decode_seq_used = torch.empty((self.batch_size,), dtype=torch.int32, device=dev)
         self._install_attention_backend()
+        # One-token steps from fused kernels where the architecture allows
+        # (tilequant_amd.fused_decode); otherwise the model's own forward.
+        self._fused = None
+        if fused_decode and not prefill_only:
+            from .fused_decode import FusedDecodeStep
+
+            try:
+                self._fused = FusedDecodeStep(model, self.cache, self.batch_size, self.max_cache_len, self.device)
+            except (ValueError, AttributeError):
+                self._fused = None
         self._prefill_graph: Optional[torch.cuda.CUDAGraph] = None
         self._graph: Optional[torch.cuda.CUDAGraph] = None
         self._prefill_logits: Optional[torch.Tensor] = None
@@ -205,10 +221,11 @@ class CudaGraphGreedyDecoder:
     @classmethod
     @torch.inference_mode()
     def prepare(cls, model: torch.nn.Module, *, prompt_tokens: int = 128, max_new_tokens: int = 512,
-                batch_size: int = 1, device="cuda", prefill_only: bool = False) -> "CudaGraphGreedyDecoder":
+                batch_size: int = 1, device="cuda", prefill_only: bool = False,
+                fused_decode: bool = True) -> "CudaGraphGreedyDecoder":
         """Allocate, warm up and capture the prefill and decode graphs."""
         dec = cls(model, prompt_tokens=prompt_tokens, max_new_tokens=max_new_tokens, batch_size=batch_size,
-                  device=device, prefill_only=prefill_only)
+                  device=device, prefill_only=prefill_only, fused_decode=fused_decode)
         try:
             dec._capture()
         except BaseException:
@@ -263,10 +280,14 @@ class CudaGraphGreedyDecoder:
     def _decode_body(self) -> None:
         self._attention_is_prefill = False
         self._decode_seq_used.copy_(self._position + 1)
-        out = self.model(input_ids=self._token, attention_mask=None, position_ids=self._position.view(1, 1),
-                         past_key_values=self.cache, cache_position=self._position, use_cache=True, logits_to_keep=1)
-        self._decode_logits = out.logits
-        self._next_token.copy_(out.logits.argmax(dim=-1))
+        if self._fused is not None:
+            logits = self._fused(self._token, self._position, self._decode_seq_used)
+        else:
+            logits = self.model(input_ids=self._token, attention_mask=None, position_ids=self._position.view(1, 1),
+                                past_key_values=self.cache, cache_position=self._position, use_cache=True,
+                                logits_to_keep=1).logits
+        self._decode_logits = logits
+        self._next_token.copy_(logits.argmax(dim=-1))
         # position P consumes generated token P - prompt and produces the next one
         col = (self._position - self.prompt_tokens + 1).view(1, 1).expand(self.batch_size, 1)
         self._generated.scatter_(1, col, self._next_token)
