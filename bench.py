@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--e2e", type=int, default=1, help="end-to-end generation section (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end section (profiling)")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill section (profiling)")
     ap.add_argument("--e2e-batch", type=int, default=4)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-output", type=int, default=256)
@@ -381,6 +382,9 @@ def main():
     torch.cuda.set_device(device)
     if args.e2e_only:
         print(json.dumps({"e2e": e2e_measure(args, device)}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_measure(args, device)}), flush=True)
         return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)

@@ -1149,7 +1149,12 @@ gemm_prefill_async_kernel(GemmArgs a) {
       const int p = min(base + s, end - 1);
       issue(p, __builtin_amdgcn_readfirstlane(lds_read_i32(mx_lds + 4 * (p - base))), s);
     }
-    for (int p = base; p < end; ++p) {
+    // Software pipeline across K steps: the 16 MFMAs of step p are issued
+    // before the fp32 epilogue (cvt + FMA by its scale) of step p - 1, so the
+    // VALU epilogue of one step runs while the matrix cores work on the next.
+    // Two result sets alternate (the loop is unrolled by two so they stay in
+    // registers).
+    auto step = [&](int p, v4i (&dnew)[4][4], float& snew) {
       const int stage = (p - base) % P;
       wait_vmcnt<5 * (P - 2)>();
       // s_barrier without __syncthreads' release fence: that fence waits for
@@ -1187,11 +1192,34 @@ gemm_prefill_async_kernel(GemmArgs a) {
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+        for (int jb = 0; jb < 4; ++jb)
+          dnew[tb][jb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+      snew = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc)));
+    };
+    auto epilogue = [&](const v4i (&d)[4][4], float sc) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], sc, acc[tb][jb][v]);
-        }
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[tb][jb][v], sc, acc[tb][jb][v]);
+    };
+    v4i d0[4][4], d1[4][4];
+    float s0 = 0.0f, s1 = 0.0f;
+    int p = base;
+    if (p < end) step(p++, d0, s0);
+    while (p + 1 < end) {
+      step(p++, d1, s1);
+      epilogue(d0, s0);
+      step(p++, d0, s0);
+      epilogue(d1, s1);
+    }
+    if (p < end) {
+      step(p++, d1, s1);
+      epilogue(d0, s0);
+      epilogue(d1, s1);
+    } else if (end > base) {
+      epilogue(d0, s0);
     }
     wait_vmcnt<0>();   // drain the re-issued tail loads before the stages are reused
   }
@@ -1231,6 +1259,410 @@ gemm_prefill_async_kernel(GemmArgs a) {
         const int col = r * 64 + jb * 16 + arow;
         if (row < a.n && col < a.m) {
           const float sum = acc[tb][jb][v];
+          uint16_t y;
+          if (a.out_bf16) {
+            y = Bf16::from_f32(sum);
+            if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+          } else {
+            y = Fp16::from_f32(sum);
+            if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+          }
+          a.out[(int64_t)row * a.ldo + col] = y;
+        }
+      }
+}
+
+// ---- prefill kernel v3: two row tiles per workgroup, 4-stage DMA ring ------
+//
+// Workgroup (row-tile pair r0 = 2 bx, r0 + 1; token block of 256), 8 waves:
+// wave w computes tokens (w & 3) * 64 .. + 64 of row tile r0 + (w >> 2), i.e.
+// 16 v_mfma_i32_16x16x64_i8 per K step, as gemm_prefill_async_kernel.  The
+// 16 KiB activation slice of a K step is shared by both row tiles (half the
+// activation traffic per MFMA), and four stages of 24 KiB (slice + two weight
+// tiles) keep three K steps of global -> LDS DMA in flight.  The K loop runs
+// over every column tile c; an LDS map gives each row's INT8 position at c
+// (or -1 where the tile is 16-bit: that row's MFMAs skip the step), so the
+// INT8 tiles of each row are still accumulated in ascending column order,
+// then its 16-bit tiles -- the reference's order.  Eight waves per workgroup
+// (two per SIMD) let one wave's fp32 epilogue overlap another's MFMAs.  LDS
+// reads inside the pipeline are inline asm for the reason given at
+// gemm_prefill_async_kernel.
+constexpr int kP3Threads = 512;
+constexpr int kP3Stage = kPfXBytes + 2 * 4096;
+constexpr int kP3Stages = 4;
+constexpr int kP3MaxCols = 512;   // k <= 32768
+
+template <class XT>
+__global__ void __launch_bounds__(kP3Threads)
+gemm_prefill_v3_kernel(GemmArgs a) {
+  __shared__ __align__(16) int8_t smem[kP3Stages * kP3Stage];
+  __shared__ int pos8[2][kP3MaxCols];
+  __shared__ float scl[2][kP3MaxCols];
+  constexpr int P = kP3Stages;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int tq = wave & 3, rt = wave >> 2;
+  const int r0 = blockIdx.x * 2, r = r0 + rt;
+  const int n0 = blockIdx.y * kPfTokens;
+  const int arow = lane & 15, akq = lane >> 4;
+  const int n_tc = a.n_tc;
+  const int t8 = a.rp8[a.n_tr];
+
+  // ---- position / scale map of the two row tiles
+  for (int i = t; i < 2 * kP3MaxCols; i += kP3Threads) (&pos8[0][0])[i] = -1;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int rr = r0 + j;
+    if (rr >= a.n_tr) continue;
+    const int lo = a.rp8[rr], hi = a.rp8[rr + 1];
+    for (int p = lo + t; p < hi; p += kP3Threads) {
+      const int c = col_of(a.ids8[p], rr * n_tc, n_tc);
+      pos8[j][c] = p;
+      scl[j][c] = a.sx[c] * a.sw8[p];
+    }
+  }
+  __syncthreads();
+
+  v4f acc[4][4];   // [token block][j-block]
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (t8 > 0) {
+    // DMA lanes: wave w moves token blocks 2w, 2w + 1 of the slice and 1 KiB
+    // (j-block w & 3) of the weight tile of row r0 + (w >> 2)
+    int64_t xrow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      xrow[i] = (int64_t)min(n0 + (2 * wave + i) * 16 + arow, a.n - 1) * a.ldq + akq * 16;
+    const int wj = wave >> 2, wjb = wave & 3;
+    const int w_off = (a.layout == TQ_LAYOUT_MFMA) ? wjb * 1024 + lane * 16
+                                                   : (wjb * 16 + (lane & 15)) * 64 + (lane >> 4) * 16;
+    const uint32_t smem_lds = lds_addr(smem);
+    const uint32_t pos_lds = lds_addr(&pos8[0][0]), scl_lds = lds_addr(&scl[0][0]);
+    auto meta_pos = [&](int j, int c) {   // INT8 position of tile (r0 + j, c), -1 if 16-bit
+      int v;
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v)
+                   : "v"(pos_lds + 4 * (j * kP3MaxCols + c)) : "memory");
+      return __builtin_amdgcn_readfirstlane(v);
+    };
+    auto issue = [&](int c, int st, int pw) {   // pw: this wave's weight position (>= 0)
+      int8_t* sp = smem + st * kP3Stage;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_global_load_lds(a.xq + xrow[i] + c * 64, sp + (2 * wave + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off, sp + kPfXBytes + wj * 4096 + wjb * 1024,
+                                       16, 0, 0);
+    };
+    // a 16-bit position has no INT8 tile: the weight DMA reads a valid tile instead (never used)
+    auto pos_or_any = [&](int p) { return p >= 0 ? p : 0; };
+#pragma unroll
+    for (int st = 0; st < P - 1; ++st) {
+      const int c = min(st, n_tc - 1);
+      issue(c, st, pos_or_any(meta_pos(wj, c)));
+    }
+    const uint32_t w_rd = smem_lds + kPfXBytes + rt * 4096 + lane * 16;
+    const uint32_t x_rd = smem_lds + tq * 4096 + lane * 16;
+
+    for (int c = 0; c < n_tc; ++c) {
+      const int stage = c % P;
+      wait_vmcnt<3 * (P - 2)>();
+      asm volatile("s_barrier" ::: "memory");
+      const int cn = min(c + P - 1, n_tc - 1);
+      int pn, pc;
+      float sc;
+      asm volatile(
+          "ds_read_b32 %0, %3\n\t"
+          "ds_read_b32 %1, %4\n\t"
+          "ds_read_b32 %2, %5\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(pn), "=&v"(pc), "=&v"(sc)
+          : "v"(pos_lds + 4 * (wj * kP3MaxCols + cn)), "v"(pos_lds + 4 * (rt * kP3MaxCols + c)),
+            "v"(scl_lds + 4 * (rt * kP3MaxCols + c))
+          : "memory");
+      issue(cn, (stage + P - 1) % P, pos_or_any(__builtin_amdgcn_readfirstlane(pn)));
+      const bool has = __builtin_amdgcn_readfirstlane(pc) >= 0 && r < a.n_tr;
+      if (!has) continue;   // 16-bit tile (or no row): this wave skips the step
+      const float scu = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc)));
+      v4i bw[4], ax[4];
+      const uint32_t so = stage * kP3Stage;
+      asm volatile(
+          "ds_read_b128 %0, %8\n\t"
+          "ds_read_b128 %1, %8 offset:1024\n\t"
+          "ds_read_b128 %2, %8 offset:2048\n\t"
+          "ds_read_b128 %3, %8 offset:3072\n\t"
+          "ds_read_b128 %4, %9\n\t"
+          "ds_read_b128 %5, %9 offset:1024\n\t"
+          "ds_read_b128 %6, %9 offset:2048\n\t"
+          "ds_read_b128 %7, %9 offset:3072\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+            "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
+          : "v"(w_rd + so), "v"(x_rd + so)
+          : "memory");
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], scu, acc[tb][jb][v]);
+        }
+    }
+    wait_vmcnt<0>();   // drain the re-issued tail loads
+  }
+
+  if (r >= a.n_tr) return;   // odd row-tile count: the second half of the last pair is empty
+  // ---- 16-bit tiles of row r (straight from global; rare by construction)
+  if (a.w16 != nullptr) {
+    const int lo16 = a.rp16[r], hi16 = a.rp16[r + 1];
+    for (int q = lo16; q < hi16; ++q) {
+      const int c = col_of(a.ids16[q], r * n_tc, n_tc);
+      v4i bw[4][2];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        bw[jb][0] = load_w16(a, q, jb, 0, lane);
+        bw[jb][1] = load_w16(a, q, jb, 1, lane);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int row = n0 + tq * 64 + tb * 16 + arow;
+        const v4i a0 = load_xf<1>(a, row, c * 64 + akq * 8);
+        const v4i a1 = load_xf<1>(a, row, c * 64 + 32 + akq * 8);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          acc[tb][jb] = mfma16<XT>(a0, bw[jb][0], acc[tb][jb]);
+          acc[tb][jb] = mfma16<XT>(a1, bw[jb][1], acc[tb][jb]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = n0 + tq * 64 + tb * 16 + 4 * akq + v;
+        const int col = r * 64 + jb * 16 + arow;
+        if (row < a.n && col < a.m) {
+          const float sum = acc[tb][jb][v];
+          uint16_t y;
+          if (a.out_bf16) {
+            y = Bf16::from_f32(sum);
+            if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
+          } else {
+            y = Fp16::from_f32(sum);
+            if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
+          }
+          a.out[(int64_t)row * a.ldo + col] = y;
+        }
+      }
+}
+
+// ---- prefill kernel v4: 64 x 128 wave tiles ---------------------------------
+//
+// As gemm_prefill_v3_kernel (two row tiles per workgroup, 256 tokens, DMA
+// ring, LDS position map), but 4 waves that each own 64 tokens x BOTH row
+// tiles: 32 MFMAs per K step for 12 KiB of LDS operand reads (v3: 16 MFMAs
+// for 8 KiB), which is what bounds the MFMA rate once the LDS port is busy.
+// 3 stages of 24 KiB + the maps = 76 KiB: two workgroups per CU.
+constexpr int kP4Threads = 256;
+constexpr int kP4Stages = 3;
+constexpr int kP4MaxCols = 256;   // k <= 16384
+
+template <class XT>
+__global__ void __launch_bounds__(kP4Threads)
+gemm_prefill_v4_kernel(GemmArgs a) {
+  __shared__ __align__(16) int8_t smem[kP4Stages * kP3Stage];
+  __shared__ int pos8[2][kP4MaxCols];
+  __shared__ float scl[2][kP4MaxCols];
+  constexpr int P = kP4Stages;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r0 = blockIdx.x * 2;
+  const int n0 = blockIdx.y * kPfTokens;
+  const int arow = lane & 15, akq = lane >> 4;
+  const int n_tc = a.n_tc;
+  const int t8 = a.rp8[a.n_tr];
+  const bool has1 = r0 + 1 < a.n_tr;   // odd row-tile count: the last pair has one row
+
+  for (int i = t; i < 2 * kP4MaxCols; i += kP4Threads) (&pos8[0][0])[i] = -1;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int rr = r0 + j;
+    if (rr >= a.n_tr) continue;
+    const int lo = a.rp8[rr], hi = a.rp8[rr + 1];
+    for (int p = lo + t; p < hi; p += kP4Threads) {
+      const int c = col_of(a.ids8[p], rr * n_tc, n_tc);
+      pos8[j][c] = p;
+      scl[j][c] = a.sx[c] * a.sw8[p];
+    }
+  }
+  __syncthreads();
+
+  v4f acc[4][8];   // [token block][row tile * 4 + j-block]
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (t8 > 0) {
+    // DMA lanes: wave w moves token blocks 4w .. 4w + 3 of the slice and
+    // j-blocks 2(w & 1), 2(w & 1) + 1 of the weight tile of row r0 + (w >> 1)
+    int64_t xrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xrow[i] = (int64_t)min(n0 + (4 * wave + i) * 16 + arow, a.n - 1) * a.ldq + akq * 16;
+    const int wj = wave >> 1;
+    int w_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int jb = 2 * (wave & 1) + i;
+      w_off[i] = (a.layout == TQ_LAYOUT_MFMA) ? jb * 1024 + lane * 16
+                                              : (jb * 16 + (lane & 15)) * 64 + (lane >> 4) * 16;
+    }
+    const uint32_t smem_lds = lds_addr(smem);
+    const uint32_t pos_lds = lds_addr(&pos8[0][0]), scl_lds = lds_addr(&scl[0][0]);
+    auto meta_pos = [&](int j, int c) {
+      int v;
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v)
+                   : "v"(pos_lds + 4 * (j * kP4MaxCols + c)) : "memory");
+      return __builtin_amdgcn_readfirstlane(v);
+    };
+    auto issue = [&](int c, int st, int pw) {
+      int8_t* sp = smem + st * kP3Stage;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_global_load_lds(a.xq + xrow[i] + c * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
+                                         sp + kPfXBytes + wj * 4096 + (2 * (wave & 1) + i) * 1024, 16, 0, 0);
+    };
+    auto pos_or_any = [&](int p) { return p >= 0 ? p : 0; };
+#pragma unroll
+    for (int st = 0; st < P - 1; ++st) {
+      const int c = min(st, n_tc - 1);
+      issue(c, st, pos_or_any(meta_pos(wj, c)));
+    }
+    const uint32_t w_rd = smem_lds + kPfXBytes + lane * 16;
+    const uint32_t x_rd = smem_lds + wave * 4096 + lane * 16;
+
+    for (int c = 0; c < n_tc; ++c) {
+      const int stage = c % P;
+      wait_vmcnt<6 * (P - 2)>();
+      asm volatile("s_barrier" ::: "memory");
+      const int cn = min(c + P - 1, n_tc - 1);
+      int pn, p0c, p1c;
+      float sc0, sc1;
+      asm volatile(
+          "ds_read_b32 %0, %5\n\t"
+          "ds_read_b32 %1, %6\n\t"
+          "ds_read_b32 %2, %7\n\t"
+          "ds_read_b32 %3, %8\n\t"
+          "ds_read_b32 %4, %9\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(pn), "=&v"(p0c), "=&v"(p1c), "=&v"(sc0), "=&v"(sc1)
+          : "v"(pos_lds + 4 * (wj * kP4MaxCols + cn)), "v"(pos_lds + 4 * c), "v"(pos_lds + 4 * (kP4MaxCols + c)),
+            "v"(scl_lds + 4 * c), "v"(scl_lds + 4 * (kP4MaxCols + c))
+          : "memory");
+      issue(cn, (stage + P - 1) % P, pos_or_any(__builtin_amdgcn_readfirstlane(pn)));
+      const bool h0 = __builtin_amdgcn_readfirstlane(p0c) >= 0;
+      const bool h1 = __builtin_amdgcn_readfirstlane(p1c) >= 0 && has1;
+      if (!h0 && !h1) continue;
+      const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc0)));
+      const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));
+      const uint32_t so = stage * kP3Stage;
+      v4i ax[4], bw[8];
+      asm volatile(
+          "ds_read_b128 %0, %4\n\t"
+          "ds_read_b128 %1, %4 offset:1024\n\t"
+          "ds_read_b128 %2, %4 offset:2048\n\t"
+          "ds_read_b128 %3, %4 offset:3072\n\t"
+          : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
+          : "v"(x_rd + so)
+          : "memory");
+      asm volatile(
+          "ds_read_b128 %0, %8\n\t"
+          "ds_read_b128 %1, %8 offset:1024\n\t"
+          "ds_read_b128 %2, %8 offset:2048\n\t"
+          "ds_read_b128 %3, %8 offset:3072\n\t"
+          "ds_read_b128 %4, %8 offset:4096\n\t"
+          "ds_read_b128 %5, %8 offset:5120\n\t"
+          "ds_read_b128 %6, %8 offset:6144\n\t"
+          "ds_read_b128 %7, %8 offset:7168\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+            "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
+          : "v"(w_rd + so)
+          : "memory");
+      if (h0) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], s0, acc[tb][jb][v]);
+          }
+      }
+      if (h1) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[4 + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[tb][4 + jb][v] = fmaf((float)d[v], s1, acc[tb][4 + jb][v]);
+          }
+      }
+    }
+    wait_vmcnt<0>();
+  }
+
+  // ---- 16-bit tiles of both rows, then the epilogue
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = r0 + j;
+    if (r >= a.n_tr || a.w16 == nullptr) continue;
+    const int lo16 = a.rp16[r], hi16 = a.rp16[r + 1];
+    for (int q = lo16; q < hi16; ++q) {
+      const int c = col_of(a.ids16[q], r * n_tc, n_tc);
+      v4i bw[4][2];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        bw[jb][0] = load_w16(a, q, jb, 0, lane);
+        bw[jb][1] = load_w16(a, q, jb, 1, lane);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int row = n0 + wave * 64 + tb * 16 + arow;
+        const v4i a0 = load_xf<1>(a, row, c * 64 + akq * 8);
+        const v4i a1 = load_xf<1>(a, row, c * 64 + 32 + akq * 8);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          acc[tb][4 * j + jb] = mfma16<XT>(a0, bw[jb][0], acc[tb][4 * j + jb]);
+          acc[tb][4 * j + jb] = mfma16<XT>(a1, bw[jb][1], acc[tb][4 * j + jb]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = n0 + wave * 64 + tb * 16 + 4 * akq + v;
+        const int r = r0 + (jj >> 2);
+        const int col = r * 64 + (jj & 3) * 16 + arow;
+        if (row < a.n && r < a.n_tr && col < a.m) {
+          const float sum = acc[tb][jj][v];
           uint16_t y;
           if (a.out_bf16) {
             y = Bf16::from_f32(sum);
@@ -1533,7 +1965,15 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                    : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
-    if (a.xvec) {   // DMA path: whole 16-byte activation chunks, aligned rows
+    if (a.xvec && n_tc <= kP4MaxCols) {   // DMA path, 64 x 128 wave tiles
+      const dim3 g4((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
+      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v4_kernel<Bf16>, g4, dim3(kP4Threads), 0, s, a);
+      else hipLaunchKernelGGL(gemm_prefill_v4_kernel<Fp16>, g4, dim3(kP4Threads), 0, s, a);
+    } else if (a.xvec && n_tc <= kP3MaxCols) {   // DMA path, two row tiles per workgroup
+      const dim3 g3((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
+      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v3_kernel<Bf16>, g3, dim3(kP3Threads), 0, s, a);
+      else hipLaunchKernelGGL(gemm_prefill_v3_kernel<Fp16>, g3, dim3(kP3Threads), 0, s, a);
+    } else if (a.xvec) {   // DMA path: whole 16-byte activation chunks, aligned rows
       if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL((gemm_prefill_async_kernel<Bf16, kPfStages>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((gemm_prefill_async_kernel<Fp16, kPfStages>), grid, block, 0, s, a);
     } else {
