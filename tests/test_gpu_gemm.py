@@ -375,6 +375,36 @@ def test_prefill_dma_and_register_paths_agree_bitwise(n, m, k, frac):
     assert torch.equal(_gemm(pack, xd, xq, sx), _gemm(pack, xf_odd, xq_odd, sx))
 
 
+@pytest.mark.parametrize("n,m,k,frac", [(300, 200, 640, 0.2), (260, 320, 1024, 0.1), (513, 192, 2048, 0.5)])
+def test_prefill_dma_path_ragged_outputs_bias_and_strides(n, m, k, frac):
+    """The DMA kernel's edges: ragged M (partial last row tile), an odd
+    row-tile count (a workgroup with one row), 16-bit tiles in both rows of
+    a pair, bias, fp16 output, and an output row stride that forbids 16-byte
+    stores -- bitwise equal to the register-staged kernel (unaligned
+    activation rows) and within tolerance of the oracle."""
+    W, pack, ids16 = _case(m, k, frac, seed=n + m + k)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=n + 3)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    xq_odd = torch.zeros((n, k + 8), dtype=torch.int8, device="cuda")[:, :k]
+    xq_odd.copy_(xq)
+    xf_odd = torch.zeros((n, k + 4), dtype=xd.dtype, device="cuda")[:, :k]
+    xf_odd.copy_(xd)
+    bias = (torch.randn(m, generator=torch.Generator().manual_seed(n)) * 0.5).to(torch.bfloat16).cuda()
+    y = _gemm(pack, xd, xq, sx, bias=bias)
+    assert torch.equal(y, _gemm(pack, xf_odd, xq_odd, sx, bias=bias))
+    rows = np.unique(np.r_[0:4, n - 4:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc, bias=values(bias.cpu()))
+    wide = torch.full((n, m + 3), 5.0, dtype=torch.bfloat16, device="cuda")
+    _gemm(pack, xd, xq, sx, bias=bias, out=wide[:, :m])
+    assert torch.equal(wide[:, :m], y) and torch.all(wide[:, m:] == 5)
+    y16 = _gemm(pack, xd, xq, sx, out_dtype=torch.float16)
+    assert torch.equal(y16, _gemm(pack, xf_odd, xq_odd, sx, out_dtype=torch.float16))
+
+
 def test_prefill_rows_longer_than_one_metadata_chunk():
     # 1100 tiles per row tile: the DMA kernel stages tile metadata in chunks of 512
     n, m, k = 80, 128, 64 * 1100

@@ -56,6 +56,7 @@ struct GemmArgs {
   int out_bf16;   // output dtype: 1 bf16, 0 fp16
   int layout;     // TQ_LAYOUT_*
   int xvec;       // activations allow 16-byte loads (aligned rows, k == 64 * n_tc)
+  int ovec;       // output rows allow 16-byte stores (16-byte aligned base, ldo % 8 == 0)
   int splits;       // split-K decode kernel: splits per row tile
   int32_t* counters;  // [n_tr] arrival counters (zero between launches)
   float* partials;    // [n_tr, splits, n, 64] fp32 split partials
@@ -1463,41 +1464,64 @@ gemm_prefill_v3_kernel(GemmArgs a) {
       }
 }
 
-// ---- prefill kernel v4: 64 x 128 wave tiles ---------------------------------
+// ---- prefill kernel v5: 64 x 128 wave tiles, 16-bit tiles in the ring -------
 //
-// As gemm_prefill_v3_kernel (two row tiles per workgroup, 256 tokens, DMA
-// ring, LDS position map), but 4 waves that each own 64 tokens x BOTH row
-// tiles: 32 MFMAs per K step for 12 KiB of LDS operand reads (v3: 16 MFMAs
-// for 8 KiB), which is what bounds the MFMA rate once the LDS port is busy.
-// 3 stages of 24 KiB + the maps = 76 KiB: two workgroups per CU.
-constexpr int kP4Threads = 256;
-constexpr int kP4Stages = 3;
-constexpr int kP4MaxCols = 256;   // k <= 16384
+// Two row tiles x 256 tokens per workgroup, 4 waves that each own 64 tokens x
+// both row tiles (32 MFMAs per K step for 12 KiB of LDS operand reads).  The
+// K loop is one list of steps fed through a 3-stage DMA ring
+// (global_load_lds, 24 KiB per stage, two workgroups per CU):
+//   steps 0 .. n_tc-1      INT8 column c: 256 x 64 codes + both rows' 4 KiB
+//                          weight tiles (a row whose tile at c is 16-bit
+//                          skips its MFMAs)
+//   then 2 per 16-bit tile half h of the tile: 256 x 32 activations (16 KiB)
+//                          + the tile's 64 x 32 half (4 KiB), 16 bf16/fp16
+//                          MFMAs into the row's accumulators
+// so the accumulation order per output is the reference's: INT8 tiles by
+// column, then 16-bit tiles by position, K halves in order.  The epilogue
+// stages the rounded outputs through LDS and writes 16-byte row chunks.
+constexpr int kP5Threads = 256;
+template <class T> struct TypeTag { using type = T; };
+constexpr int kP5Stages = 3;
+constexpr int kP5MaxCols = 256;   // k <= 16384
+constexpr int kP5OutRow = 272;    // LDS bytes per staged output row (256 + 16: no bank conflicts)
+static_assert(4 * 64 * kP5OutRow <= kP5Stages * kP3Stage, "output staging fits the ring");
 
 template <class XT>
-__global__ void __launch_bounds__(kP4Threads)
-gemm_prefill_v4_kernel(GemmArgs a) {
-  __shared__ __align__(16) int8_t smem[kP4Stages * kP3Stage];
-  __shared__ int pos8[2][kP4MaxCols];
-  __shared__ float scl[2][kP4MaxCols];
-  constexpr int P = kP4Stages;
+__global__ void __launch_bounds__(kP5Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_prefill_v5_kernel(GemmArgs a) {
+  __shared__ __align__(16) int8_t smem[kP5Stages * kP3Stage];
+  __shared__ int pos8[2][kP5MaxCols];
+  __shared__ float scl[2][kP5MaxCols];
+  __shared__ int list16[2 * kP5MaxCols];   // (q << 9) | (row << 8) | column
+  constexpr int P = kP5Stages;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r0 = blockIdx.x * 2;
   const int n0 = blockIdx.y * kPfTokens;
   const int arow = lane & 15, akq = lane >> 4;
   const int n_tc = a.n_tc;
-  const int t8 = a.rp8[a.n_tr];
   const bool has1 = r0 + 1 < a.n_tr;   // odd row-tile count: the last pair has one row
-
-  for (int i = t; i < 2 * kP4MaxCols; i += kP4Threads) (&pos8[0][0])[i] = -1;
+  const int n8s = a.rp8[a.n_tr] > 0 ? n_tc : 0;   // INT8 steps (none if the matrix has no INT8 tile)
+  int n16 = 0, n16_0 = 0;
+  if (a.w16 != nullptr) {
+    const int lo0 = a.rp16[r0], c0 = a.rp16[r0 + 1] - lo0;
+    n16_0 = c0;
+    const int lo1 = has1 ? a.rp16[r0 + 1] : 0, c1 = has1 ? a.rp16[r0 + 2] - lo1 : 0;
+    n16 = c0 + c1;
+    for (int i = t; i < n16; i += kP5Threads) {
+      const int j = i >= c0;
+      const int q = j ? lo1 + (i - c0) : lo0 + i;
+      list16[i] = (q << 9) | (j << 8) | col_of(a.ids16[q], (r0 + j) * n_tc, n_tc);
+    }
+  }
+  for (int i = t; i < 2 * kP5MaxCols; i += kP5Threads) (&pos8[0][0])[i] = -1;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int rr = r0 + j;
-    if (rr >= a.n_tr) continue;
+    if (rr >= a.n_tr || n8s == 0) continue;
     const int lo = a.rp8[rr], hi = a.rp8[rr + 1];
-    for (int p = lo + t; p < hi; p += kP4Threads) {
+    for (int p = lo + t; p < hi; p += kP5Threads) {
       const int c = col_of(a.ids8[p], rr * n_tc, n_tc);
       pos8[j][c] = p;
       scl[j][c] = a.sx[c] * a.sw8[p];
@@ -1511,13 +1535,18 @@ gemm_prefill_v4_kernel(GemmArgs a) {
 #pragma unroll
     for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (t8 > 0) {
-    // DMA lanes: wave w moves token blocks 4w .. 4w + 3 of the slice and
-    // j-blocks 2(w & 1), 2(w & 1) + 1 of the weight tile of row r0 + (w >> 1)
-    int64_t xrow[4];
+  const int S = n8s + 2 * n16;
+  if (S > 0) {
+    // DMA lanes: INT8 steps move token blocks 4w .. 4w + 3 and j-blocks
+    // 2(w & 1), 2(w & 1) + 1 of row r0 + (w >> 1); 16-bit steps move the same
+    // token blocks and j-block w of the tile half.  6 loads per wave per step.
+    int64_t xrow8[4], xrow16[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      xrow[i] = (int64_t)min(n0 + (4 * wave + i) * 16 + arow, a.n - 1) * a.ldq + akq * 16;
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = min(n0 + (4 * wave + i) * 16 + arow, a.n - 1);
+      xrow8[i] = row * a.ldq + akq * 16;
+      xrow16[i] = row * a.ldx + akq * 8;
+    }
     const int wj = wave >> 1;
     int w_off[2];
 #pragma unroll
@@ -1526,39 +1555,62 @@ gemm_prefill_v4_kernel(GemmArgs a) {
       w_off[i] = (a.layout == TQ_LAYOUT_MFMA) ? jb * 1024 + lane * 16
                                               : (jb * 16 + (lane & 15)) * 64 + (lane >> 4) * 16;
     }
+    const int w16_off = (a.layout == TQ_LAYOUT_MFMA) ? wave * 1024 + lane * 8
+                                                     : (wave * 16 + (lane & 15)) * 64 + (lane >> 4) * 8;
     const uint32_t smem_lds = lds_addr(smem);
     const uint32_t pos_lds = lds_addr(&pos8[0][0]), scl_lds = lds_addr(&scl[0][0]);
-    auto meta_pos = [&](int j, int c) {
+    const uint32_t l16_lds = lds_addr(list16);
+    // LDS byte address of the DMA metadata of step sn (INT8: this wave's row position; 16-bit: list entry)
+    auto dma_meta_addr = [&](int sn) -> uint32_t {
+      return sn < n8s ? pos_lds + 4 * (wj * kP5MaxCols + sn) : l16_lds + 4 * ((sn - n8s) >> 1);
+    };
+    auto issue = [&](int sn, int st, int meta) {
+      int8_t* sp = smem + st * kP3Stage;
+      if (sn < n8s) {
+        const int pw = meta >= 0 ? meta : 0;   // a 16-bit tile here: any valid INT8 tile, unused
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_global_load_lds(a.xq + xrow8[i] + sn * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
+                                           sp + kPfXBytes + wj * 4096 + (2 * (wave & 1) + i) * 1024, 16, 0, 0);
+      } else {
+        const int h = (sn - n8s) & 1;
+        const int c = meta & 255;
+        const int64_t q = (unsigned)meta >> 9;
+        const int col = c * 64 + h * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_global_load_lds(a.xf + xrow16[i] + col, sp + (4 * wave + i) * 1024, 16, 0, 0);
+        const uint16_t* wsrc = a.w16 + q * 4096 + w16_off + ((a.layout == TQ_LAYOUT_MFMA) ? h * 512 : h * 32);
+        // the same 1 KiB twice keeps the per-step load count at 6
+        __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
+      }
+    };
+    auto read_meta = [&](uint32_t addr) {
       int v;
-      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v)
-                   : "v"(pos_lds + 4 * (j * kP4MaxCols + c)) : "memory");
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
       return __builtin_amdgcn_readfirstlane(v);
     };
-    auto issue = [&](int c, int st, int pw) {
-      int8_t* sp = smem + st * kP3Stage;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_global_load_lds(a.xq + xrow[i] + c * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
-                                         sp + kPfXBytes + wj * 4096 + (2 * (wave & 1) + i) * 1024, 16, 0, 0);
-    };
-    auto pos_or_any = [&](int p) { return p >= 0 ? p : 0; };
 #pragma unroll
     for (int st = 0; st < P - 1; ++st) {
-      const int c = min(st, n_tc - 1);
-      issue(c, st, pos_or_any(meta_pos(wj, c)));
+      const int sn = min(st, S - 1);
+      issue(sn, st, read_meta(dma_meta_addr(sn)));
     }
     const uint32_t w_rd = smem_lds + kPfXBytes + lane * 16;
     const uint32_t x_rd = smem_lds + wave * 4096 + lane * 16;
 
-    for (int c = 0; c < n_tc; ++c) {
-      const int stage = c % P;
+    auto step = [&](auto mode_tag, int s) {
+      constexpr int MODE = decltype(mode_tag)::value;
+      const int stage = s % P;
       wait_vmcnt<6 * (P - 2)>();
       asm volatile("s_barrier" ::: "memory");
-      const int cn = min(c + P - 1, n_tc - 1);
-      int pn, p0c, p1c;
+      const int sn = min(s + P - 1, S - 1);
+      constexpr bool is8 = MODE == 0;
+      const int c8 = max(min(s, n8s - 1), 0);
+      int mn, m0, m1;
       float sc0, sc1;
       asm volatile(
           "ds_read_b32 %0, %5\n\t"
@@ -1567,113 +1619,142 @@ gemm_prefill_v4_kernel(GemmArgs a) {
           "ds_read_b32 %3, %8\n\t"
           "ds_read_b32 %4, %9\n\t"
           "s_waitcnt lgkmcnt(0)"
-          : "=&v"(pn), "=&v"(p0c), "=&v"(p1c), "=&v"(sc0), "=&v"(sc1)
-          : "v"(pos_lds + 4 * (wj * kP4MaxCols + cn)), "v"(pos_lds + 4 * c), "v"(pos_lds + 4 * (kP4MaxCols + c)),
-            "v"(scl_lds + 4 * c), "v"(scl_lds + 4 * (kP4MaxCols + c))
+          : "=&v"(mn), "=&v"(m0), "=&v"(m1), "=&v"(sc0), "=&v"(sc1)
+          : "v"(dma_meta_addr(sn)), "v"(is8 ? pos_lds + 4 * s : l16_lds + 4 * ((s - n8s) >> 1)),
+            "v"(pos_lds + 4 * (kP5MaxCols + c8)), "v"(scl_lds + 4 * c8), "v"(scl_lds + 4 * (kP5MaxCols + c8))
           : "memory");
-      issue(cn, (stage + P - 1) % P, pos_or_any(__builtin_amdgcn_readfirstlane(pn)));
-      const bool h0 = __builtin_amdgcn_readfirstlane(p0c) >= 0;
-      const bool h1 = __builtin_amdgcn_readfirstlane(p1c) >= 0 && has1;
-      if (!h0 && !h1) continue;
-      const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc0)));
-      const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));
+      issue(sn, (stage + P - 1) % P, __builtin_amdgcn_readfirstlane(mn));
+      const int meta0 = __builtin_amdgcn_readfirstlane(m0);
       const uint32_t so = stage * kP3Stage;
-      v4i ax[4], bw[8];
-      asm volatile(
-          "ds_read_b128 %0, %4\n\t"
-          "ds_read_b128 %1, %4 offset:1024\n\t"
-          "ds_read_b128 %2, %4 offset:2048\n\t"
-          "ds_read_b128 %3, %4 offset:3072\n\t"
-          : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
-          : "v"(x_rd + so)
-          : "memory");
-      asm volatile(
-          "ds_read_b128 %0, %8\n\t"
-          "ds_read_b128 %1, %8 offset:1024\n\t"
-          "ds_read_b128 %2, %8 offset:2048\n\t"
-          "ds_read_b128 %3, %8 offset:3072\n\t"
-          "ds_read_b128 %4, %8 offset:4096\n\t"
-          "ds_read_b128 %5, %8 offset:5120\n\t"
-          "ds_read_b128 %6, %8 offset:6144\n\t"
-          "ds_read_b128 %7, %8 offset:7168\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
-            "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
-          : "v"(w_rd + so)
-          : "memory");
-      if (h0) {
+      if constexpr (is8) {
+        const bool h0 = meta0 >= 0;
+        const bool h1 = __builtin_amdgcn_readfirstlane(m1) >= 0 && has1;
+        if (!h0 && !h1) return;
+        const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc0)));
+        const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));
+        v4i ax[4], bw[8];
+        asm volatile(
+            "ds_read_b128 %0, %4\n\t"
+            "ds_read_b128 %1, %4 offset:1024\n\t"
+            "ds_read_b128 %2, %4 offset:2048\n\t"
+            "ds_read_b128 %3, %4 offset:3072\n\t"
+            : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
+            : "v"(x_rd + so)
+            : "memory");
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\t"
+            "ds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\t"
+            "ds_read_b128 %5, %8 offset:5120\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\t"
+            "ds_read_b128 %7, %8 offset:7168\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+              "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
+            : "v"(w_rd + so)
+            : "memory");
+        if (h0) {
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], s0, acc[tb][jb][v]);
+            }
+        }
+        if (h1) {
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[4 + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[tb][4 + jb][v] = fmaf((float)d[v], s1, acc[tb][4 + jb][v]);
+            }
+        }
+      } else {
+        v4i ax[4], bw[4];
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\t"
+            "ds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %9\n\t"
+            "ds_read_b128 %5, %9 offset:1024\n\t"
+            "ds_read_b128 %6, %9 offset:2048\n\t"
+            "ds_read_b128 %7, %9 offset:3072\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3]),
+              "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3])
+            : "v"(x_rd + so), "v"(w_rd + so)
+            : "memory");
+        constexpr int J = MODE == 2 ? 4 : 0;   // the row's accumulators
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-          for (int jb = 0; jb < 4; ++jb) {
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], s0, acc[tb][jb][v]);
-          }
+          for (int jb = 0; jb < 4; ++jb) acc[tb][J + jb] = mfma16<XT>(ax[tb], bw[jb], acc[tb][J + jb]);
       }
-      if (h1) {
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-          for (int jb = 0; jb < 4; ++jb) {
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[4 + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[tb][4 + jb][v] = fmaf((float)d[v], s1, acc[tb][4 + jb][v]);
-          }
-      }
-    }
+    };
+    // list16 holds row r0's 16-bit tiles before row r0 + 1's: three loops, one accumulator set each
+    for (int s = 0; s < n8s; ++s) step(std::integral_constant<int, 0>{}, s);
+    for (int s = n8s; s < n8s + 2 * n16_0; ++s) step(std::integral_constant<int, 1>{}, s);
+    for (int s = n8s + 2 * n16_0; s < S; ++s) step(std::integral_constant<int, 2>{}, s);
     wait_vmcnt<0>();
   }
+  __syncthreads();   // every wave is done with the ring: reuse it for the outputs
 
-  // ---- 16-bit tiles of both rows, then the epilogue
+  // ---- epilogue: round, bias (double rounding), stage rows in LDS, 16-byte stores
+  uint16_t* so16 = reinterpret_cast<uint16_t*>(smem + wave * 64 * kP5OutRow);
+  auto stage_out = [&](auto out_tag, auto bias_tag) {
+    using OT = typename decltype(out_tag)::type;
+    constexpr bool HB = decltype(bias_tag)::value;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = r0 + j;
-    if (r >= a.n_tr || a.w16 == nullptr) continue;
-    const int lo16 = a.rp16[r], hi16 = a.rp16[r + 1];
-    for (int q = lo16; q < hi16; ++q) {
-      const int c = col_of(a.ids16[q], r * n_tc, n_tc);
-      v4i bw[4][2];
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        bw[jb][0] = load_w16(a, q, jb, 0, lane);
-        bw[jb][1] = load_w16(a, q, jb, 1, lane);
-      }
+      for (int jj = 0; jj < 8; ++jj) {
+        const int col = (r0 + (jj >> 2)) * 64 + (jj & 3) * 16 + arow;
+        float bv = 0.f;
+        if constexpr (HB) bv = OT::to_f32(a.bias[min(col, a.m - 1)]);
+        uint16_t* dst = so16 + (tb * 16 + 4 * akq) * (kP5OutRow / 2) + jj * 16 + arow;
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const int row = n0 + wave * 64 + tb * 16 + arow;
-        const v4i a0 = load_xf<1>(a, row, c * 64 + akq * 8);
-        const v4i a1 = load_xf<1>(a, row, c * 64 + 32 + akq * 8);
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          acc[tb][4 * j + jb] = mfma16<XT>(a0, bw[jb][0], acc[tb][4 * j + jb]);
-          acc[tb][4 * j + jb] = mfma16<XT>(a1, bw[jb][1], acc[tb][4 * j + jb]);
+        for (int v = 0; v < 4; v += 2) {
+          uint32_t y2 = OT::pack2(acc[tb][jj][v], acc[tb][jj][v + 1]);
+          if constexpr (HB)   // the reference's double rounding: round(round(acc) + bias)
+            y2 = OT::pack2(OT::to_f32((uint16_t)y2) + bv, OT::to_f32((uint16_t)(y2 >> 16)) + bv);
+          dst[v * (kP5OutRow / 2)] = (uint16_t)y2;
+          dst[(v + 1) * (kP5OutRow / 2)] = (uint16_t)(y2 >> 16);
         }
       }
+  };
+  if (a.out_bf16) {
+    if (a.bias) stage_out(TypeTag<Bf16>{}, std::true_type{});
+    else stage_out(TypeTag<Bf16>{}, std::false_type{});
+  } else {
+    if (a.bias) stage_out(TypeTag<Fp16>{}, std::true_type{});
+    else stage_out(TypeTag<Fp16>{}, std::false_type{});
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave reads back only its own rows
+  const int cw = has1 ? 128 : 64;       // valid staged columns
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int rr = i * 4 + (lane >> 4);   // staged row 0..63
+    const int ch = lane & 15;             // 16-byte chunk: columns ch*8 .. ch*8+7
+    const int row = n0 + wave * 64 + rr;
+    const int col = r0 * 64 + ch * 8;
+    if (row >= a.n || ch * 8 >= cw || col >= a.m) continue;
+    const v4i val = *reinterpret_cast<const v4i*>(smem + wave * 64 * kP5OutRow + rr * kP5OutRow + ch * 16);
+    uint16_t* dst = a.out + (int64_t)row * a.ldo + col;
+    if (a.ovec && col + 8 <= a.m) {
+      *reinterpret_cast<v4i*>(dst) = val;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (col + u < a.m) dst[u] = (uint16_t)((uint32_t)val[u >> 1] >> (16 * (u & 1)));
     }
   }
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = n0 + wave * 64 + tb * 16 + 4 * akq + v;
-        const int r = r0 + (jj >> 2);
-        const int col = r * 64 + (jj & 3) * 16 + arow;
-        if (row < a.n && r < a.n_tr && col < a.m) {
-          const float sum = acc[tb][jj][v];
-          uint16_t y;
-          if (a.out_bf16) {
-            y = Bf16::from_f32(sum);
-            if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
-          } else {
-            y = Fp16::from_f32(sum);
-            if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
-          }
-          a.out[(int64_t)row * a.ldo + col] = y;
-        }
-      }
 }
 
 // ---- host side -----------------------------------------------------------
@@ -1949,6 +2030,7 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
   a.xvec = xvec_ok(a);
+  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec) {
@@ -1965,10 +2047,11 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                    : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
-    if (a.xvec && n_tc <= kP4MaxCols) {   // DMA path, 64 x 128 wave tiles
-      const dim3 g4((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
-      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v4_kernel<Bf16>, g4, dim3(kP4Threads), 0, s, a);
-      else hipLaunchKernelGGL(gemm_prefill_v4_kernel<Fp16>, g4, dim3(kP4Threads), 0, s, a);
+    if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 23)) {
+      // DMA ring, 64 x 128 wave tiles, 16-bit tiles in the ring
+      const dim3 g5((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
+      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v5_kernel<Bf16>, g5, dim3(kP5Threads), 0, s, a);
+      else hipLaunchKernelGGL(gemm_prefill_v5_kernel<Fp16>, g5, dim3(kP5Threads), 0, s, a);
     } else if (a.xvec && n_tc <= kP3MaxCols) {   // DMA path, two row tiles per workgroup
       const dim3 g3((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
       if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v3_kernel<Bf16>, g3, dim3(kP3Threads), 0, s, a);
@@ -2019,6 +2102,7 @@ extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, in
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
   a.xvec = (k == n_tc * 64 && (x_fp_stride_n % 8) == 0 && aligned16(x_fp)) ? 1 : 0;
+  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (split_k <= 1 && a.xvec) {
     const DecodePlan d = plan_decode(n, k, n_tr, n_tc, true);
@@ -2052,6 +2136,7 @@ extern "C" int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_st
   a.n = n; a.m = n_tr * 64; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
   a.layout = tile_layout;
   a.xvec = xvec_ok(a);
+  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
   a.sx = nullptr; a.sw8 = nullptr;  // the dump path reads no scales
   return (int)launch_dump(a, static_cast<hipStream_t>(stream));
 }
