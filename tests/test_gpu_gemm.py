@@ -375,9 +375,10 @@ def test_prefill_dma_and_register_paths_agree_bitwise(n, m, k, frac):
     assert torch.equal(_gemm(pack, xd, xq, sx), _gemm(pack, xf_odd, xq_odd, sx))
 
 
-@pytest.mark.parametrize("n,m,k,frac", [(300, 200, 640, 0.2), (260, 320, 1024, 0.1), (513, 192, 2048, 0.5)])
+@pytest.mark.parametrize("n,m,k,frac", [(300, 200, 640, 0.2), (260, 320, 1024, 0.1), (513, 192, 2048, 0.5),
+                                         (1000, 3000, 640, 0.2), (700, 3072, 1024, 0.5)])
 def test_prefill_dma_path_ragged_outputs_bias_and_strides(n, m, k, frac):
-    """The DMA kernel's edges: ragged M (partial last row tile), an odd
+    """The DMA kernels' edges: ragged M (partial last row tile), an odd
     row-tile count (a workgroup with one row), 16-bit tiles in both rows of
     a pair, bias, fp16 output, and an output row stride that forbids 16-byte
     stores -- bitwise equal to the register-staged kernel (unaligned

@@ -1564,30 +1564,43 @@ gemm_prefill_v5_kernel(GemmArgs a) {
     auto dma_meta_addr = [&](int sn) -> uint32_t {
       return sn < n8s ? pos_lds + 4 * (wj * kP5MaxCols + sn) : l16_lds + 4 * ((sn - n8s) >> 1);
     };
-    auto issue = [&](int sn, int st, int meta) {
+    // The step's 6 loads in 3 parts of 2, issued at points spread over the
+    // MFMA phase: a burst of all waves' loads right after the barrier backs
+    // up the texture path and stalls the issuing waves.
+    auto issue_part = [&](int sn, int st, int meta, int part) {
       int8_t* sp = smem + st * kP3Stage;
       if (sn < n8s) {
-        const int pw = meta >= 0 ? meta : 0;   // a 16-bit tile here: any valid INT8 tile, unused
+        if (part < 2) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_amdgcn_global_load_lds(a.xq + xrow8[i] + sn * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
+          for (int i = 2 * part; i < 2 * part + 2; ++i)
+            __builtin_amdgcn_global_load_lds(a.xq + xrow8[i] + sn * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
+        } else {
+          const int pw = meta >= 0 ? meta : 0;   // a 16-bit tile here: any valid INT8 tile, unused
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
-                                           sp + kPfXBytes + wj * 4096 + (2 * (wave & 1) + i) * 1024, 16, 0, 0);
+          for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
+                                             sp + kPfXBytes + wj * 4096 + (2 * (wave & 1) + i) * 1024, 16, 0, 0);
+        }
       } else {
         const int h = (sn - n8s) & 1;
-        const int c = meta & 255;
-        const int64_t q = (unsigned)meta >> 9;
-        const int col = c * 64 + h * 32;
+        if (part < 2) {
+          const int col = (meta & 255) * 64 + h * 32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_amdgcn_global_load_lds(a.xf + xrow16[i] + col, sp + (4 * wave + i) * 1024, 16, 0, 0);
-        const uint16_t* wsrc = a.w16 + q * 4096 + w16_off + ((a.layout == TQ_LAYOUT_MFMA) ? h * 512 : h * 32);
-        // the same 1 KiB twice keeps the per-step load count at 6
-        __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
+          for (int i = 2 * part; i < 2 * part + 2; ++i)
+            __builtin_amdgcn_global_load_lds(a.xf + xrow16[i] + col, sp + (4 * wave + i) * 1024, 16, 0, 0);
+        } else {
+          const int64_t q = (unsigned)meta >> 9;
+          const uint16_t* wsrc = a.w16 + q * 4096 + w16_off + ((a.layout == TQ_LAYOUT_MFMA) ? h * 512 : h * 32);
+          // the same 1 KiB twice keeps the per-step load count at 6
+          __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
+        }
       }
+    };
+    auto issue = [&](int sn, int st, int meta) {
+      issue_part(sn, st, meta, 0);
+      issue_part(sn, st, meta, 1);
+      issue_part(sn, st, meta, 2);
     };
     auto read_meta = [&](uint32_t addr) {
       int v;
@@ -1623,13 +1636,18 @@ gemm_prefill_v5_kernel(GemmArgs a) {
           : "v"(dma_meta_addr(sn)), "v"(is8 ? pos_lds + 4 * s : l16_lds + 4 * ((s - n8s) >> 1)),
             "v"(pos_lds + 4 * (kP5MaxCols + c8)), "v"(scl_lds + 4 * c8), "v"(scl_lds + 4 * (kP5MaxCols + c8))
           : "memory");
-      issue(sn, (stage + P - 1) % P, __builtin_amdgcn_readfirstlane(mn));
+      const int dst = (stage + P - 1) % P, dmeta = __builtin_amdgcn_readfirstlane(mn);
+      issue_part(sn, dst, dmeta, 0);
       const int meta0 = __builtin_amdgcn_readfirstlane(m0);
       const uint32_t so = stage * kP3Stage;
       if constexpr (is8) {
         const bool h0 = meta0 >= 0;
         const bool h1 = __builtin_amdgcn_readfirstlane(m1) >= 0 && has1;
-        if (!h0 && !h1) return;
+        if (!h0 && !h1) {
+          issue_part(sn, dst, dmeta, 1);
+          issue_part(sn, dst, dmeta, 2);
+          return;
+        }
         const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc0)));
         const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));
         v4i ax[4], bw[8];
@@ -1655,26 +1673,28 @@ gemm_prefill_v5_kernel(GemmArgs a) {
               "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
             : "v"(w_rd + so)
             : "memory");
-        if (h0) {
+        // one row tile's 16 MFMAs (+ epilogue), with a load part issued after the first 8
+        auto row_mfma = [&](auto j_tag, float sc, int part) {
+          constexpr int J = decltype(j_tag)::value;
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb)
+          for (int tb = 0; tb < 4; ++tb) {
+            if (tb == 2) {
+              __builtin_amdgcn_sched_barrier(0);
+              issue_part(sn, dst, dmeta, part);
+              __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
-              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[J + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-              for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], s0, acc[tb][jb][v]);
+              for (int v = 0; v < 4; ++v) acc[tb][J + jb][v] = fmaf((float)d[v], sc, acc[tb][J + jb][v]);
             }
-        }
-        if (h1) {
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[4 + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-              for (int v = 0; v < 4; ++v) acc[tb][4 + jb][v] = fmaf((float)d[v], s1, acc[tb][4 + jb][v]);
-            }
-        }
+          }
+        };
+        if (h0) row_mfma(std::integral_constant<int, 0>{}, s0, 1);
+        else issue_part(sn, dst, dmeta, 1);
+        if (h1) row_mfma(std::integral_constant<int, 4>{}, s1, 2);
+        else issue_part(sn, dst, dmeta, 2);
       } else {
         v4i ax[4], bw[4];
         asm volatile(
@@ -1692,6 +1712,8 @@ gemm_prefill_v5_kernel(GemmArgs a) {
             : "v"(x_rd + so), "v"(w_rd + so)
             : "memory");
         constexpr int J = MODE == 2 ? 4 : 0;   // the row's accumulators
+        issue_part(sn, dst, dmeta, 1);
+        issue_part(sn, dst, dmeta, 2);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
