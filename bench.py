@@ -56,6 +56,11 @@ def parse():
     ap.add_argument("--e2e", type=int, default=1, help="end-to-end generation section (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end section (profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill section (profiling)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the decode GEMM launches (3 eager steps) and a 256 MiB copy: the workload of "
+                         "the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic")
+    ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="read the two --pmc passes' counter_collection.csv and write " + TRAFFIC_FILE)
     ap.add_argument("--e2e-batch", type=int, default=4)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-output", type=int, default=256)
@@ -66,6 +71,66 @@ def parse():
     ap.add_argument("--e2e-module-path", type=int, default=1,
                     help="also time both models with the modules' own forward in the decode graph")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = "profiles/decode_gemm_traffic.json"
+TRAFFIC_COPY_BYTES = 256 << 20
+GEMM_KERNEL = "tq::gemm_decode_kernel"
+
+
+def _counter_rows(d):
+    import csv
+    import glob
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def traffic_summarize(args):
+    """HBM bytes per decode GEMM launch from two rocprofv3 --pmc passes of
+    --traffic-probe (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
+    scaled by what the same counter reads for the probe's plain copy of
+    TRAFFIC_COPY_BYTES (read once, written once)."""
+    def per_kernel(rows, counter):
+        gemm, copy = [], []
+        for r in rows:
+            if r["Counter_Name"] != counter:
+                continue
+            v = float(r["Counter_Value"])
+            if GEMM_KERNEL in r["Kernel_Name"]:
+                gemm.append(v)
+            elif "neg_kernel" in r["Kernel_Name"] and int(r["Grid_Size"]) >= (TRAFFIC_COPY_BYTES >> 6):
+                copy.append(v)
+        if not gemm or not copy:
+            raise SystemExit(f"{counter}: no {GEMM_KERNEL} or copy dispatches found")
+        return statistics.mean(gemm), statistics.median(copy), len(gemm)
+    fg, fc, n_f = per_kernel(_counter_rows(args.traffic_summarize[0]), "FETCH_SIZE")
+    wg, wc, n_w = per_kernel(_counter_rows(args.traffic_summarize[1]), "WRITE_SIZE")
+    f_scale = TRAFFIC_COPY_BYTES / (fc * 1024.0)
+    w_scale = TRAFFIC_COPY_BYTES / (wc * 1024.0)
+    out = {"kernel": GEMM_KERNEL, "tokens": args.tokens, "layers": args.layers, "keep": args.keep,
+           "gemm_dispatches": n_f, "fetch_kib_per_dispatch": fg, "write_kib_per_dispatch": wg,
+           "copy_bytes": TRAFFIC_COPY_BYTES, "copy_fetch_kib": fc, "copy_write_kib": wc,
+           "fetch_scale": f_scale, "write_scale": w_scale,
+           "traffic_bytes_per_launch": fg * 1024.0 * f_scale + wg * 1024.0 * w_scale}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
+def traffic_for(args):
+    """roofline.traffic from the committed --pmc summary when it was taken on this workload, else None."""
+    try:
+        with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if (t.get("kernel"), t.get("tokens"), t.get("layers"), t.get("keep")) != (GEMM_KERNEL, args.tokens,
+                                                                           args.layers, args.keep):
+        return None
+    return t["traffic_bytes_per_launch"]
 
 
 def keep_ids(n_tr, n_tc, frac, rng):
@@ -368,6 +433,9 @@ def cpu_baseline(args, layers, xs):
 
 def main():
     args = parse()
+    if args.traffic_summarize:
+        traffic_summarize(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -388,6 +456,27 @@ def main():
         return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)
+    if args.traffic_probe:
+        quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in GROUPS}
+        for _ in range(3):
+            for mods in layers:
+                for name, _, _ in GROUPS:
+                    lin = mods[name]
+                    xq, sx = quant[name]
+                    gemm_mixed_rows_splitk(x_fp=xs[name], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                           int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                           int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                           fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
+                                           M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
+                                           out_dtype=torch.bfloat16, tile_layout=lin.tile_layout)
+        src = torch.ones(TRAFFIC_COPY_BYTES // 4, device=device, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)   # a plain elementwise kernel: reads and writes TRAFFIC_COPY_BYTES
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_probe": "done", "gemm_launches": 3 * len(layers) * len(GROUPS),
+                          "copy_bytes": TRAFFIC_COPY_BYTES}), flush=True)
+        return
 
     def step():
         outs = []
@@ -553,7 +642,7 @@ def main():
         "hbm_frac_step": info["packed_bytes"] / step_s / 1e9 / HBM_PEAK_GBPS,
         "eager_ms_per_step": eager_s * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_for(args),
                      "kernel": "tq::gemm_decode_kernel", "avg_launch_us": gemm_avg_s * 1e6,
                      "bytes_per_launch": bytes_per_launch, "launches_per_step": len(launches),
                      "group_avg_us": group_us,
