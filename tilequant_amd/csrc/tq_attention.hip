@@ -16,13 +16,14 @@
 //       16-byte loads per lane), so the chunk costs one memory round trip.
 //   QK: a wave covers 4 keys per step, 16 lanes per key row (16 bytes = 8
 //       elements each, so each row is one coalesced 256-byte read); the 8-wide
-//       partial dots are summed across the 16 lanes with DPP.
-//   softmax: scores (pre-multiplied by scale * log2 e) in LDS; after one
-//       barrier every wave derives the chunk's max and sum itself.
-//   PV: same lane mapping over V, probabilities recomputed from the scores;
-//       per-lane accumulators for G heads x 8 dimensions, reduced across the
-//       wave with xor shuffles, then across the 4 waves through LDS in wave
-//       order.
+//       partial dots are summed across the 16 lanes with DPP, so every lane of
+//       a row holds its key's score.
+//   softmax + PV per wave: the max and sum over the wave's 32 keys come from
+//       the lane's 8 scores and two cross-row butterflies (gfx950
+//       v_permlane16_swap / v_permlane32_swap), the same for the 8-dimension
+//       PV accumulators -- no score exchange through LDS.
+//   the 4 waves' partials (max, sum, o) are combined through LDS in wave
+//       order, rescaled to the chunk max, with one barrier.
 // Everything accumulates in fp32; results are bitwise reproducible.
 #include "tq_common.h"
 
@@ -57,6 +58,27 @@ __device__ inline float row16_sum(float x) {
   return x;
 }
 
+// Sum / max over the 4 rows of 16 lanes (lanes l, l^16, l^32, l^48), the
+// same value and the same association ((r0 o r1) o (r2 o r3)) in every lane.
+__device__ inline float rows4_sum(float x) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const unsigned b = __float_as_uint(x);
+  u2 r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const unsigned c = __float_as_uint(x);
+  r = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float rows4_max(float x) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const unsigned b = __float_as_uint(x);
+  u2 r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const unsigned c = __float_as_uint(x);
+  r = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <class XT>
 __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
 #pragma unroll
@@ -69,8 +91,9 @@ __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
 template <class XT, int G>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_split_kernel(AttnArgs a) {
-  __shared__ float sc[G][kAttnChunk];                               // scaled scores (log2 units)
-  __shared__ float opart[kAttnThreads / kWave][G][kAttnD];
+  constexpr int kWaves = kAttnThreads / kWave;
+  __shared__ float wo[kWaves][G][kAttnD];   // per-wave unnormalised o
+  __shared__ float wml[kWaves][G][2];       // per-wave max, sum
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int s = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads, kvh = blockIdx.y - (blockIdx.y / a.kv_heads) * a.kv_heads;
@@ -85,26 +108,32 @@ attn_split_kernel(AttnArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g)
     qw[g] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8);
-  const int64_t kv_base = (int64_t)b * a.kv_sb + (int64_t)kvh * a.kv_sh + ch * 8;
+  // K/V rows through buffer resources spanning the valid prefix of this
+  // (b, kv head): keys past seq_used read as 0 without touching memory, so
+  // every load is unconditional and all of them stay in flight together.
+  const int64_t kv_base = (int64_t)b * a.kv_sb + (int64_t)kvh * a.kv_sh;
+  const int span = len > 0 ? (int)(((int64_t)(len - 1) * a.kv_sl + kAttnD) * 2) : 0;
+  const __amdgpu_buffer_rsrc_t krs = row_rsrc(a.k + kv_base, span);
+  const __amdgpu_buffer_rsrc_t vrs = row_rsrc(a.v + kv_base, span);
   u32x4 kw[kSteps], vw[kSteps];
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
     const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
-    kw[i] = vw[i] = u32x4{0, 0, 0, 0};
-    if (key < len) {
-      kw[i] = *reinterpret_cast<const u32x4*>(a.k + kv_base + (int64_t)key * a.kv_sl);
-      vw[i] = *reinterpret_cast<const u32x4*>(a.v + kv_base + (int64_t)key * a.kv_sl);
-    }
+    // a key past the prefix gets an offset past the span (rows are not always packed: kv_sl >= D)
+    const int off = key < len ? (int)(((int64_t)key * a.kv_sl + ch * 8) * 2) : span;
+    kw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+    vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first use
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) unpack8<XT>(qw[g], qv[g]);
 
   // ---- QK: 16 lanes per key row, partial dots summed across the row with DPP
+  float sco[kSteps][G];   // scaled scores (log2 units) of the lane's key per step
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
-    const int kloc = wave * (4 * kSteps) + 4 * i + kl;
-    const bool valid = key0 + kloc < len;
+    const bool valid = key0 + wave * (4 * kSteps) + 4 * i + kl < len;
     float kf[8];
     unpack8<XT>(kw[i], kf);
 #pragma unroll
@@ -113,31 +142,28 @@ attn_split_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
       d = row16_sum(d);
-      if (ch == 0) sc[g][kloc] = valid ? d * a.scale_log2 : -INFINITY;
+      sco[i][g] = valid ? d * a.scale_log2 : -INFINITY;
     }
   }
-  __syncthreads();
 
-  // ---- softmax statistics of the chunk, computed redundantly by every wave
-  //      (no further barrier): each lane reads kAttnChunk / 64 scores per head
-  float mloc[G], lsum[G];
+  // ---- this wave's softmax statistics over its 32 keys, then PV
+  float mw[G], lw[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float m = -INFINITY;
+    float m = sco[0][g];
 #pragma unroll
-    for (int j = 0; j < kAttnChunk / kWave; ++j) m = fmaxf(m, sc[g][lane + 64 * j]);
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int i = 1; i < kSteps; ++i) m = fmaxf(m, sco[i][g]);
+    m = rows4_max(m);
     float l = 0.0f;
-    if (m != -INFINITY) {
 #pragma unroll
-      for (int j = 0; j < kAttnChunk / kWave; ++j) l += exp2f(sc[g][lane + 64 * j] - m);
+    for (int i = 0; i < kSteps; ++i) {
+      const float pr = m == -INFINITY ? 0.0f : exp2f(sco[i][g] - m);
+      sco[i][g] = pr;
+      l += pr;
     }
-    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-    mloc[g] = m;
-    lsum[g] = l;
+    mw[g] = m;
+    lw[g] = rows4_sum(l);
   }
-
-  // ---- PV with the probabilities recomputed from the scores
   float o[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -145,38 +171,46 @@ attn_split_kernel(AttnArgs a) {
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
-    const int kloc = wave * (4 * kSteps) + 4 * i + kl;
     float vf[8];
     unpack8<XT>(vw[i], vf);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float p = mloc[g] == -INFINITY ? 0.0f : exp2f(sc[g][kloc] - mloc[g]);
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vf[e], o[g][e]);
-    }
+      for (int e = 0; e < 8; ++e) o[g][e] = fmaf(sco[i][g], vf[e], o[g][e]);
   }
-  // reduce the 4 keys-per-step lanes (lane, lane^16, lane^32, lane^48) in a fixed order
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float x = o[g][e];
-      x += __shfl_xor(x, 16);
-      x += __shfl_xor(x, 32);
-      if (kl == 0) opart[wave][g][ch * 8 + e] = x;
+      const float x = rows4_sum(o[g][e]);
+      if (kl == 0) wo[wave][g][ch * 8 + e] = x;
     }
+    if (lane == 0) {
+      wml[wave][g][0] = mw[g];
+      wml[wave][g][1] = lw[g];
+    }
+  }
   __syncthreads();
-  // partial record per query head: o[D], m, l (m in log2 units of the scaled score)
+  // ---- combine the waves in wave order, rescaled to the chunk max; one
+  //      partial record per query head: o[D], m, l (m in log2 units)
   for (int e = t; e < G * kAttnD; e += kAttnThreads) {
     const int g = e / kAttnD, d = e - g * kAttnD;
-    float x = opart[0][g][d];
+    float M = wml[0][g][0];
 #pragma unroll
-    for (int w = 1; w < kAttnThreads / kWave; ++w) x += opart[w][g][d];
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][g][0]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mwv = wml[w][g][0];
+      const float c = mwv == -INFINITY ? 0.0f : exp2f(mwv - M);
+      O = fmaf(c, wo[w][g][d], O);
+      L = fmaf(c, wml[w][g][1], L);
+    }
     float* rec = a.part + ((int64_t)(b * a.q_heads + kvh * G + g) * a.n_splits + s) * (kAttnD + 2);
-    rec[d] = x;
+    rec[d] = O;
     if (d == 0) {
-      rec[kAttnD] = mloc[g];
-      rec[kAttnD + 1] = lsum[g];
+      rec[kAttnD] = M;
+      rec[kAttnD + 1] = L;
     }
   }
 }
@@ -316,6 +350,8 @@ static int attn_setup(AttnArgs& a, const void* q, int64_t q_stride_b, int64_t q_
     return TQ_ERR_ALIGN;
   if (workspace == nullptr || workspace_elems < tq_decode_attention_workspace_elems(batch, q_heads, max_len))
     return TQ_ERR_WORKSPACE;
+  // one (b, kv head)'s valid rows are addressed through a 32-bit buffer range
+  if (kv_stride_l < head_dim || ((int64_t)max_len * kv_stride_l + head_dim) * 2 >= (1LL << 31)) return TQ_ERR_ARG;
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_stride_b; a.q_sh = q_stride_h;
   a.k = static_cast<const uint16_t*>(k); a.v = static_cast<const uint16_t*>(v);
   a.kv_sb = kv_stride_b; a.kv_sl = kv_stride_l; a.kv_sh = kv_stride_h;

@@ -175,6 +175,13 @@ __device__ inline float block_max(float v, float* red, int nwaves) {
   return r;
 }
 
+// Raw buffer resource over `bytes` bytes at p (stride 0): loads at offsets >=
+// bytes return 0 and touch no memory.  Word 3 = 0x00020000 is the gfx9-family
+// descriptor format (32-bit data format, no swizzle).
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
 __host__ __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Workgroup barrier for LDS hand-offs that leaves outstanding global loads in

@@ -661,12 +661,6 @@ gemm_splitk_kernel(GemmArgs a) {
 
 constexpr int kDecCodesMax = 96 * 1024;   // LDS bytes for staged codes
 
-// Raw buffer resource over `bytes` bytes at p (stride 0): loads at offsets >=
-// bytes return 0 and touch no memory.  Word 3 = 0x00020000 is the gfx9-family
-// descriptor format (32-bit data format, no swizzle).
-__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
-}
 
 // Byte offset of this lane's 16-byte B-operand chunk of j-block jb, k-half h
 // inside a 16-bit tile (the element offsets of load_w16, times two).
