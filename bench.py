@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--e2e", type=int, default=1, help="end-to-end generation section (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end section (profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill section (profiling)")
+    ap.add_argument("--qwen", type=int, default=1, help="Qwen2.5-7B/14B shapes section (BASELINE configs[3]); 0 = skip")
+    ap.add_argument("--qwen-only", action="store_true", help="run only the Qwen section (profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the decode GEMM launches (3 eager steps) and a 256 MiB copy: the workload of "
                          "the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic")
@@ -198,6 +200,161 @@ def make_inputs(args, device):
 
 
 INT8_PEAK_TOPS = 5030.0   # dense INT8 MFMA, 256 CU x 2.4 GHz x 8192 ops/clk
+
+# Qwen2.5 linear shapes (hidden, kv out, mlp)
+QWEN = (("qwen2.5-7b", 3584, 512, 18944), ("qwen2.5-14b", 5120, 1024, 13824))
+
+
+def _groups_of(hidden, kv, mlp):
+    return (("qkv", (hidden, kv, kv), hidden), ("o", (hidden,), hidden),
+            ("gate_up", (mlp, mlp), hidden), ("down", (hidden,), mlp))
+
+
+def _clustered_pack(m, k, frac, gen, cpu_gen, device, cfg):
+    """A bf16 weight with structure (3% of the 64-column input blocks x4, 3% of
+    the 64-row output blocks x3, on top of N(0, 0.02)) and the reference's
+    top-k mask on per-tile sum|W| (k = max(1, ceil(frac * tiles)),
+    src/quantization/decisions.py:176): the BF16 tiles cluster in those bands,
+    so row tiles get very uneven BF16/INT8 mixes."""
+    import torch
+    from tilequant_amd.pack import pack_weight_from_tile_ids
+
+    n_tr, n_tc = m // 64, k // 64
+    W = torch.randn((m, k), generator=gen, device=device, dtype=torch.float32) * 0.02
+    cb = torch.randperm(n_tc, generator=cpu_gen)[: max(1, round(0.03 * n_tc))].to(device)
+    rb = torch.randperm(n_tr, generator=cpu_gen)[: max(1, round(0.03 * n_tr))].to(device)
+    W4 = W.view(n_tr, 64, n_tc, 64)
+    W4[:, :, cb, :] *= 4
+    W4[rb] *= 3
+    W = W.to(torch.bfloat16)
+    scores = W.float().abs().view(n_tr, 64, n_tc, 64).sum(dim=(1, 3)).flatten()
+    kk = max(1, int(math.ceil(frac * n_tr * n_tc)))
+    ids16 = torch.topk(scores, kk).indices.sort().values
+    mask = torch.zeros(n_tr * n_tc, dtype=torch.bool, device=device)
+    mask[ids16] = True
+    ids8 = torch.nonzero(~mask).flatten()
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=ids8.cpu(),
+                                     fp16_tile_ids=ids16.cpu(), cfg=cfg)
+    del W, scores
+    return pack
+
+
+def qwen_measure(args, device):
+    """Qwen2.5-7B / 14B linear shapes with clustered
+    keep10 / keep20 masks.  Decode (4 tokens): a HIP graph of quantize + GEMM
+    over whole layers, as many layers as needed to stream more than 512 MB of
+    distinct packed weights; GEMM kernel time from a graph of the GEMM launches
+    alone.  Prefill (8192 tokens): one layer through MixedLinear."""
+    import statistics as st
+    import torch
+    from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+    from tilequant_amd.mixed_linear import MixedLinear
+    from tilequant_amd.pack import concat_packs_along_rows
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    out = {}
+    s = torch.cuda.Stream()
+
+    def graph_time(fn, reps):
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        with torch.cuda.stream(s):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / reps   # ms
+
+    for model, hidden, kv, mlp in QWEN:
+        groups = _groups_of(hidden, kv, mlp)
+        for keep in (0.10, 0.20):
+            gen = torch.Generator(device=device)
+            gen.manual_seed(args.seed + 11)
+            cpu_gen = torch.Generator(device="cpu")
+            cpu_gen.manual_seed(args.seed + 12)
+            layers, packed, t16, max_row16 = [], 0, 0, 0
+            while packed <= 512 * 1024 * 1024:
+                mods = {}
+                for name, widths, k in groups:
+                    packs = [_clustered_pack(m, k, keep, gen, cpu_gen, device, cfg) for m in widths]
+                    pack = packs[0] if len(packs) == 1 else concat_packs_along_rows(packs)
+                    mods[name] = MixedLinear(pack, None, cfg)
+                    t8, n16 = int(pack.int8_tiles.shape[0]), int(pack.fp16_tiles.shape[0])
+                    packed += 4096 * t8 + 8192 * n16 + 4 * t8
+                    t16 += n16
+                    rp = pack.fp16_row_ptr.cpu()
+                    max_row16 = max(max_row16, int((rp[1:] - rp[:-1]).max()))
+                layers.append(mods)
+            gx = torch.Generator(device="cpu")
+            gx.manual_seed(args.seed + 13)
+            xs = {name: (torch.randn((4, k), generator=gx) * 1.0).to(torch.bfloat16).to(device) for name, _, k in groups}
+            ops = sum(2 * 4 * mods[name].M_orig * mods[name].K_orig for mods in layers for name, _, _ in groups)
+            step_ms = graph_time(lambda: [mods[name](xs[name]) for mods in layers for name, _, _ in groups], 10)
+            quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in groups}
+            outs = {(i, name): torch.empty((4, mods[name].M_orig), device=device, dtype=torch.bfloat16)
+                    for i, mods in enumerate(layers) for name, _, _ in groups}
+
+            def gemms():
+                for i, mods in enumerate(layers):
+                    for name, _, _ in groups:
+                        lin = mods[name]
+                        xq, sx = quant[name]
+                        gemm_mixed_rows_splitk(x_fp=xs[name], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                               int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                               int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                               fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
+                                               M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
+                                               out_dtype=torch.bfloat16, out=outs[(i, name)],
+                                               tile_layout=lin.tile_layout)
+            gemm_ms = graph_time(gemms, 10)
+            n_launch = len(layers) * len(groups)
+            achieved = packed / n_launch / (gemm_ms / n_launch / 1e3) / 1e9
+            dec = {"layers": len(layers), "packed_bytes": packed, "bf16_tiles": t16,
+                   "max_bf16_tiles_per_row_tile": max_row16, "ms_per_step": step_ms,
+                   "tops": ops / (step_ms / 1e3) / 1e12, "gbps_packed_weights": packed / (step_ms / 1e3) / 1e9,
+                   "gemm_avg_launch_us": gemm_ms * 1e3 / n_launch, "gemm_gbps": achieved,
+                   "gemm_hbm_frac": achieved / HBM_PEAK_GBPS}
+            del outs, quant
+            # prefill: one layer, 8192 tokens
+            mods = layers[0]
+            pre = {}
+            pops = 0
+            for name, _, k in groups:
+                x = torch.randn((args.prefill_tokens, k), generator=gx).to(torch.bfloat16).to(device)
+                lin = mods[name]
+                lin(x)
+                torch.cuda.synchronize()
+                times = []
+                for _ in range(3):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    lin(x)
+                    e1.record()
+                    torch.cuda.synchronize()
+                    times.append(e0.elapsed_time(e1))
+                pre[name] = st.median(times)
+                pops += 2 * args.prefill_tokens * lin.M_orig * lin.K_orig
+                del x
+            pms = sum(pre.values())
+            out.setdefault(model, {})[f"keep{int(round(keep * 100)):02d}"] = {
+                "decode_4tok": dec,
+                "prefill": {"tokens": args.prefill_tokens, "layer_ms": pms, "tops": pops / (pms / 1e3) / 1e12,
+                            "frac_int8_peak": pops / (pms / 1e3) / 1e12 / INT8_PEAK_TOPS,
+                            "group_ms": pre}}
+            del layers, mods
+            torch.cuda.empty_cache()
+    out["data"] = ("random-init weights with 3% of input-column and output-row 64-blocks scaled (x4, x3) and the "
+                   "top-k per-tile sum|W| mask; decode activations N(0,1) at 4 tokens")
+    return out
 
 
 def prefill_measure(args, device):
@@ -454,6 +611,9 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_measure(args, device)}), flush=True)
         return
+    if args.qwen_only:
+        print(json.dumps({"qwen": qwen_measure(args, device)}), flush=True)
+        return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)
     if args.traffic_probe:
@@ -617,6 +777,8 @@ def main():
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
     torch.cuda.empty_cache()
+    qwen = qwen_measure(args, device) if args.qwen else None
+    torch.cuda.empty_cache()
     e2e = e2e_measure(args, device) if args.e2e else None
 
     result = {
@@ -651,6 +813,7 @@ def main():
                                "per-launch average includes the inter-kernel gaps"},
         "dense_bf16": dense,
         "prefill": prefill,
+        "qwen": qwen,
         "e2e": e2e,
         "cpu_baseline": cpu,
     }

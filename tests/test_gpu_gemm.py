@@ -406,6 +406,50 @@ def test_prefill_dma_path_ragged_outputs_bias_and_strides(n, m, k, frac):
     assert torch.equal(y16, _gemm(pack, xf_odd, xq_odd, sx, out_dtype=torch.float16))
 
 
+@pytest.mark.parametrize("k,frac", [(3584, 0.10), (18944, 0.20), (5120, 0.20), (13824, 0.10)])
+@pytest.mark.parametrize("n", [4, 300])
+def test_qwen_widths_with_clustered_masks(k, frac, n):
+    """the Qwen2.5-7B / 14B K widths (hidden 3584 / 5120,
+    MLP 18944 / 13824) with BF16 tiles clustered by the top-k per-tile sum|W|
+    rule on a weight with heavy column and row bands, so some row tiles are
+    mostly BF16 and others all INT8.  Decode (4 tokens) and prefill (300)
+    kernels vs the oracle; the prefill DMA kernel bitwise vs the register one."""
+    from oracle import masks as om
+
+    m = 384
+    W = make_w(m, k, seed=k + n).float()
+    n_tr, n_tc = m // 64, k // 64
+    g = torch.Generator().manual_seed(k)
+    cb = torch.randperm(n_tc, generator=g)[: max(1, n_tc // 20)]
+    W.view(n_tr, 64, n_tc, 64)[:, :, cb, :] *= 4
+    W.view(n_tr, 64, n_tc, 64)[1] *= 3
+    W = W.to(torch.bfloat16)
+    scores = W.float().abs().view(n_tr, 64, n_tc, 64).sum(dim=(1, 3)).numpy()
+    ids16 = om.topk_ids(scores, frac)
+    ids8 = complement(ids16, n_tr * n_tc)
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(ids8),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=CFG, tile_layout="mfma")
+    rp = pack.fp16_row_ptr.cpu().numpy()
+    per_row = rp[1:] - rp[:-1]
+    assert per_row.max() > 2 * max(1, per_row.min())   # uneven mixes across row tiles
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=k - n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    y = _gemm(pack, xd, xq, sx)
+    rows = np.unique(np.r_[0:4, n - 4:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc)
+    if n > 64:
+        xq_odd = torch.zeros((n, k + 8), dtype=torch.int8, device="cuda")[:, :k]
+        xq_odd.copy_(xq)
+        xf_odd = torch.zeros((n, k + 4), dtype=xd.dtype, device="cuda")[:, :k]
+        xf_odd.copy_(xd)
+        assert torch.equal(y, _gemm(pack, xf_odd, xq_odd, sx))
+
+
 def test_prefill_rows_longer_than_one_metadata_chunk():
     # 1100 tiles per row tile: the DMA kernel stages tile metadata in chunks of 512
     n, m, k = 80, 128, 64 * 1100

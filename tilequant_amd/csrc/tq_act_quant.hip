@@ -13,6 +13,8 @@
 // Kernels
 //   act_quant_fused      grid n_tc, 256 threads: absmax -> scale -> codes in one
 //                        launch (reference :77-112 for n <= 128; any n works).
+//   act_quant_small      the same for n <= 8 rows: one wave per tile, values
+//                        loaded once, wave-level absmax.
 //   act_absmax_partial   grid (n_tc, n_rb): max over a 256-row block; writes the
 //                        scale directly when n_rb == 1, else a partial.
 //   act_scales_finalize  max over the n_rb partials (fixed order; max is exact
@@ -90,6 +92,30 @@ act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __re
   }
 }
 
+// Few rows (n <= 8, the decode case): one wave per column tile, lane l holds
+// row l / 8, columns 8 (l % 8) .. +7, loaded once; the tile's absmax is a
+// wave reduction (no LDS, no barrier) and the codes come from the same
+// registers.  Same closed form as act_quant_fused_kernel, bit for bit (the
+// absmax is exact and order-free).  Vector layout only: unit column stride,
+// 16-byte aligned rows, k a multiple of 64, 8-byte aligned code rows.
+constexpr int kSmallMaxRows = 8;
+
+template <class T>
+__global__ void __launch_bounds__(kQuantThreads)
+act_quant_small_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, int n_tc) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int c = blockIdx.x * (kQuantThreads / kWave) + (threadIdx.x >> 6);
+  if (c >= n_tc) return;   // whole waves
+  const int row = lane >> 3, col = c * kTile + (lane & 7) * 8;
+  u32x4 w = u32x4{0, 0, 0, 0};
+  if (row < v.n) w = load8(v, row, col);
+  const float a = wave_max_nonneg(max8<T>(w, 0.0f));
+  const float s = act_scale_from_absmax<T>(a);
+  const CodeScale cs(s);
+  if (lane == 0) sx[c] = s;
+  if (row < v.n) *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(w, cs);
+}
+
 template <class T>
 __global__ void __launch_bounds__(kQuantThreads)
 act_absmax_partial_kernel(XView v, float* __restrict__ out, int rows_per_block, int write_scale) {
@@ -160,7 +186,17 @@ extern "C" int tq_act_quant_fused(const void* x, int64_t x_stride_n, int64_t x_s
   if (sx == nullptr || (n > 0 && (q == nullptr || q_stride_n < k))) return TQ_ERR_ARG;
   XView v{static_cast<const uint16_t*>(x), x_stride_n, x_stride_k, n, k};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(n_tiles_of(k));
+  const int n_tc = n_tiles_of(k);
+  if (n > 0 && n <= kSmallMaxRows && x_stride_k == 1 && (x_stride_n % 8) == 0 && aligned16(x) && (k % kTile) == 0 &&
+      (q_stride_n % 8) == 0 && ((uintptr_t)q & 7u) == 0) {
+    const dim3 g((n_tc + kQuantThreads / kWave - 1) / (kQuantThreads / kWave));
+    if (x_dtype == TQ_DTYPE_BF16)
+      hipLaunchKernelGGL(act_quant_small_kernel<Bf16>, g, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx, n_tc);
+    else
+      hipLaunchKernelGGL(act_quant_small_kernel<Fp16>, g, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx, n_tc);
+    return (int)hipGetLastError();
+  }
+  dim3 grid(n_tc);
   if (x_dtype == TQ_DTYPE_BF16)
     hipLaunchKernelGGL(act_quant_fused_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx);
   else

@@ -1476,7 +1476,7 @@ gemm_prefill_v3_kernel(GemmArgs a) {
 constexpr int kP5Threads = 256;
 template <class T> struct TypeTag { using type = T; };
 constexpr int kP5Stages = 3;
-constexpr int kP5MaxCols = 256;   // k <= 16384
+constexpr int kP5MaxCols = 304;   // k <= 19456 (Qwen2.5-7B down: 296 column tiles); LDS 81 KB
 constexpr int kP5OutRow = 272;    // LDS bytes per staged output row (256 + 16: no bank conflicts)
 static_assert(4 * 64 * kP5OutRow <= kP5Stages * kP3Stage, "output staging fits the ring");
 
@@ -1486,7 +1486,7 @@ gemm_prefill_v5_kernel(GemmArgs a) {
   __shared__ __align__(16) int8_t smem[kP5Stages * kP3Stage];
   __shared__ int pos8[2][kP5MaxCols];
   __shared__ float scl[2][kP5MaxCols];
-  __shared__ int list16[2 * kP5MaxCols];   // (q << 9) | (row << 8) | column
+  __shared__ int list16[2 * kP5MaxCols];   // (q << 10) | (row << 9) | column
   constexpr int P = kP5Stages;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1505,7 +1505,7 @@ gemm_prefill_v5_kernel(GemmArgs a) {
     for (int i = t; i < n16; i += kP5Threads) {
       const int j = i >= c0;
       const int q = j ? lo1 + (i - c0) : lo0 + i;
-      list16[i] = (q << 9) | (j << 8) | col_of(a.ids16[q], (r0 + j) * n_tc, n_tc);
+      list16[i] = (q << 10) | (j << 9) | col_of(a.ids16[q], (r0 + j) * n_tc, n_tc);
     }
   }
   for (int i = t; i < 2 * kP5MaxCols; i += kP5Threads) (&pos8[0][0])[i] = -1;
@@ -1578,12 +1578,12 @@ gemm_prefill_v5_kernel(GemmArgs a) {
       } else {
         const int h = (sn - n8s) & 1;
         if (part < 2) {
-          const int col = (meta & 255) * 64 + h * 32;
+          const int col = (meta & 511) * 64 + h * 32;
 #pragma unroll
           for (int i = 2 * part; i < 2 * part + 2; ++i)
             __builtin_amdgcn_global_load_lds(a.xf + xrow16[i] + col, sp + (4 * wave + i) * 1024, 16, 0, 0);
         } else {
-          const int64_t q = (unsigned)meta >> 9;
+          const int64_t q = (unsigned)meta >> 10;
           const uint16_t* wsrc = a.w16 + q * 4096 + w16_off + ((a.layout == TQ_LAYOUT_MFMA) ? h * 512 : h * 32);
           // the same 1 KiB twice keeps the per-step load count at 6
           __builtin_amdgcn_global_load_lds(wsrc, sp + kPfXBytes + wave * 1024, 16, 0, 0);
@@ -2063,7 +2063,7 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                    : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
-    if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 23)) {
+    if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 22)) {
       // DMA ring, 64 x 128 wave tiles, 16-bit tiles in the ring
       const dim3 g5((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
       if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v5_kernel<Bf16>, g5, dim3(kP5Threads), 0, s, a);
