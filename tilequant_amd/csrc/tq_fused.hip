@@ -36,10 +36,19 @@ __device__ inline float wg_max_nonneg(float v, float* red) {
   return r;
 }
 
-// Sum over a wave (every lane receives it), fixed xor-butterfly order.
-__device__ inline float wave_sum(float v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+// Sum over a wave (every lane receives it), fixed order: DPP sums within
+// rows of 16 lanes, then gfx950's v_permlane16_swap / v_permlane32_swap
+// across rows ((r0 + r1) + (r2 + r3) in every lane).
+__device__ inline float wave_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  u2 r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 struct NormArgs {
@@ -65,6 +74,18 @@ add_rmsnorm_quant_kernel(NormArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int c = blockIdx.x;
   const int cpr = a.k >> 3;           // 8-element chunks per row
+  // This workgroup's tile (thread t -> rows wave + 4i, column c*64 + t%64),
+  // loaded first: it does not depend on the row norms, so its round trip
+  // overlaps the row loads below.
+  const int col = c * 64 + lane;
+  uint16_t xt[16], dt[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = min(wave + 4 * i, a.n - 1);
+    xt[i] = a.x[(int64_t)row * a.ldx + col];
+    dt[i] = a.delta ? a.delta[(int64_t)row * a.ldd + col] : (uint16_t)0;
+  }
+  const uint16_t wraw = a.w[col];
   // Passes of kNormBatch chunks per lane: all loads of a pass are issued
   // before the first use (one memory round trip per pass, not per chunk).
   constexpr int kNormBatch = 8;
@@ -94,19 +115,18 @@ add_rmsnorm_quant_kernel(NormArgs a) {
     if (lane == 0) rinv[row] = rsqrtf(ss / (float)a.k + a.eps);
   }
   __syncthreads();
-  // tile c: thread t -> row t / 64 (+4 per pass), column c*64 + t%64
-  const int col = c * 64 + lane;
+  // tile c
   float am = 0.0f;
   float yv[16];
-  const float wv = XT::to_f32(a.w[col]);
+  const float wv = XT::to_f32(wraw);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = wave + 4 * i;
     yv[i] = 0.0f;
     if (row < a.n) {
-      float hv = XT::to_f32(a.x[(int64_t)row * a.ldx + col]);
+      float hv = XT::to_f32(xt[i]);
       if (a.delta) {
-        hv = XT::round(hv + XT::to_f32(a.delta[(int64_t)row * a.ldd + col]));
+        hv = XT::round(hv + XT::to_f32(dt[i]));
         if (a.h) a.h[(int64_t)row * a.ldh + col] = XT::from_f32(hv);
       }
       const float nrm = XT::round(hv * rinv[row]);   // hidden_states.to(input_dtype)
@@ -191,18 +211,21 @@ template <class XT>
 __global__ void __launch_bounds__(64)
 rope_cache_kernel(RopeArgs a) {
   const int b = blockIdx.x, j = blockIdx.y, d = threadIdx.x;
+  // every load first (none depends on the position), then the position check
+  const uint16_t* src = a.qkv + (int64_t)b * a.ldqkv + (int64_t)j * 128;
+  const uint16_t rlo = src[d], rhi = src[d + 64];
+  const uint16_t rc0 = a.cos[d], rc1 = a.cos[d + 64], rs0 = a.sin[d], rs1 = a.sin[d + 64];
   const int64_t p = a.pos[0];
   if (p < 0 || p >= a.max_len) return;   // never indexes outside the cache
-  const uint16_t* src = a.qkv + (int64_t)b * a.ldqkv + (int64_t)j * 128;
-  const float lo = XT::to_f32(src[d]), hi = XT::to_f32(src[d + 64]);
+  const float lo = XT::to_f32(rlo), hi = XT::to_f32(rhi);
   if (j >= a.hq + a.hkv) {   // v head: copy into the cache
     uint16_t* dst = a.v_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq - a.hkv) * a.c_sh + p * a.c_sl;
-    dst[d] = src[d];
-    dst[d + 64] = src[d + 64];
+    dst[d] = rlo;
+    dst[d + 64] = rhi;
     return;
   }
-  const float c0 = XT::to_f32(a.cos[d]), c1 = XT::to_f32(a.cos[d + 64]);
-  const float s0 = XT::to_f32(a.sin[d]), s1 = XT::to_f32(a.sin[d + 64]);
+  const float c0 = XT::to_f32(rc0), c1 = XT::to_f32(rc1);
+  const float s0 = XT::to_f32(rs0), s1 = XT::to_f32(rs1);
   const float o0 = XT::round(XT::round(lo * c0) + XT::round(-hi * s0));
   const float o1 = XT::round(XT::round(hi * c1) + XT::round(lo * s1));
   uint16_t* dst = (j < a.hq) ? a.q_out + (int64_t)b * a.q_sb + (int64_t)j * a.q_sh
