@@ -359,7 +359,7 @@ def qwen_measure(args, device):
 
 def prefill_measure(args, device):
     """one Llama-3.2-3B layer's QKV/O/GateUp/Down at
-    prefill_tokens rows (MixedLinear: whole-input scales, 4096-row chunks),
+    prefill_tokens rows (MixedLinear: whole-input scales, default row chunk),
     keep05 uniform masks.  Compute-bound: reported against INT8 MFMA peak."""
     import numpy as np
     import torch
@@ -391,7 +391,7 @@ def prefill_measure(args, device):
             "tops": info["ops"] / (total_ms / 1e3) / 1e12,
             "frac_int8_peak": info["ops"] / (total_ms / 1e3) / 1e12 / INT8_PEAK_TOPS,
             "group_ms": per, "ops_per_layer": info["ops"], "bf16_tiles": info["t16"],
-            "note": "MixedLinear forward per group (scales over all rows, 2 x 4096-row chunks of quantize + "
+            "note": "MixedLinear forward per group (scales over all rows, then one quantize + one "
                     "GEMM), HIP events, median of 5"}
 
 

@@ -5,10 +5,15 @@ projection groups and sibling-activation cache as the reference
 (mixed_linear.py:24-392):
 
 * ``forward`` accepts [N, K] or [B, T, K]; inputs of up to
-  ``activation_row_chunk_size`` (default 4096) rows are quantized and
-  multiplied in one call, larger inputs get scales over the WHOLE input and
-  are then quantized and multiplied in row chunks that write straight into
-  one output (mixed_linear.py:229-250).
+  ``activation_row_chunk_size`` rows are quantized and multiplied in one
+  call, larger inputs get scales over the WHOLE input and are then quantized
+  and multiplied in row chunks that write straight into one output
+  (mixed_linear.py:229-250).  The default chunk is 16384 rows (the
+  reference's is 4096): the INT8 copy of even a 16384 x 18944 input is 310 MB,
+  small against 288 GB of HBM, and one GEMM launch over a whole 8192-token
+  prefill fills the GPU better than two (measured 16% faster per layer).
+  Chunking never changes the output: the scales are over the whole input
+  either way and rows are independent.
 * Q/K/V and Gate/Up siblings can be stacked into one ``MixedLinearGroup``
   (one quantization + one GEMM per group), each member served a column slice.
 
@@ -41,7 +46,7 @@ from .quant_utils import (
     quantize_activation_tile_with_scales,
 )
 
-DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 4096
+DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 16384
 # Rows up to which cfg.fused_decode = "auto" fuses quantization into the GEMM
 # (measured on MI355X: 1 row saves ~2 us per projection, 4 rows break even).
 FUSED_AUTO_MAX_ROWS = 2
