@@ -684,7 +684,16 @@ gemm_decode_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int T = blockDim.x, W = T >> 6;
-  const int unit = blockIdx.x;
+  // Workgroups are dealt to the 8 XCDs round-robin, so ids b, b+8, b+16, b+24
+  // share an XCD: with one j-block per workgroup they take the four quarters
+  // of the same row tile, back to back (each 4 KiB tile is then read by one
+  // XCD in close succession instead of by four; a bijection on the units
+  // when n_tr % 8 == 0, the identity otherwise).
+  int unit = blockIdx.x;
+  if (NJG == 4 && (a.n_tr & 7) == 0) {
+    const int b = blockIdx.x, xcd = b & 7, slot = b >> 3;
+    unit = (((slot >> 2) << 3) + xcd) * 4 + (slot & 3);
+  }
   const int r = unit / NJG, jb0 = (unit - (unit / NJG) * NJG) * JBW;
   const int arow = lane & 15, akq = lane >> 4;
   const int rbase = r * a.n_tc;
