@@ -497,7 +497,7 @@ def e2e_measure(args, device):
     dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
     res["tilequant_graph"] = run(graph_request, dec)
     res["tilequant_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
-    res["tilequant_graph"]["decode_step"] = "fused (10 launches per layer)" if dec._fused else "model forward"
+    res["tilequant_graph"]["decode_step"] = "fused (9 launches per layer)" if dec._fused else "model forward"
     dec.close()
     del dec
     if args.e2e_module_path:

@@ -170,6 +170,23 @@ int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int64_t q_strid
                               int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
                               float scale, float* workspace, int64_t workspace_elems, void* stream);
 
+/* tq_rope_cache followed by tq_decode_attention (q_out NULL) or
+ * tq_decode_attention_quant, in one split pass: qkv is the stacked [batch,
+ * (q_heads + 2 kv_heads) * 128] q/k/v projection output (row stride
+ * qkv_stride); the split kernel applies RoPE to the q heads it reads, and the
+ * workgroup whose 128-key chunk holds *position writes that token's rotated k
+ * and its v into the caches (nothing is written when *position is outside
+ * [0, max_len)) and uses them in registers.  Outputs, codes, scales and cache
+ * contents are bitwise those of the two-launch sequence.  No reference
+ * counterpart: it fuses the Hugging Face rotary embedding and StaticCache
+ * update that precede _cuda_graph_attention (src/runtime/graph_decode.py:56-71). */
+int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+                             const int64_t* position, void* k_cache, void* v_cache, int64_t cache_stride_b,
+                             int64_t cache_stride_l, int64_t cache_stride_h, const int32_t* seq_used, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b,
+                             float* sx_out, int dtype, int batch, int q_heads, int kv_heads, int head_dim,
+                             int max_len, float scale, float* workspace, int64_t workspace_elems, void* stream);
+
 /* ---- decode-step producers fused with the activation quantization ---------
  * Each computes a decoder-layer step that feeds a mixed tile GEMM and, when
  * q_out is non-null, quantizes its output like tq_act_quant_fused (scales over

@@ -332,6 +332,72 @@ def test_attention_quant_equals_attention_then_quantizer():
     assert torch.equal(qo, q_ref) and torch.equal(sx, sx_ref)
 
 
+@pytest.mark.parametrize("B,hq,hkv,L,pos,quant", [(4, 24, 8, 2304, 2047, True), (4, 24, 8, 700, 128, False),
+                                                    (2, 7, 1, 300, 0, True), (3, 40, 8, 513, 127, True),
+                                                    (1, 8, 2, 256, 255, False), (2, 24, 8, 300, 300, True)])
+def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, quant):
+    """tq_decode_attention_rope against tq_rope_cache followed by
+    tq_decode_attention(_quant): outputs, codes, scales and both caches
+    bitwise equal.  Positions at chunk edges (0, 127, 128, 255) and in the
+    middle; seq_used = position + 1 except one row whose length stops short of
+    the new key (it must not be read); pos == L writes nothing."""
+    D = 128
+    g = torch.Generator().manual_seed(B * 31 + pos)
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(DEV)
+    ang = torch.randn(D, generator=g) * 3
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    kc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    vc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    position = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    seq = torch.full((B,), min(pos + 1, L), dtype=torch.int32, device=DEV)
+    if B > 1:
+        seq[1] = max(pos - 5, 1)
+    ws = decode_attention_workspace(B, hq, L, DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    code = 0
+
+    def outputs():
+        return (torch.full((B, hq * D), 7.0, dtype=torch.bfloat16, device=DEV),
+                torch.zeros((B, hq * D), dtype=torch.int8, device=DEV),
+                torch.zeros((hq * D // 64,), dtype=torch.float32, device=DEV))
+
+    # two launches
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    q_rot = torch.empty((B, hq, D), dtype=torch.bfloat16, device=DEV)
+    rc = nat.lib().tq_rope_cache(qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), position.data_ptr(),
+                                 q_rot.data_ptr(), q_rot.stride(0), q_rot.stride(1), kc1.data_ptr(), vc1.data_ptr(),
+                                 kc1.stride(0), kc1.stride(1), kc1.stride(2), code, B, hq, hkv, D, L, stream)
+    assert rc == 0
+    if pos >= L:   # tq_rope_cache leaves q untouched for a position outside the cache: rotate it here
+        from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+        qh = qkv[:, :hq * D].view(B, 1, hq, D).transpose(1, 2)
+        q_rot.copy_(apply_rotary_pos_emb(qh, qh, cos.view(1, 1, D), sin.view(1, 1, D))[0][:, :, 0])
+    out1, qo1, sx1 = outputs()
+    args = (q_rot.data_ptr(), q_rot.stride(0), q_rot.stride(1), kc1.data_ptr(), vc1.data_ptr(), kc1.stride(0),
+            kc1.stride(2), kc1.stride(1), seq.data_ptr(), out1.data_ptr(), out1.stride(0), D)
+    tail = (code, B, hq, hkv, D, L, D ** -0.5, ws.data_ptr(), ws.numel(), stream)
+    if quant:
+        rc = nat.lib().tq_decode_attention_quant(*args, qo1.data_ptr(), qo1.stride(0), sx1.data_ptr(), *tail)
+    else:
+        rc = nat.lib().tq_decode_attention(*args, *tail)
+    assert rc == 0
+    # one split pass
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    out2, qo2, sx2 = outputs()
+    rc = nat.lib().tq_decode_attention_rope(
+        qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), position.data_ptr(), kc2.data_ptr(),
+        vc2.data_ptr(), kc2.stride(0), kc2.stride(2), kc2.stride(1), seq.data_ptr(), out2.data_ptr(), out2.stride(0),
+        D, qo2.data_ptr() if quant else None, qo2.stride(0), sx2.data_ptr() if quant else None, code, B, hq, hkv, D,
+        L, D ** -0.5, ws.data_ptr(), ws.numel(), stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out1)
+    assert torch.equal(qo2, qo1) and torch.equal(sx2, sx1)
+    assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
+    if pos < L:
+        assert not torch.equal(kc2[:, :, pos], kc0[:, :, pos])
+
+
 @pytest.mark.parametrize("family", ["llama", "qwen"])
 def test_fused_decode_step_matches_module_forward(family):
     """The fused one-token step against the model's own forward in the same

@@ -406,6 +406,32 @@ def test_prefill_dma_path_ragged_outputs_bias_and_strides(n, m, k, frac):
     assert torch.equal(y16, _gemm(pack, xf_odd, xq_odd, sx, out_dtype=torch.float16))
 
 
+@pytest.mark.parametrize("n,m,k,frac", [(8192, 3072, 256, 0.25), (8192, 3000, 320, 0.1), (8192, 5120, 128, 0.3),
+                                         (4096, 4096, 128, 0.3)])
+def test_prefill_dma_path_full_grid_at_8192_tokens(n, m, k, frac):
+    """Llama o/down and qkv widths at 8192 tokens (768 and 1280 row-pair x
+    token-block workgroups, more than one round of the 512 workgroup slots
+    of a 256-CU MI355X; m = 3000 leaves the last pair with one row tile; the
+    last case fills the slots exactly).  Bitwise equal to the register-staged
+    kernel, and within tolerance of the oracle on rows of the first, middle
+    and last token blocks."""
+    W, pack, ids16 = _case(m, k, frac, seed=m + k)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=n + k)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    y = _gemm(pack, xd, xq, sx)
+    xq_odd = torch.zeros((n, k + 8), dtype=torch.int8, device="cuda")[:, :k]
+    xq_odd.copy_(xq)
+    xf_odd = torch.zeros((n, k + 4), dtype=xd.dtype, device="cuda")[:, :k]
+    xf_odd.copy_(xd)
+    assert torch.equal(y, _gemm(pack, xf_odd, xq_odd, sx))
+    rows = np.unique(np.r_[0:3, n // 2:n // 2 + 3, n - 300:n - 297, n - 3:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc)
+
+
 @pytest.mark.parametrize("k,frac", [(3584, 0.10), (18944, 0.20), (5120, 0.20), (13824, 0.10)])
 @pytest.mark.parametrize("n", [4, 300])
 def test_qwen_widths_with_clustered_masks(k, frac, n):

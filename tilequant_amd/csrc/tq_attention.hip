@@ -25,6 +25,13 @@
 //   the 4 waves' partials (max, sum, o) are combined through LDS in wave
 //       order, rescaled to the chunk max, with one barrier.
 // Everything accumulates in fp32; results are bitwise reproducible.
+//
+// RoPE form (tq_decode_attention_rope): the split kernel reads q from the
+// stacked q/k/v projection output and applies RoPE itself, each (head, 8-element
+// chunk) once, shared through LDS; the workgroup whose chunk holds the new
+// position writes that token's rotated k and its v into the caches and
+// substitutes them for the rows it loaded before writing.  This replaces a
+// separate RoPE + cache-write launch per layer, bit for bit.
 #include "tq_common.h"
 
 namespace tq {
@@ -47,7 +54,39 @@ struct AttnArgs {
   float* part;       // [batch * q_heads][n_splits][D + 2]
   int batch, q_heads, kv_heads, G, max_len, n_splits;
   float scale_log2;  // scale * log2(e)
+  // RoPE-fused form: q (= qkv rows) is the raw stacked projection output
+  // [batch, (q_heads + 2 kv_heads) * D] with row stride q_sb; the new token's
+  // rotated k and raw v go to the caches at *pos.
+  const uint16_t* cos;   // [D] at the position
+  const uint16_t* sin;
+  const int64_t* pos;
+  uint16_t* k_out;       // the k / v caches, writable
+  uint16_t* v_out;
 };
+
+// RoPE of one 8-element chunk (HF apply_rotary_pos_emb: q * cos +
+// rotate_half(q) * sin, each product and the sum rounded to the 16-bit type):
+// own = elements 8ch .. 8ch+7 of the head, partner = those of chunk ch ^ 8
+// (d +- 64); the first half subtracts partner * sin, the second adds it.
+template <class XT>
+__device__ inline u32x4 rope8(u32x4 own, u32x4 partner, u32x4 c, u32x4 sn, bool first_half) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float x = XT::to_f32((uint16_t)(own[i] >> (16 * j)));
+      const float y = XT::to_f32((uint16_t)(partner[i] >> (16 * j)));
+      const float cc = XT::to_f32((uint16_t)(c[i] >> (16 * j)));
+      const float ss = XT::to_f32((uint16_t)(sn[i] >> (16 * j)));
+      const float o = XT::round(XT::round(x * cc) + XT::round((first_half ? -y : y) * ss));
+      w |= (uint32_t)XT::from_f32(o) << (16 * j);
+    }
+    r[i] = w;
+  }
+  return r;
+}
 
 // sum over the 16 lanes of a DPP row (every lane receives the sum)
 __device__ inline float row16_sum(float x) {
@@ -88,7 +127,7 @@ __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
   }
 }
 
-template <class XT, int G>
+template <class XT, int G, bool ROPE>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_split_kernel(AttnArgs a) {
   constexpr int kWaves = kAttnThreads / kWave;
@@ -105,9 +144,34 @@ attn_split_kernel(AttnArgs a) {
   // ---- every load of the workgroup is issued up front: q, then all K and V
   //      rows of this wave's keys (keys past the valid length are not read)
   u32x4 qw[G];
+  if constexpr (!ROPE) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    qw[g] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8);
+    for (int g = 0; g < G; ++g)
+      qw[g] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8);
+  }
+  // RoPE form: thread t < 16 (G + 2) owns chunk ich of item it -- query head
+  // g < G, the new token's k (it = G) or v (it = G + 1) -- and loads that
+  // chunk, its RoPE partner chunk ich ^ 8 and cos / sin; none of these loads
+  // depends on another.  Each (item, chunk) is rotated once and shared through
+  // LDS (every lane needs all of them for its own chunk).
+  __shared__ u32x4 rq[ROPE ? G + 2 : 1][16];
+  const int it = t >> 4, ich = t & 15;
+  u32x4 own{}, partner{}, cw{}, sw{};
+  int64_t pos = -1;
+  if constexpr (ROPE) {
+    if (it < G + 2) {
+      const uint16_t* row = a.q + (int64_t)b * a.q_sb;
+      const int64_t head = it < G ? (int64_t)(kvh * G + it) * a.q_sh
+                                  : (int64_t)(a.q_heads + (it - G) * a.kv_heads + kvh) * kAttnD;
+      own = *reinterpret_cast<const u32x4*>(row + head + ich * 8);
+      if (it <= G) {
+        partner = *reinterpret_cast<const u32x4*>(row + head + (ich ^ 8) * 8);
+        cw = *reinterpret_cast<const u32x4*>(a.cos + ich * 8);
+        sw = *reinterpret_cast<const u32x4*>(a.sin + ich * 8);
+      }
+    }
+    pos = a.pos[0];
+  }
   // K/V rows through buffer resources spanning the valid prefix of this
   // (b, kv head): keys past seq_used read as 0 without touching memory, so
   // every load is unconditional and all of them stay in flight together.
@@ -125,6 +189,28 @@ attn_split_kernel(AttnArgs a) {
     vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first use
+  // RoPE form: the workgroup whose chunk holds the new position writes the
+  // token's rotated k and its v into the caches (the bytes tq_rope_cache
+  // writes) and uses them in registers for that key (pk; -1 elsewhere): its
+  // own cache rows were loaded before they were written.  The substitution is
+  // a per-lane select at each row's first use, so no wait for the other rows.
+  u32x4 kn{}, vnw{};
+  int pk = -1;
+  if constexpr (ROPE) {
+    const bool mine = pos >= 0 && pos < a.max_len && pos / kAttnChunk == s;
+    if (it < G + 2) {
+      const u32x4 r = it <= G ? rope8<XT>(own, partner, cw, sw, ich < 8) : own;
+      rq[it][ich] = r;
+      if (it >= G && mine)
+        *reinterpret_cast<u32x4*>((it == G ? a.k_out : a.v_out) + kv_base + pos * a.kv_sl + ich * 8) = r;
+    }
+    lds_barrier();   // the K/V loads stay in flight
+#pragma unroll
+    for (int g = 0; g < G; ++g) qw[g] = rq[g][ch];
+    kn = rq[G][ch];
+    vnw = rq[G + 1][ch];
+    if (mine) pk = (int)pos;
+  }
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) unpack8<XT>(qw[g], qv[g]);
@@ -133,9 +219,10 @@ attn_split_kernel(AttnArgs a) {
   float sco[kSteps][G];   // scaled scores (log2 units) of the lane's key per step
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
-    const bool valid = key0 + wave * (4 * kSteps) + 4 * i + kl < len;
+    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
+    const bool valid = key < len;
     float kf[8];
-    unpack8<XT>(kw[i], kf);
+    unpack8<XT>((ROPE && key == pk) ? kn : kw[i], kf);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float d = 0.0f;
@@ -172,7 +259,8 @@ attn_split_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
     float vf[8];
-    unpack8<XT>(vw[i], vf);
+    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
+    unpack8<XT>((ROPE && key == pk) ? vnw : vw[i], vf);
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -311,18 +399,18 @@ attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* 
 
 static int attn_splits(int max_len) { return (max_len + kAttnChunk - 1) / kAttnChunk; }
 
-template <class XT>
+template <class XT, bool ROPE = false>
 static void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(kAttnThreads);
   switch (a.G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<XT, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<XT, 2>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((attn_split_kernel<XT, 3>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<XT, 4>), grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL((attn_split_kernel<XT, 5>), grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL((attn_split_kernel<XT, 6>), grid, block, 0, s, a); break;
-    case 7: hipLaunchKernelGGL((attn_split_kernel<XT, 7>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<XT, 8>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<XT, 1, ROPE>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<XT, 2, ROPE>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((attn_split_kernel<XT, 3, ROPE>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<XT, 4, ROPE>), grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((attn_split_kernel<XT, 5, ROPE>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((attn_split_kernel<XT, 6, ROPE>), grid, block, 0, s, a); break;
+    case 7: hipLaunchKernelGGL((attn_split_kernel<XT, 7, ROPE>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<XT, 8, ROPE>), grid, block, 0, s, a); break;
   }
 }
 
@@ -408,6 +496,42 @@ extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int6
   } else {
     launch_split<Fp16>(a, g1, s);
     hipLaunchKernelGGL(attn_merge_quant_kernel<Fp16>, g2, dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+                                        const int64_t* position, void* k_cache, void* v_cache,
+                                        int64_t cache_stride_b, int64_t cache_stride_l, int64_t cache_stride_h,
+                                        const int32_t* seq_used, void* out, int64_t out_stride_b,
+                                        int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b,
+                                        float* sx_out, int dtype, int batch, int q_heads, int kv_heads,
+                                        int head_dim, int max_len, float scale, float* workspace,
+                                        int64_t workspace_elems, void* stream) {
+  if (q_out != nullptr && (batch > kMergeQuantMaxRows || sx_out == nullptr)) return TQ_ERR_ARG;
+  if (batch > 0 && max_len > 0 && (!cos || !sin || !position)) return TQ_ERR_ARG;
+  if ((cos && !aligned16(cos)) || (sin && !aligned16(sin))) return TQ_ERR_ALIGN;
+  if (qkv_stride < (int64_t)(q_heads + 2 * kv_heads) * head_dim) return TQ_ERR_ARG;
+  AttnArgs a{};
+  const int rc = attn_setup(a, qkv, qkv_stride, head_dim, k_cache, v_cache, cache_stride_b, cache_stride_l,
+                            cache_stride_h, seq_used, out, out_stride_b, out_stride_h, dtype, batch, q_heads,
+                            kv_heads, head_dim, max_len, scale, workspace, workspace_elems);
+  if (rc != 1) return rc;
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.pos = position;
+  a.k_out = static_cast<uint16_t*>(k_cache);
+  a.v_out = static_cast<uint16_t*>(v_cache);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g1(a.n_splits, batch * kv_heads);
+  if (dtype == TQ_DTYPE_BF16) {
+    launch_split<Bf16, true>(a, g1, s);
+    if (q_out) hipLaunchKernelGGL(attn_merge_quant_kernel<Bf16>, dim3(q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+    else hipLaunchKernelGGL(attn_merge_kernel<Bf16>, dim3(batch * q_heads), dim3(kAttnD), 0, s, a);
+  } else {
+    launch_split<Fp16, true>(a, g1, s);
+    if (q_out) hipLaunchKernelGGL(attn_merge_quant_kernel<Fp16>, dim3(q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+    else hipLaunchKernelGGL(attn_merge_kernel<Fp16>, dim3(batch * q_heads), dim3(kAttnD), 0, s, a);
   }
   return (int)hipGetLastError();
 }

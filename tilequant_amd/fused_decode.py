@@ -6,15 +6,15 @@ layers, final norm, LM head -- with per layer:
 
   add_rmsnorm_quant  residual add + input RMSNorm + INT8 codes of the result
   QKV GEMM           stacked Q/K/V MixedLinear on the codes (or F.linear)
-  rope_cache         RoPE on q/k, k/v written into the cache at the position
-  decode attention   split kernel + merge that also quantizes for O
+  decode attention   split kernel that applies RoPE to q/k and writes the new
+                     token's k/v into the cache, + merge that quantizes for O
   O GEMM
   add_rmsnorm_quant  residual add + post-attention RMSNorm + codes
   Gate/Up GEMM       stacked
   silu_mul_quant     SiLU(gate) * up + codes
   Down GEMM
 
-i.e. 10 launches per layer where the modules issue ~40 (norm, RoPE, cache
+i.e. 9 launches per layer where the modules issue ~40 (norm, RoPE, cache
 update, residual and activation elementwise kernels, one quantization per
 GEMM).  The arithmetic follows the modules op by op (see csrc/tq_fused.hip);
 the GEMMs are exactly the MixedLinear kernels on exactly the activation
@@ -103,7 +103,6 @@ class FusedDecodeStep:
         self.y = e(B, H)
         self.yq, self.ysx = e(B, H, d=torch.int8), e(H // 64, d=torch.float32)
         self.qkv_out = e(B, qkv_w)
-        self.q_rot = e(B, self.hq, self.head_dim)
         self.attn = e(B, self.hq * self.head_dim)
         self.aq = e(B, self.hq * self.head_dim, d=torch.int8)
         self.asx = e(self.hq * self.head_dim // 64, d=torch.float32)
@@ -162,24 +161,17 @@ class FusedDecodeStep:
             self._linear(ly.qkv, self.y, self.yq, self.ysx, self.qkv_out)
             layer_cache = self.cache.layers[li]
             kc, vc = layer_cache.keys, layer_cache.values
-            rc = nat.lib().tq_rope_cache(
-                nat.ptr(self.qkv_out), self.qkv_out.stride(0), nat.ptr(cos), nat.ptr(sin), nat.ptr(position),
-                nat.ptr(self.q_rot), self.q_rot.stride(0), self.q_rot.stride(1), nat.ptr(kc), nat.ptr(vc),
-                kc.stride(0), kc.stride(1), kc.stride(2), self.code, B, self.hq, self.hkv, self.head_dim, self.L,
-                stream)
-            nat.check(rc, "tq_rope_cache")
+            # RoPE, the cache write of the new token and attention (+ the O
+            # projection's quantization) in one split pass and one merge
             q8o = self._quantized(ly.o)
-            args = (nat.ptr(self.q_rot), self.q_rot.stride(0), self.q_rot.stride(1), nat.ptr(kc), nat.ptr(vc),
-                    kc.stride(0), kc.stride(2), kc.stride(1), nat.ptr(seq_used), nat.ptr(self.attn),
-                    self.attn.stride(0), self.head_dim)
-            tail = (self.code, B, self.hq, self.hkv, self.head_dim, self.L, self.scale, nat.ptr(self.attn_ws),
-                    self.attn_ws.numel(), stream)
-            if q8o:
-                rc = nat.lib().tq_decode_attention_quant(*args, nat.ptr(self.aq), self.aq.stride(0),
-                                                         nat.ptr(self.asx), *tail)
-            else:
-                rc = nat.lib().tq_decode_attention(*args, *tail)
-            nat.check(rc, "tq_decode_attention")
+            rc = nat.lib().tq_decode_attention_rope(
+                nat.ptr(self.qkv_out), self.qkv_out.stride(0), nat.ptr(cos), nat.ptr(sin), nat.ptr(position),
+                nat.ptr(kc), nat.ptr(vc), kc.stride(0), kc.stride(2), kc.stride(1), nat.ptr(seq_used),
+                nat.ptr(self.attn), self.attn.stride(0), self.head_dim,
+                nat.ptr(self.aq) if q8o else None, self.aq.stride(0), nat.ptr(self.asx) if q8o else None,
+                self.code, B, self.hq, self.hkv, self.head_dim, self.L, self.scale, nat.ptr(self.attn_ws),
+                self.attn_ws.numel(), stream)
+            nat.check(rc, "tq_decode_attention_rope")
             self._linear(ly.o, self.attn, self.aq, self.asx, self.o_out)
             k ^= 1
             h2 = self.h[k]

@@ -17,9 +17,10 @@ ROCm specifics (this build's own design):
   token-major re-layout is needed.
 * Prefill attention is SDPA restricted to the fused flash / memory-efficient
   backends (causal, grouped-query); the unfused math backend is never used.
-* The one-token step runs ``FusedDecodeStep`` (10 launches per decoder layer:
-  residual + RMSNorm + INT8 quantization, RoPE + cache write, attention whose
-  merge quantizes for O, SiLU * up + quantization, four GEMMs) for Llama /
+* The one-token step runs ``FusedDecodeStep`` (9 launches per decoder layer:
+  residual + RMSNorm + INT8 quantization, attention with RoPE and the cache
+  write in its split kernel and a merge that quantizes for O, SiLU * up +
+  quantization, four GEMMs) for Llama /
   Qwen2 layouts with head_dim 128 and up to 16 sequences; ``fused_decode=False``
   (or any other architecture) replays the model's own forward as the reference
   does.
