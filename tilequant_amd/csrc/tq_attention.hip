@@ -118,6 +118,28 @@ __device__ inline float rows4_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Dot product of 8 packed 16-bit values with an fp32 accumulator, two
+// products per v_dot2 instruction (exact products, fp32 sums) -- half the
+// instructions of unpacking both operands and chaining fmas.
+template <class XT>
+__device__ inline float dot8(u32x4 x, u32x4 y, float acc) {
+  if constexpr (std::is_same<XT, Bf16>::value) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const v8bf xv = __builtin_bit_cast(v8bf, x), yv = __builtin_bit_cast(v8bf, y);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 0, 1), __builtin_shufflevector(yv, yv, 0, 1), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 2, 3), __builtin_shufflevector(yv, yv, 2, 3), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 4, 5), __builtin_shufflevector(yv, yv, 4, 5), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 6, 7), __builtin_shufflevector(yv, yv, 6, 7), acc, false);
+  } else {
+    const v8h xv = __builtin_bit_cast(v8h, x), yv = __builtin_bit_cast(v8h, y);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(xv, xv, 0, 1), __builtin_shufflevector(yv, yv, 0, 1), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(xv, xv, 2, 3), __builtin_shufflevector(yv, yv, 2, 3), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(xv, xv, 4, 5), __builtin_shufflevector(yv, yv, 4, 5), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(xv, xv, 6, 7), __builtin_shufflevector(yv, yv, 6, 7), acc, false);
+  }
+  return acc;
+}
+
 template <class XT>
 __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
 #pragma unroll
@@ -211,9 +233,6 @@ attn_split_kernel(AttnArgs a) {
     vnw = rq[G + 1][ch];
     if (mine) pk = (int)pos;
   }
-  float qv[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) unpack8<XT>(qw[g], qv[g]);
 
   // ---- QK: 16 lanes per key row, partial dots summed across the row with DPP
   float sco[kSteps][G];   // scaled scores (log2 units) of the lane's key per step
@@ -221,14 +240,10 @@ attn_split_kernel(AttnArgs a) {
   for (int i = 0; i < kSteps; ++i) {
     const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
     const bool valid = key < len;
-    float kf[8];
-    unpack8<XT>((ROPE && key == pk) ? kn : kw[i], kf);
+    const u32x4 kk = (ROPE && key == pk) ? kn : kw[i];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float d = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
-      d = row16_sum(d);
+      const float d = row16_sum(dot8<XT>(qw[g], kk, 0.0f));
       sco[i][g] = valid ? d * a.scale_log2 : -INFINITY;
     }
   }
@@ -307,7 +322,7 @@ attn_split_kernel(AttnArgs a) {
 // batches of kMergeBatch splits, every load of a batch issued before its
 // first use.  With at most kMergeBatch splits this is the plain two-pass
 // formula (global max, then the weighted sums in split order).
-constexpr int kMergeBatch = 16;
+constexpr int kMergeBatch = 32;
 
 __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d) {
   float M = -INFINITY, L = 0.0f, acc = 0.0f;
