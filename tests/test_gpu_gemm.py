@@ -247,6 +247,26 @@ def test_fused_equals_two_launch_path_bitwise(n):
     assert_gemm_close(y1, acc, sab, 48)
 
 
+@pytest.mark.parametrize("m,k", [(16384, 3072), (9216, 3584)])
+@pytest.mark.parametrize("n", [1, 2, 4, 16])
+def test_fused_equals_two_launch_path_on_many_unit_grids(m, k, n):
+    """Grids of more than 512 one-j-block workgroups (stacked gate/up widths)
+    take 4-wave workgroups with 12- or 16-tile batches: the fused and the
+    two-launch paths (and the split-K kernel with one split) still sum the
+    same terms in the same order."""
+    W, pack, ids16 = _case(m, k, 0.01, seed=950 + n + k)
+    x = make_x(n, k, seed=951 + n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y2 = _gemm(pack, xd, xq, sx)
+    for split_k in (None, 1):
+        assert torch.equal(_fused(pack, xd, split_k=split_k), y2), f"split_k={split_k}"
+        assert torch.equal(_gemm(pack, xd, xq, sx, split_k=split_k), y2)
+    op = oracle_pack(W, ids16)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y2, acc, sab, pack.n_tc)
+
+
 @pytest.mark.parametrize("n", [1, 4, 8, 16])
 def test_fused_equals_two_launch_path_on_whole_tile_schedule(n):
     """Stacked gate/up width (256 row tiles): whole-tile workgroups."""

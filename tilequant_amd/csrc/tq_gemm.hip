@@ -1847,8 +1847,23 @@ static int plan_max_waves(int jbw, int tb) {
 #ifndef TQ_DEC_UMAX_JB4
 #define TQ_DEC_UMAX_JB4 6
 #endif
-static int decode_waves(int jbw, int n_tc) {
-  const int umax = jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+// Grids of more than kDecManyUnits one-j-block workgroups run several per CU;
+// there a wave count that is not a multiple of 4 (e.g. 6 waves for 48 column
+// tiles) leaves wave slots of the four SIMDs unusable, and only ~3 of the 4
+// workgroups per CU that the registers allow start together (measured on
+// MI355X for the stacked gate/up projection: 1024 workgroups, ~770 in the first
+// round).  Those grids use 4 waves with batches of up to 16 tiles (32 < n_tc
+// <= 64): 6% faster there, slower on grids of <= 2 workgroups per CU.
+constexpr int kDecManyUnits = 512;
+static bool decode_wide_batches(int jbw, int tb, int units, int n_tc) {
+  return jbw == 1 && tb == 1 && units > kDecManyUnits && n_tc > 32 && n_tc <= 64;
+}
+static int decode_umax(int jbw, int tb, int units, int n_tc) {
+  if (decode_wide_batches(jbw, tb, units, n_tc)) return n_tc <= 48 ? 12 : 16;
+  return jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+}
+static int decode_waves(int jbw, int tb, int units, int n_tc) {
+  const int umax = decode_umax(jbw, tb, units, n_tc);
   const int wmax = jbw == 1 ? 16 : 8;
   int W = (n_tc + umax - 1) / umax;
   return W < 4 ? 4 : (W > wmax ? wmax : W);
@@ -1863,7 +1878,7 @@ static SplitPlan plan_split(int n, int n_tr, int n_tc, int split_k) {
   if (p.S > 1 && units > kCounterCap) p.S = 1;
   const int per_split = (n_tc + p.S - 1) / p.S;
   const int U = plan_u(p.jbw, p.tb);
-  int W = p.S == 1 ? decode_waves(p.jbw, n_tc) : (per_split + U - 1) / U;
+  int W = p.S == 1 ? decode_waves(p.jbw, p.tb, units, n_tc) : (per_split + U - 1) / U;
   const int wmax = plan_max_waves(p.jbw, p.tb);
   if (W > wmax) W = wmax;
   p.W = W < 1 ? 1 : W;
@@ -1945,9 +1960,10 @@ static DecodePlan plan_decode(int n, int k, int n_tr, int n_tc, bool quant) {
   p.ok = false;
   p.tb = pick_tb(n);
   p.jbw = pick_jbw(n, n_tr);
-  p.umax = p.jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+  const int units = n_tr * (4 / p.jbw);
+  p.umax = decode_umax(p.jbw, p.tb, units, n_tc);
   if (n < 1 || n > kDecodeMaxTokens || k != n_tc * 64 || (quant && n > kFusedMaxTokens)) return p;
-  const int W = decode_waves(p.jbw, n_tc);
+  const int W = decode_waves(p.jbw, p.tb, units, n_tc);
   p.W = W;
   const int64_t T = (int64_t)W * kWave;
   const int64_t codes = (int64_t)n * (k + 16);
@@ -1998,7 +2014,10 @@ static hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, hipStrea
     else if (p.tb == 1) launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
     else launch_decode_c<XT, 2, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
   } else {
-    if constexpr (QUANT) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
+    // p.umax is TQ_DEC_UMAX_JB1 except for many-unit grids with one token block
+    if (p.tb == 1 && p.umax == 12) launch_decode_c<XT, 1, 1, 12, QUANT>(a, p, s);
+    else if (p.tb == 1 && p.umax == 16) launch_decode_c<XT, 1, 1, 16, QUANT>(a, p, s);
+    else if constexpr (QUANT) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
     else if (p.tb == 1) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
     else launch_decode_c<XT, 2, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
   }
