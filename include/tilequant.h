@@ -173,14 +173,16 @@ int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int64_t q_strid
 /* tq_rope_cache followed by tq_decode_attention (q_out NULL) or
  * tq_decode_attention_quant, in one split pass: qkv is the stacked [batch,
  * (q_heads + 2 kv_heads) * 128] q/k/v projection output (row stride
- * qkv_stride); the split kernel applies RoPE to the q heads it reads, and the
+ * qkv_stride); cos_table / sin_table are [max_len, 128] (row stride 128) and
+ * their rows at *position are the RoPE factors (the row index is clamped into
+ * the table).  The split kernel applies RoPE to the q heads it reads, and the
  * workgroup whose 128-key chunk holds *position writes that token's rotated k
  * and its v into the caches (nothing is written when *position is outside
  * [0, max_len)) and uses them in registers.  Outputs, codes, scales and cache
- * contents are bitwise those of the two-launch sequence.  No reference
+ * contents are bitwise those of the two-launch sequence with the table rows.  No reference
  * counterpart: it fuses the Hugging Face rotary embedding and StaticCache
  * update that precede _cuda_graph_attention (src/runtime/graph_decode.py:56-71). */
-int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos_table, const void* sin_table,
                              const int64_t* position, void* k_cache, void* v_cache, int64_t cache_stride_b,
                              int64_t cache_stride_l, int64_t cache_stride_h, const int32_t* seq_used, void* out,
                              int64_t out_stride_b, int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b,
@@ -217,6 +219,21 @@ int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* cos, const vo
                   void* q_out, int64_t q_stride_b, int64_t q_stride_h, void* k_cache, void* v_cache,
                   int64_t cache_stride_b, int64_t cache_stride_h, int64_t cache_stride_l, int dtype, int n,
                   int q_heads, int kv_heads, int head_dim, int max_len, void* stream);
+
+/* Greedy decoding step on the device: next_token[b] = token[b] = argmax_v
+ * logits[b, v] (torch.argmax order: NaN first, lowest index among equals),
+ * generated[b, *position - prompt_len + 1] = that token (no write outside
+ * [0, generated_len) or when generated is NULL), then *position += 1 and
+ * seq_used[b] = *position + 1 (seq_used nullable).  batch <= 256; logits
+ * 16-bit [batch, vocab] with row stride logits_stride; workspace =
+ * tq_greedy_step_workspace_elems(batch) int32 elements.  Replaces the
+ * argmax / scatter / token copy / position update of the reference's captured
+ * decode loop (src/runtime/graph_decode.py:347-385). */
+int64_t tq_greedy_step_workspace_elems(int batch);
+int tq_greedy_step(const void* logits, int64_t logits_stride, int dtype, int batch, int vocab, int32_t* workspace,
+                   int64_t workspace_elems, int64_t* next_token, int64_t* token, int64_t* generated,
+                   int64_t generated_stride, int generated_len, int64_t* position, int prompt_len,
+                   int32_t* seq_used, void* stream);
 
 /* ---- load-time packing -------------------------------------------------
  * w [m, k] (x_dtype, row stride w_stride_m) is read as if zero-padded to

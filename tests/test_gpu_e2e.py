@@ -340,12 +340,18 @@ def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, qua
     tq_decode_attention(_quant): outputs, codes, scales and both caches
     bitwise equal.  Positions at chunk edges (0, 127, 128, 255) and in the
     middle; seq_used = position + 1 except one row whose length stops short of
-    the new key (it must not be read); pos == L writes nothing."""
+    the new key (it must not be read); pos == L writes nothing.  The fused
+    entry reads cos / sin from [L, 128] tables at the device position (the
+    row index clamped into the table)."""
     D = 128
     g = torch.Generator().manual_seed(B * 31 + pos)
     qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(DEV)
     ang = torch.randn(D, generator=g) * 3
     cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    cos_t = torch.randn((L, D), generator=g).to(torch.bfloat16).to(DEV)
+    sin_t = torch.randn((L, D), generator=g).to(torch.bfloat16).to(DEV)
+    cos_t[min(pos, L - 1)] = cos
+    sin_t[min(pos, L - 1)] = sin
     kc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
     vc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
     position = torch.tensor([pos], dtype=torch.int64, device=DEV)
@@ -385,7 +391,7 @@ def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, qua
     kc2, vc2 = kc0.clone(), vc0.clone()
     out2, qo2, sx2 = outputs()
     rc = nat.lib().tq_decode_attention_rope(
-        qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), position.data_ptr(), kc2.data_ptr(),
+        qkv.data_ptr(), qkv.stride(0), cos_t.data_ptr(), sin_t.data_ptr(), position.data_ptr(), kc2.data_ptr(),
         vc2.data_ptr(), kc2.stride(0), kc2.stride(2), kc2.stride(1), seq.data_ptr(), out2.data_ptr(), out2.stride(0),
         D, qo2.data_ptr() if quant else None, qo2.stride(0), sx2.data_ptr() if quant else None, code, B, hq, hkv, D,
         L, D ** -0.5, ws.data_ptr(), ws.numel(), stream)
@@ -396,6 +402,65 @@ def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, qua
     assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
     if pos < L:
         assert not torch.equal(kc2[:, :, pos], kc0[:, :, pos])
+
+
+@pytest.mark.parametrize("B,V,dtype", [(4, 128256, torch.bfloat16), (1, 1000, torch.float16), (16, 40001, torch.bfloat16),
+                                       (3, 77, torch.bfloat16)])
+def test_greedy_step_matches_torch_argmax_and_bookkeeping(B, V, dtype):
+    """tq_greedy_step: torch.argmax results (planted ties, a NaN row, an
+    all -inf row), token feedback, the generated column, the position and
+    seq_used updates; a position past the generated buffer writes no column."""
+    g = torch.Generator().manual_seed(V + B)
+    logits = (torch.randn((B, 1, V), generator=g) * 4).to(dtype).to(DEV)
+    if B > 2:
+        logits[0, 0, 5] = logits[0, 0, V - 3] = 1000.0          # tie: the lower index wins
+        logits[1, 0, V // 2] = float("nan")                       # NaN beats every number
+        logits[1, 0, V // 3] = float("nan")
+        logits[2] = float("-inf")                                 # all -inf: index 0
+    prompt, gen_len = 50, 8
+    ws = torch.empty((nat.lib().tq_greedy_step_workspace_elems(B),), dtype=torch.int32, device=DEV)
+    for step, pos0 in enumerate([prompt, prompt + 3, prompt + gen_len + 2]):
+        nxt = torch.full((B, 1), -1, dtype=torch.long, device=DEV)
+        tok = torch.full((B, 1), -1, dtype=torch.long, device=DEV)
+        gen = torch.zeros((B, gen_len), dtype=torch.long, device=DEV)
+        position = torch.tensor([pos0], dtype=torch.long, device=DEV)
+        seq = torch.zeros((B,), dtype=torch.int32, device=DEV)
+        lg = logits.view(B, V)
+        rc = nat.lib().tq_greedy_step(lg.data_ptr(), lg.stride(0), nat.dtype_code(dtype), B, V, ws.data_ptr(),
+                                      ws.numel(), nxt.data_ptr(), tok.data_ptr(), gen.data_ptr(), gen.stride(0),
+                                      gen_len, position.data_ptr(), prompt, seq.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        ref = logits.argmax(dim=-1)
+        assert torch.equal(nxt, ref) and torch.equal(tok, ref)
+        col = pos0 - prompt + 1
+        exp_gen = torch.zeros_like(gen)
+        if 0 <= col < gen_len:
+            exp_gen[:, col] = ref[:, 0]
+        assert torch.equal(gen, exp_gen)
+        assert int(position) == pos0 + 1 and torch.all(seq == pos0 + 2)
+    if B > 2:
+        assert int(nxt[0, 0]) == 5 and int(nxt[2, 0]) == 0 and int(nxt[1, 0]) == V // 3
+
+
+def test_rotary_tables_equal_per_position_values():
+    """The fused step's RoPE tables (the model's rotary module over all cache
+    positions at once) equal its one-position outputs bit for bit."""
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    from transformers import LlamaConfig
+
+    cfg = LlamaConfig(hidden_size=3072, num_attention_heads=24, num_key_value_heads=8, max_position_embeddings=131072,
+                      rope_theta=500000.0, rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                                                         "high_freq_factor": 4.0,
+                                                         "original_max_position_embeddings": 8192})
+    rot = LlamaRotaryEmbedding(cfg).to(DEV)
+    L = 2304
+    x = torch.empty((1, 1, 1), dtype=torch.bfloat16, device=DEV)
+    cos_t, sin_t = rot(x, torch.arange(L, device=DEV).view(1, -1))
+    for p in (0, 1, 127, 2047, 2303):
+        c, s_ = rot(x, torch.tensor([[p]], device=DEV))
+        assert torch.equal(c.reshape(-1), cos_t[0, p]) and torch.equal(s_.reshape(-1), sin_t[0, p]), p
 
 
 @pytest.mark.parametrize("family", ["llama", "qwen"])

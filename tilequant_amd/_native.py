@@ -57,6 +57,8 @@ _SIGNATURES = {
                                        _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
     "tq_decode_attention_rope": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                       _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
+    "tq_greedy_step_workspace_elems": (_i64, [_i]),
+    "tq_greedy_step": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _p, _p, _p, _i64, _i, _p, _i, _p, _p]),
     "tq_add_rmsnorm_quant": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _p, _i64, _p,
                                   _i, _i, _i, _p]),
     "tq_silu_mul_quant": (_i, [_p, _i64, _p, _i64, _p, _i64, _p, _i, _i, _i, _p]),

@@ -57,7 +57,7 @@ struct AttnArgs {
   // RoPE-fused form: q (= qkv rows) is the raw stacked projection output
   // [batch, (q_heads + 2 kv_heads) * D] with row stride q_sb; the new token's
   // rotated k and raw v go to the caches at *pos.
-  const uint16_t* cos;   // [D] at the position
+  const uint16_t* cos;   // [max_len, D] tables; row *pos (clamped into the table) is used
   const uint16_t* sin;
   const int64_t* pos;
   uint16_t* k_out;       // the k / v caches, writable
@@ -124,7 +124,6 @@ __device__ inline float rows4_max(float x) {
 template <class XT>
 __device__ inline float dot8(u32x4 x, u32x4 y, float acc) {
   if constexpr (std::is_same<XT, Bf16>::value) {
-    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
     const v8bf xv = __builtin_bit_cast(v8bf, x), yv = __builtin_bit_cast(v8bf, y);
     acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 0, 1), __builtin_shufflevector(yv, yv, 0, 1), acc, false);
     acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(xv, xv, 2, 3), __builtin_shufflevector(yv, yv, 2, 3), acc, false);
@@ -173,14 +172,17 @@ attn_split_kernel(AttnArgs a) {
   }
   // RoPE form: thread t < 16 (G + 2) owns chunk ich of item it -- query head
   // g < G, the new token's k (it = G) or v (it = G + 1) -- and loads that
-  // chunk, its RoPE partner chunk ich ^ 8 and cos / sin; none of these loads
-  // depends on another.  Each (item, chunk) is rotated once and shared through
-  // LDS (every lane needs all of them for its own chunk).
+  // chunk, its RoPE partner chunk ich ^ 8 and the cos / sin table rows at the
+  // position (read in the same scalar round trip as seq_used, so the K/V and
+  // table loads go out together).  Each (item, chunk) is rotated once and
+  // shared through LDS (every lane needs all of them for its own chunk).
   __shared__ u32x4 rq[ROPE ? G + 2 : 1][16];
   const int it = t >> 4, ich = t & 15;
   u32x4 own{}, partner{}, cw{}, sw{};
   int64_t pos = -1;
   if constexpr (ROPE) {
+    pos = a.pos[0];
+    const int64_t trow = min(max(pos, (int64_t)0), (int64_t)a.max_len - 1) * kAttnD;
     if (it < G + 2) {
       const uint16_t* row = a.q + (int64_t)b * a.q_sb;
       const int64_t head = it < G ? (int64_t)(kvh * G + it) * a.q_sh
@@ -188,11 +190,10 @@ attn_split_kernel(AttnArgs a) {
       own = *reinterpret_cast<const u32x4*>(row + head + ich * 8);
       if (it <= G) {
         partner = *reinterpret_cast<const u32x4*>(row + head + (ich ^ 8) * 8);
-        cw = *reinterpret_cast<const u32x4*>(a.cos + ich * 8);
-        sw = *reinterpret_cast<const u32x4*>(a.sin + ich * 8);
+        cw = *reinterpret_cast<const u32x4*>(a.cos + trow + ich * 8);
+        sw = *reinterpret_cast<const u32x4*>(a.sin + trow + ich * 8);
       }
     }
-    pos = a.pos[0];
   }
   // K/V rows through buffer resources spanning the valid prefix of this
   // (b, kv head): keys past seq_used read as 0 without touching memory, so
@@ -515,7 +516,7 @@ extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int6
   return (int)hipGetLastError();
 }
 
-extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* cos_table, const void* sin_table,
                                         const int64_t* position, void* k_cache, void* v_cache,
                                         int64_t cache_stride_b, int64_t cache_stride_l, int64_t cache_stride_h,
                                         const int32_t* seq_used, void* out, int64_t out_stride_b,
@@ -524,16 +525,16 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
                                         int head_dim, int max_len, float scale, float* workspace,
                                         int64_t workspace_elems, void* stream) {
   if (q_out != nullptr && (batch > kMergeQuantMaxRows || sx_out == nullptr)) return TQ_ERR_ARG;
-  if (batch > 0 && max_len > 0 && (!cos || !sin || !position)) return TQ_ERR_ARG;
-  if ((cos && !aligned16(cos)) || (sin && !aligned16(sin))) return TQ_ERR_ALIGN;
+  if (batch > 0 && max_len > 0 && (!cos_table || !sin_table || !position)) return TQ_ERR_ARG;
+  if ((cos_table && !aligned16(cos_table)) || (sin_table && !aligned16(sin_table))) return TQ_ERR_ALIGN;
   if (qkv_stride < (int64_t)(q_heads + 2 * kv_heads) * head_dim) return TQ_ERR_ARG;
   AttnArgs a{};
   const int rc = attn_setup(a, qkv, qkv_stride, head_dim, k_cache, v_cache, cache_stride_b, cache_stride_l,
                             cache_stride_h, seq_used, out, out_stride_b, out_stride_h, dtype, batch, q_heads,
                             kv_heads, head_dim, max_len, scale, workspace, workspace_elems);
   if (rc != 1) return rc;
-  a.cos = static_cast<const uint16_t*>(cos);
-  a.sin = static_cast<const uint16_t*>(sin);
+  a.cos = static_cast<const uint16_t*>(cos_table);
+  a.sin = static_cast<const uint16_t*>(sin_table);
   a.pos = position;
   a.k_out = static_cast<uint16_t*>(k_cache);
   a.v_out = static_cast<uint16_t*>(v_cache);

@@ -234,6 +234,95 @@ rope_cache_kernel(RopeArgs a) {
   dst[d + 64] = XT::from_f32(o1);
 }
 
+// ---- greedy decode step: argmax over the vocabulary + token bookkeeping ----
+//
+// torch.argmax semantics (ATen's GreaterOrNan): a NaN beats every number,
+// equal values (or two NaNs) go to the lower index.
+struct ArgBest {
+  float v;
+  int i;
+};
+__device__ inline bool arg_better(float a, int ia, float b, int ib) {
+  if (a != a) return b != b ? ia < ib : true;
+  if (b != b) return false;
+  return a == b ? ia < ib : a > b;
+}
+__device__ inline ArgBest arg_pick(ArgBest x, float v, int i) { return arg_better(v, i, x.v, x.i) ? ArgBest{v, i} : x; }
+// wave-wide best (every lane receives it); the pairing order does not matter:
+// the rule is a total order with a unique winner
+__device__ inline ArgBest wave_arg_best(ArgBest x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v = __shfl_xor(x.v, off);
+    const int i = __shfl_xor(x.i, off);
+    x = arg_pick(x, v, i);
+  }
+  return x;
+}
+
+constexpr int kArgSplits = 32;      // partial results per row
+constexpr int kArgThreads = 256;
+
+// workgroup (split s, row b): best of logits[b, s * per .. (s + 1) * per)
+template <class XT>
+__global__ void __launch_bounds__(kArgThreads)
+argmax_partial_kernel(const uint16_t* __restrict__ x, int64_t ldx, int m, int per, float* __restrict__ pv,
+                      int* __restrict__ pi) {
+  __shared__ ArgBest red[kArgThreads / kWave];
+  const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const uint16_t* row = x + (int64_t)b * ldx;
+  const int lo = s * per, hi = min(lo + per, m);
+  ArgBest best{-INFINITY, 0x7fffffff};
+  constexpr int kBatch = 8;   // independent loads in flight per thread
+  for (int j0 = lo + t; j0 < hi; j0 += kArgThreads * kBatch) {
+    uint16_t r[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u * kArgThreads;
+      r[u] = row[min(j, hi - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u * kArgThreads;
+      if (j < hi) best = arg_pick(best, XT::to_f32(r[u]), j);
+    }
+  }
+  best = wave_arg_best(best);
+  if ((t & 63) == 0) red[t >> 6] = best;
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < kArgThreads / kWave; ++w) best = arg_pick(best, red[w].v, red[w].i);
+    pv[b * kArgSplits + s] = best.v;
+    pi[b * kArgSplits + s] = best.i;
+  }
+}
+
+// One workgroup: wave w finishes rows w, w + 4, ...; then the bookkeeping of
+// the reference's greedy loop (src/runtime/graph_decode.py:347-385): the
+// token is fed back, recorded at column position - prompt_len + 1 of
+// `generated`, the position advances and seq_used becomes new position + 1.
+__global__ void __launch_bounds__(kArgThreads)
+greedy_finish_kernel(const float* __restrict__ pv, const int* __restrict__ pi, int n, int64_t* __restrict__ next,
+                     int64_t* __restrict__ token, int64_t* __restrict__ gen, int64_t ldg, int gen_len,
+                     int64_t* __restrict__ position, int prompt_len, int32_t* __restrict__ seq_used) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t pos = position[0];
+  for (int b = wave; b < n; b += kArgThreads / kWave) {
+    ArgBest best{-INFINITY, 0x7fffffff};
+    if (lane < kArgSplits) best = ArgBest{pv[b * kArgSplits + lane], pi[b * kArgSplits + lane]};
+    best = wave_arg_best(best);
+    if (lane == 0) {
+      next[b] = best.i;
+      token[b] = best.i;
+      const int64_t col = pos - prompt_len + 1;
+      if (gen != nullptr && col >= 0 && col < gen_len) gen[(int64_t)b * ldg + col] = best.i;
+    }
+  }
+  __syncthreads();   // every wave has read the position
+  if (t < n && seq_used != nullptr) seq_used[t] = (int32_t)(pos + 2);
+  if (t == 0) position[0] = pos + 1;
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace tq
@@ -302,5 +391,34 @@ extern "C" int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* co
   const dim3 grid(n, q_heads + 2 * kv_heads);
   if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(rope_cache_kernel<Bf16>, grid, dim3(64), 0, s, a);
   else hipLaunchKernelGGL(rope_cache_kernel<Fp16>, grid, dim3(64), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t tq_greedy_step_workspace_elems(int batch) {
+  return batch > 0 ? (int64_t)batch * kArgSplits * 2 : 0;
+}
+
+extern "C" int tq_greedy_step(const void* logits, int64_t logits_stride, int dtype, int batch, int vocab,
+                              int32_t* workspace, int64_t workspace_elems, int64_t* next_token, int64_t* token,
+                              int64_t* generated, int64_t generated_stride, int generated_len, int64_t* position,
+                              int prompt_len, int32_t* seq_used, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (batch < 0 || vocab <= 0 || batch > kArgThreads || logits_stride < vocab) return TQ_ERR_ARG;
+  if (batch == 0) return TQ_OK;
+  if (!logits || !next_token || !token || !position) return TQ_ERR_ARG;
+  if (!workspace || workspace_elems < tq_greedy_step_workspace_elems(batch)) return TQ_ERR_WORKSPACE;
+  float* pv = reinterpret_cast<float*>(workspace);
+  int* pi = workspace + (int64_t)batch * kArgSplits;
+  const int per = (vocab + kArgSplits - 1) / kArgSplits;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* x = static_cast<const uint16_t*>(logits);
+  if (dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(argmax_partial_kernel<Bf16>, dim3(kArgSplits, batch), dim3(kArgThreads), 0, s, x,
+                       logits_stride, vocab, per, pv, pi);
+  else
+    hipLaunchKernelGGL(argmax_partial_kernel<Fp16>, dim3(kArgSplits, batch), dim3(kArgThreads), 0, s, x,
+                       logits_stride, vocab, per, pv, pi);
+  hipLaunchKernelGGL(greedy_finish_kernel, dim3(1), dim3(kArgThreads), 0, s, pv, pi, batch, next_token, token,
+                     generated, generated_stride, generated_len, position, prompt_len, seq_used);
   return (int)hipGetLastError();
 }

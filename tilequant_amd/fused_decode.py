@@ -113,6 +113,15 @@ class FusedDecodeStep:
         self.d_out = e(B, H)
         self.final = e(B, H)
         self.attn_ws = decode_attention_workspace(B, self.hq, self.L, dev)
+        # RoPE factors of every cache position, from the model's own rotary
+        # module (per position the same fp32 product inv_freq * p, cos/sin and
+        # rounding as a one-position call, so the rows equal the per-step
+        # values); the attention kernel reads the row at the device position
+        with torch.inference_mode():
+            pos = torch.arange(self.L, device=dev).view(1, -1)
+            cos, sin = self.text.rotary_emb(torch.empty((1, 1, 1), device=dev, dtype=dt), pos)
+        self.cos_table = cos.reshape(self.L, self.head_dim).contiguous()
+        self.sin_table = sin.reshape(self.L, self.head_dim).contiguous()
 
     # -- kernels -------------------------------------------------------------
     def _norm(self, x, delta, ln, h_out, y_out, q_out, sx_out) -> None:
@@ -148,8 +157,6 @@ class FusedDecodeStep:
         B, dev = self.B, self.device
         stream = nat.stream_handle(dev)
         x = self.text.embed_tokens(token).view(B, self.hidden)
-        cos, sin = self.text.rotary_emb(x.view(B, 1, self.hidden), position.view(1, 1))
-        cos, sin = cos.reshape(-1), sin.reshape(-1)
         cur, delta = x, None
         k = 0
         for li, ly in enumerate(self.layers):
@@ -165,7 +172,8 @@ class FusedDecodeStep:
             # projection's quantization) in one split pass and one merge
             q8o = self._quantized(ly.o)
             rc = nat.lib().tq_decode_attention_rope(
-                nat.ptr(self.qkv_out), self.qkv_out.stride(0), nat.ptr(cos), nat.ptr(sin), nat.ptr(position),
+                nat.ptr(self.qkv_out), self.qkv_out.stride(0), nat.ptr(self.cos_table), nat.ptr(self.sin_table),
+                nat.ptr(position),
                 nat.ptr(kc), nat.ptr(vc), kc.stride(0), kc.stride(2), kc.stride(1), nat.ptr(seq_used),
                 nat.ptr(self.attn), self.attn.stride(0), self.head_dim,
                 nat.ptr(self.aq) if q8o else None, self.aq.stride(0), nat.ptr(self.asx) if q8o else None,

@@ -40,6 +40,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from transformers import AttentionInterface, StaticCache
 from transformers.masking_utils import AttentionMaskInterface
 
+from . import _native as nat
 from .attention import decode_attention, decode_attention_workspace
 
 _GRAPH_ATTENTION = "tilequant_hip_graph"
@@ -174,6 +175,8 @@ class CudaGraphGreedyDecoder:
             self._next_token = torch.empty_like(self._token)
             self._generated = torch.empty((self.batch_size, self.max_new_tokens), dtype=torch.long, device=dev)
             self._decode_seq_used = torch.empty((self.batch_size,), dtype=torch.int32, device=dev)
+            self._greedy_ws = torch.empty((max(1, nat.lib().tq_greedy_step_workspace_elems(self.batch_size)),),
+                                          dtype=torch.int32, device=dev)
         self._install_attention_backend()
         # One-token steps from fused kernels where the architecture allows
         # (tilequant_amd.fused_decode); otherwise the model's own forward.
@@ -269,6 +272,7 @@ class CudaGraphGreedyDecoder:
         if not self._prefill_only:
             self._generated.zero_()
             self._position.fill_(self.prompt_tokens)
+            self._decode_seq_used.fill_(self.prompt_tokens + 1)   # valid length of the first decode step
         out = self.model(input_ids=self._prompt, attention_mask=None, position_ids=self._prefill_positions.view(1, -1),
                          past_key_values=self.cache, cache_position=self._prefill_positions, use_cache=True,
                          logits_to_keep=1)
@@ -280,7 +284,6 @@ class CudaGraphGreedyDecoder:
     @torch.inference_mode()
     def _decode_body(self) -> None:
         self._attention_is_prefill = False
-        self._decode_seq_used.copy_(self._position + 1)
         if self._fused is not None:
             logits = self._fused(self._token, self._position, self._decode_seq_used)
         else:
@@ -288,12 +291,23 @@ class CudaGraphGreedyDecoder:
                                 past_key_values=self.cache, cache_position=self._position, use_cache=True,
                                 logits_to_keep=1).logits
         self._decode_logits = logits
-        self._next_token.copy_(logits.argmax(dim=-1))
-        # position P consumes generated token P - prompt and produces the next one
-        col = (self._position - self.prompt_tokens + 1).view(1, 1).expand(self.batch_size, 1)
-        self._generated.scatter_(1, col, self._next_token)
-        self._token.copy_(self._next_token)
-        self._position.add_(1)
+        # position P consumes generated token P - prompt and produces the next one;
+        # seq_used becomes the next step's valid length
+        if logits.dtype in (torch.bfloat16, torch.float16) and logits.stride(-1) == 1:
+            lg = logits.reshape(self.batch_size, -1)
+            rc = nat.lib().tq_greedy_step(
+                nat.ptr(lg), lg.stride(0), nat.dtype_code(lg.dtype), self.batch_size, lg.shape[1],
+                nat.ptr(self._greedy_ws), self._greedy_ws.numel(), nat.ptr(self._next_token), nat.ptr(self._token),
+                nat.ptr(self._generated), self._generated.stride(0), self.max_new_tokens, nat.ptr(self._position),
+                self.prompt_tokens, nat.ptr(self._decode_seq_used), nat.stream_handle(self.device))
+            nat.check(rc, "tq_greedy_step")
+        else:
+            self._next_token.copy_(logits.argmax(dim=-1))
+            col = (self._position - self.prompt_tokens + 1).view(1, 1).expand(self.batch_size, 1)
+            self._generated.scatter_(1, col, self._next_token)
+            self._token.copy_(self._next_token)
+            self._position.add_(1)
+            self._decode_seq_used.copy_(self._position + 1)
 
     # ---- requests -----------------------------------------------------------
     def _prompt_from_host(self, prompt_ids) -> torch.Tensor:
