@@ -18,6 +18,8 @@
 //
 // Quantizing kernels run one workgroup per 64-column tile, so the tile's
 // absmax over all rows is local to the workgroup.
+#include <algorithm>
+
 #include "tq_common.h"
 
 namespace tq {
@@ -25,14 +27,16 @@ namespace tq {
 constexpr int kFuseThreads = 256;
 
 // Max over the workgroup of a non-negative value (all threads receive it).
+// The barriers wait for LDS traffic only: the caller's global stores issued
+// just before stay in flight (__syncthreads() would wait for them too).
 __device__ inline float wg_max_nonneg(float v, float* red) {
   v = wave_max_nonneg(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float r = red[0];
   for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
-  __syncthreads();
+  lds_barrier();
   return r;
 }
 
@@ -64,6 +68,16 @@ struct NormArgs {
   float eps;
 };
 
+// Buffer range over rows [0, n) of a [*, k] 16-bit matrix with row stride ld
+// (elements): offsets of rows >= n fall past it, so loads there read 0 and
+// stores are dropped -- every access in the kernels below is unconditional,
+// which keeps all loads of a phase in flight together (per-row branches made
+// the compiler wait for each load before the next).  A null pointer gives an
+// empty range.
+__device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, int64_t ld, int n, int k, int esize) {
+  return row_rsrc(p, p ? (int)(((int64_t)(n - 1) * ld + k) * esize) : 0);
+}
+
 // workgroup c: every row's sum of squares over all k columns (each wave takes
 // rows wave, wave + 4, ...), then the 64 columns of tile c for every row.
 template <class XT>
@@ -74,75 +88,94 @@ add_rmsnorm_quant_kernel(NormArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int c = blockIdx.x;
   const int cpr = a.k >> 3;           // 8-element chunks per row
+  const __amdgpu_buffer_rsrc_t xr = rows_rsrc(a.x, a.ldx, a.n, a.k, 2);
+  const __amdgpu_buffer_rsrc_t dr = rows_rsrc(a.delta, a.ldd, a.n, a.k, 2);
+  const bool has_delta = a.delta != nullptr;   // without it h = x (not x + 0: -0 stays -0)
   // This workgroup's tile (thread t -> rows wave + 4i, column c*64 + t%64),
   // loaded first: it does not depend on the row norms, so its round trip
   // overlaps the row loads below.
   const int col = c * 64 + lane;
-  uint16_t xt[16], dt[16];
+  const int nper = (a.n + 3) >> 2;    // tile rows per wave (wave-uniform)
+  uint32_t xt[16], dt[16];   // one register per value: no packing right after each load
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = min(wave + 4 * i, a.n - 1);
-    xt[i] = a.x[(int64_t)row * a.ldx + col];
-    dt[i] = a.delta ? a.delta[(int64_t)row * a.ldd + col] : (uint16_t)0;
+    xt[i] = 0;
+    dt[i] = 0;
+    if (i < nper) {
+      const int off = (int)(((int64_t)(wave + 4 * i) * a.ldx + col) * 2);
+      const int offd = (int)(((int64_t)(wave + 4 * i) * a.ldd + col) * 2);
+      xt[i] = __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0);
+      dt[i] = __builtin_amdgcn_raw_buffer_load_b16(dr, offd, 0, 0);
+    }
   }
   const uint16_t wraw = a.w[col];
   // Passes of kNormBatch chunks per lane: all loads of a pass are issued
   // before the first use (one memory round trip per pass, not per chunk).
+  // Chunks past the row end read 0 (an offset past the range) and add 0.
   constexpr int kNormBatch = 8;
   for (int row = wave; row < a.n; row += kFuseThreads / kWave) {
-    float ss = 0.0f;
+    // one partial sum per load slot j (eight independent fma chains instead
+    // of one 64 long), combined pairwise in a fixed order
+    float ssj[kNormBatch];
+#pragma unroll
+    for (int j = 0; j < kNormBatch; ++j) ssj[j] = 0.0f;
     for (int c0 = 0; c0 < cpr; c0 += kNormBatch * kWave) {
       u32x4 xv[kNormBatch], dv[kNormBatch];
 #pragma unroll
       for (int j = 0; j < kNormBatch; ++j) {
-        const int ch = min(c0 + j * kWave + lane, cpr - 1);
-        xv[j] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)row * a.ldx + ch * 8);
-        dv[j] = u32x4{0, 0, 0, 0};
-        if (a.delta) dv[j] = *reinterpret_cast<const u32x4*>(a.delta + (int64_t)row * a.ldd + ch * 8);
+        const int ch = c0 + j * kWave + lane;
+        const int ox = ch < cpr ? (int)(((int64_t)row * a.ldx + ch * 8) * 2) : 0x7fffffff;
+        const int od = ch < cpr ? (int)(((int64_t)row * a.ldd + ch * 8) * 2) : 0x7fffffff;
+        xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ox, 0, 0));
+        dv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, od, 0, 0));
       }
 #pragma unroll
       for (int j = 0; j < kNormBatch; ++j) {
-        if (c0 + j * kWave + lane >= cpr) continue;   // clamped duplicate: not summed
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          float hv = XT::to_f32((uint16_t)(xv[j][i >> 1] >> (16 * (i & 1))));
-          if (a.delta) hv = XT::round(hv + XT::to_f32((uint16_t)(dv[j][i >> 1] >> (16 * (i & 1)))));
-          ss = fmaf(hv, hv, ss);
+          const float xf = XT::to_f32((uint16_t)(xv[j][i >> 1] >> (16 * (i & 1))));
+          const float hv = has_delta ? XT::round(xf + XT::to_f32((uint16_t)(dv[j][i >> 1] >> (16 * (i & 1))))) : xf;
+          ssj[j] = fmaf(hv, hv, ssj[j]);
         }
       }
     }
+    float ss = ((ssj[0] + ssj[1]) + (ssj[2] + ssj[3])) + ((ssj[4] + ssj[5]) + (ssj[6] + ssj[7]));
     ss = wave_sum(ss);
     if (lane == 0) rinv[row] = rsqrtf(ss / (float)a.k + a.eps);
   }
-  __syncthreads();
-  // tile c
+  lds_barrier();
+  // tile c (rows >= n: zero values, stores dropped by the ranges)
+  const __amdgpu_buffer_rsrc_t hr = rows_rsrc(a.delta ? a.h : nullptr, a.ldh, a.n, a.k, 2);
+  const __amdgpu_buffer_rsrc_t yr = rows_rsrc(a.y, a.ldy, a.n, a.k, 2);
   float am = 0.0f;
   float yv[16];
   const float wv = XT::to_f32(wraw);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = wave + 4 * i;
     yv[i] = 0.0f;
-    if (row < a.n) {
-      float hv = XT::to_f32(xt[i]);
-      if (a.delta) {
-        hv = XT::round(hv + XT::to_f32(dt[i]));
-        if (a.h) a.h[(int64_t)row * a.ldh + col] = XT::from_f32(hv);
-      }
-      const float nrm = XT::round(hv * rinv[row]);   // hidden_states.to(input_dtype)
-      const float y = XT::round(wv * nrm);           // weight * hidden_states
-      a.y[(int64_t)row * a.ldy + col] = XT::from_f32(y);
-      yv[i] = y;
-      am = fmaxf(am, fabsf(y));
+    if (i < nper) {
+      const int row = wave + 4 * i;
+      const bool live = row < a.n;
+      const float xf = XT::to_f32((uint16_t)xt[i]);
+      const float hv = has_delta ? XT::round(xf + XT::to_f32((uint16_t)dt[i])) : xf;
+      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(hv), hr, (int)(((int64_t)row * a.ldh + col) * 2), 0, 0);
+      const float nrm = XT::round(hv * (live ? rinv[row] : 0.0f));   // hidden_states.to(input_dtype)
+      const float y = XT::round(wv * nrm);                          // weight * hidden_states
+      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, (int)(((int64_t)row * a.ldy + col) * 2), 0, 0);
+      yv[i] = live ? y : 0.0f;
+      am = fmaxf(am, fabsf(yv[i]));
     }
   }
   if (a.q == nullptr) return;
   const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
   const CodeScale cs(s);
+  const __amdgpu_buffer_rsrc_t qr = rows_rsrc(a.q, a.ldq, a.n, a.k, 1);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = wave + 4 * i;
-    if (row < a.n) a.q[(int64_t)row * a.ldq + col] = (int8_t)cs.code(yv[i]);
+    if (i < nper) {
+      const int row = wave + 4 * i;
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, (int)((int64_t)row * a.ldq + col), 0, 0);
+    }
   }
   if (t == 0) a.sx[c] = s;
 }
@@ -164,29 +197,48 @@ silu_mul_quant_kernel(SiluArgs a) {
   __shared__ float red[kFuseThreads / kWave];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int col = blockIdx.x * 64 + lane;
+  const int nper = (a.n + 3) >> 2;   // rows per wave (wave-uniform)
+  // rows >= n read 0 and their stores are dropped (buffer ranges); every
+  // load is issued before the first use
+  const __amdgpu_buffer_rsrc_t gr = rows_rsrc(a.gu, a.ldg, a.n, 2 * a.inter, 2);
+  const __amdgpu_buffer_rsrc_t yr = rows_rsrc(a.y, a.ldy, a.n, a.inter, 2);
+  uint32_t gw[16], uw[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    gw[i] = 0;
+    uw[i] = 0;
+    if (i < nper) {
+      const int off = (int)(((int64_t)(wave + 4 * i) * a.ldg + col) * 2);
+      gw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, off, 0, 0);
+      uw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, off + a.inter * 2, 0, 0);
+    }
+  }
   float am = 0.0f;
   float yv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = wave + 4 * i;
     yv[i] = 0.0f;
-    if (row < a.n) {
-      const float g = XT::to_f32(a.gu[(int64_t)row * a.ldg + col]);
-      const float u = XT::to_f32(a.gu[(int64_t)row * a.ldg + a.inter + col]);
+    if (i < nper) {
+      const int row = wave + 4 * i;
+      const float g = XT::to_f32((uint16_t)gw[i]);
+      const float u = XT::to_f32((uint16_t)uw[i]);
       const float sg = XT::round(g / (1.0f + expf(-g)));
       const float y = XT::round(sg * u);
-      a.y[(int64_t)row * a.ldy + col] = XT::from_f32(y);
-      yv[i] = y;
-      am = fmaxf(am, fabsf(y));
+      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, (int)(((int64_t)row * a.ldy + col) * 2), 0, 0);
+      yv[i] = row < a.n ? y : 0.0f;
+      am = fmaxf(am, fabsf(yv[i]));
     }
   }
   if (a.q == nullptr) return;
   const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
   const CodeScale cs(s);
+  const __amdgpu_buffer_rsrc_t qr = rows_rsrc(a.q, a.ldq, a.n, a.inter, 1);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = wave + 4 * i;
-    if (row < a.n) a.q[(int64_t)row * a.ldq + col] = (int8_t)cs.code(yv[i]);
+    if (i < nper) {
+      const int row = wave + 4 * i;
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, (int)((int64_t)row * a.ldq + col), 0, 0);
+    }
   }
   if (t == 0) a.sx[blockIdx.x] = s;
 }
@@ -338,6 +390,10 @@ extern "C" int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void*
   if (n == 0 || k == 0) return TQ_OK;
   if (!x || !weight || !y_out || (q_out && !sx_out) || (delta && !h_out)) return TQ_ERR_ARG;
   if (!al16(x) || (x_stride % 8) || (delta && (!al16(delta) || (delta_stride % 8)))) return TQ_ERR_ALIGN;
+  // every row range is addressed through a 32-bit buffer offset
+  const int64_t ld_max = std::max({x_stride, delta ? delta_stride : 0, h_out ? h_stride : 0, y_stride,
+                                   q_out ? q_stride : 0});
+  if (ld_max < k || ((int64_t)(n - 1) * ld_max + k) * 2 >= (1LL << 31)) return TQ_ERR_ARG;
   NormArgs a{};
   a.x = static_cast<const uint16_t*>(x); a.delta = static_cast<const uint16_t*>(delta);
   a.w = static_cast<const uint16_t*>(weight);
@@ -359,6 +415,10 @@ extern "C" int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y
   if (n < 0 || inter < 0 || n > 64 || (inter % 64) != 0) return TQ_ERR_ARG;
   if (n == 0 || inter == 0) return TQ_OK;
   if (!gate_up || !y_out || (q_out && !sx_out)) return TQ_ERR_ARG;
+  const int64_t ld_max = std::max({gu_stride, y_stride, q_out ? q_stride : 0});
+  if (gu_stride < 2 * (int64_t)inter || y_stride < inter || (q_out && q_stride < inter) ||
+      ((int64_t)(n - 1) * ld_max + 2 * (int64_t)inter) * 2 >= (1LL << 31))
+    return TQ_ERR_ARG;
   SiluArgs a{};
   a.gu = static_cast<const uint16_t*>(gate_up); a.y = static_cast<uint16_t*>(y_out); a.q = q_out; a.sx = sx_out;
   a.ldg = gu_stride; a.ldy = y_stride; a.ldq = q_stride; a.n = n; a.inter = inter;
