@@ -338,21 +338,23 @@ __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d)
       o[j] = r[d];
       if (s0 + j >= a.n_splits) m[j] = -INFINITY;
     }
+    // Branch-free (an early exit here made the compiler load l and o only
+    // after m had arrived: two round trips): empty splits and padding get
+    // weight 0, which adds an exact 0 to the finite partial sums.
     float Mb = M;
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, m[j]);
-    if (Mb == -INFINITY) continue;
-    const float r = exp2f(M - Mb);   // 0 while nothing has been accumulated (M = -inf)
+    const bool any = Mb != -INFINITY;
+    const float r = any ? exp2f(M - Mb) : 1.0f;   // 0 while nothing has been accumulated (M = -inf)
     L *= r;
     acc *= r;
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) {
-      if (m[j] == -INFINITY) continue;
-      const float w = exp2f(m[j] - Mb);
+      const float w = m[j] == -INFINITY ? 0.0f : exp2f(m[j] - Mb);
       L = fmaf(w, l[j], L);
       acc = fmaf(w, o[j], acc);
     }
-    M = Mb;
+    M = any ? Mb : M;
   }
   return L > 0.0f ? acc / L : 0.0f;
 }
