@@ -43,7 +43,8 @@ def _attention_reference(q, k, v, lens, scale):
     return out
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,L", [(4, 24, 8, 2304), (2, 7, 1, 300), (1, 8, 1, 64), (3, 40, 8, 513)])
+@pytest.mark.parametrize("B,Hq,Hkv,L", [(4, 24, 8, 2304), (2, 7, 1, 300), (1, 8, 1, 64), (3, 40, 8, 513),
+                                          (2, 8, 2, 8400)])
 @pytest.mark.parametrize("token_major", [False, True])
 def test_decode_attention_matches_reference(B, Hq, Hkv, L, token_major):
     g = torch.Generator().manual_seed(B * 1000 + L)

@@ -12,16 +12,19 @@
 // kv head kvh and writes a partial (running max m, sum l, unnormalised o[D])
 // per query head; a second kernel merges the splits of each (b, h) in split
 // order.  Splits past seq_used write m = -inf, l = 0.
-//   loads: all K and V rows of a wave's keys are issued at entry (8 + 8
+//   loads: all K and V rows of a wave's 32 keys are issued at entry (8 + 8
 //       16-byte loads per lane), so the chunk costs one memory round trip.
-//   QK: a wave covers 4 keys per step, 16 lanes per key row (16 bytes = 8
-//       elements each, so each row is one coalesced 256-byte read); the 8-wide
-//       partial dots are summed across the 16 lanes with DPP, so every lane of
-//       a row holds its key's score.
-//   softmax + PV per wave: the max and sum over the wave's 32 keys come from
-//       the lane's 8 scores and two cross-row butterflies (gfx950
-//       v_permlane16_swap / v_permlane32_swap), the same for the 8-dimension
-//       PV accumulators -- no score exchange through LDS.
+//   QK on the matrix cores: per 16-key block, 4 v_mfma_f32_16x16x32 with the
+//       keys as A rows and the G query heads as B columns; each A operand is a
+//       plain 16-byte load of a key row.  The kernel is VALU-bound once its
+//       data has arrived, and this replaces 8 dot2 + 8 DPP adds per (key,
+//       head) group of lanes.
+//   softmax per wave: a lane holds 8 scores of one head; max and sum over
+//       them, then over the head's 4 lanes (gfx950 v_permlane16_swap /
+//       v_permlane32_swap).  The probabilities go through LDS ([head][key],
+//       within the wave) to the PV layout: a lane takes 8 keys x 8 dimensions
+//       of the value rows, fp32 FMAs; the 4 key groups of a wave are summed
+//       with the same butterflies.
 //   the 4 waves' partials (max, sum, o) are combined through LDS in wave
 //       order, rescaled to the chunk max, with one barrier.
 // Everything accumulates in fp32; results are bitwise reproducible.
@@ -152,30 +155,38 @@ template <class XT, int G, bool ROPE>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_split_kernel(AttnArgs a) {
   constexpr int kWaves = kAttnThreads / kWave;
+  constexpr int kKeysW = kAttnChunk / kWaves;   // keys per wave: two 16-key MFMA blocks
+  constexpr int kSteps = kKeysW / 4;            // PV: 8 keys per lane
+  static_assert(kKeysW == 32 && G <= 16, "two 16-key blocks per wave, at most 16 query heads");
   __shared__ float wo[kWaves][G][kAttnD];   // per-wave unnormalised o
   __shared__ float wml[kWaves][G][2];       // per-wave max, sum
+  __shared__ __align__(16) float pl[kWaves][G][kKeysW];   // per-wave probabilities [head][key]
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int s = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads, kvh = blockIdx.y - (blockIdx.y / a.kv_heads) * a.kv_heads;
   const int len = min(max(a.seq_used[b], 0), a.max_len);
-  const int key0 = s * kAttnChunk;
-  const int kl = lane >> 4, ch = lane & 15;   // key within a step of 4, 8-element chunk
-  constexpr int kSteps = kAttnChunk / (kAttnThreads / kWave) / 4;   // 4-key steps per wave
+  const int key0 = s * kAttnChunk, wkey0 = key0 + wave * kKeysW;
+  const int kl = lane >> 4, ch = lane & 15;   // PV layout: keys 8 kl .. 8 kl + 7, 8-element chunk ch
+  const int mr = lane & 15, mg = lane >> 4;   // MFMA layout: row / column index, k group
 
   // ---- every load of the workgroup is issued up front: q, then all K and V
-  //      rows of this wave's keys (keys past the valid length are not read)
-  u32x4 qw[G];
+  //      rows of this wave's keys (keys past the valid length are not read).
+  //      MFMA step ks covers dimensions 32 ks .. 32 ks + 31: lane (mr, mg)
+  //      holds chunk 4 ks + mg of key mr of a 16-key block (A operand) and of
+  //      query head mr (B operand; columns >= G repeat head G - 1, unused).
+  u32x4 qa[4];
   if constexpr (!ROPE) {
+    const int hq = kvh * G + min(mr, G - 1);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      qw[g] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(kvh * G + g) * a.q_sh + ch * 8);
+    for (int ks = 0; ks < 4; ++ks)
+      qa[ks] = *reinterpret_cast<const u32x4*>(a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (4 * ks + mg) * 8);
   }
   // RoPE form: thread t < 16 (G + 2) owns chunk ich of item it -- query head
   // g < G, the new token's k (it = G) or v (it = G + 1) -- and loads that
   // chunk, its RoPE partner chunk ich ^ 8 and the cos / sin table rows at the
   // position (read in the same scalar round trip as seq_used, so the K/V and
   // table loads go out together).  Each (item, chunk) is rotated once and
-  // shared through LDS (every lane needs all of them for its own chunk).
+  // shared through LDS (every lane needs several of them).
   __shared__ u32x4 rq[ROPE ? G + 2 : 1][16];
   const int it = t >> 4, ich = t & 15;
   u32x4 own{}, partner{}, cw{}, sw{};
@@ -202,22 +213,27 @@ attn_split_kernel(AttnArgs a) {
   const int span = len > 0 ? (int)(((int64_t)(len - 1) * a.kv_sl + kAttnD) * 2) : 0;
   const __amdgpu_buffer_rsrc_t krs = row_rsrc(a.k + kv_base, span);
   const __amdgpu_buffer_rsrc_t vrs = row_rsrc(a.v + kv_base, span);
-  u32x4 kw[kSteps], vw[kSteps];
+  // a key past the prefix gets an offset past the span (rows are not always packed: kv_sl >= D)
+  auto kv_off = [&](int key, int chunk) { return key < len ? (int)(((int64_t)key * a.kv_sl + chunk * 8) * 2) : span; };
+  u32x4 kb[2][4], vw[kSteps];
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) {
-    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
-    // a key past the prefix gets an offset past the span (rows are not always packed: kv_sl >= D)
-    const int off = key < len ? (int)(((int64_t)key * a.kv_sl + ch * 8) * 2) : span;
-    kw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
-    vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
-  }
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      kb[blk][ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  krs, kv_off(wkey0 + 16 * blk + mr, 4 * ks + mg), 0, 0));
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i)
+    vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, kv_off(wkey0 + 8 * kl + i, ch), 0, 0));
   __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first use
+
   // RoPE form: the workgroup whose chunk holds the new position writes the
   // token's rotated k and its v into the caches (the bytes tq_rope_cache
   // writes) and uses them in registers for that key (pk; -1 elsewhere): its
-  // own cache rows were loaded before they were written.  The substitution is
-  // a per-lane select at each row's first use, so no wait for the other rows.
-  u32x4 kn{}, vnw{};
+  // own cache rows were loaded before they were written.  The new key's
+  // scores come from MFMAs of their own and replace that key's scores by a
+  // per-lane select, so no wait for the other rows.
+  u32x4 kn[4], vnw{};
   int pk = -1;
   if constexpr (ROPE) {
     const bool mine = pos >= 0 && pos < a.max_len && pos / kAttnChunk == s;
@@ -229,71 +245,101 @@ attn_split_kernel(AttnArgs a) {
     }
     lds_barrier();   // the K/V loads stay in flight
 #pragma unroll
-    for (int g = 0; g < G; ++g) qw[g] = rq[g][ch];
-    kn = rq[G][ch];
+    for (int ks = 0; ks < 4; ++ks) {
+      qa[ks] = rq[min(mr, G - 1)][4 * ks + mg];
+      kn[ks] = rq[G][4 * ks + mg];
+    }
     vnw = rq[G + 1][ch];
     if (mine) pk = (int)pos;
   }
 
-  // ---- QK: 16 lanes per key row, partial dots summed across the row with DPP
-  float sco[kSteps][G];   // scaled scores (log2 units) of the lane's key per step
+  // ---- QK on the matrix cores: sacc[blk][v] = k[key wkey0 + 16 blk + 4 mg + v] . q[head mr]
+  v4f sacc[2];
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) {
-    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
-    const bool valid = key < len;
-    const u32x4 kk = (ROPE && key == pk) ? kn : kw[i];
+  for (int blk = 0; blk < 2; ++blk) {
+    sacc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float d = row16_sum(dot8<XT>(qw[g], kk, 0.0f));
-      sco[i][g] = valid ? d * a.scale_log2 : -INFINITY;
-    }
+    for (int ks = 0; ks < 4; ++ks)
+      sacc[blk] = mfma16<XT>(__builtin_bit_cast(v4i, kb[blk][ks]), __builtin_bit_cast(v4i, qa[ks]), sacc[blk]);
+  }
+  v4f snew = v4f{0.f, 0.f, 0.f, 0.f};   // RoPE form: the new key's scores (every row holds them)
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      snew = mfma16<XT>(__builtin_bit_cast(v4i, kn[ks]), __builtin_bit_cast(v4i, qa[ks]), snew);
   }
 
-  // ---- this wave's softmax statistics over its 32 keys, then PV
-  float mw[G], lw[G];
+  // ---- this wave's softmax over its 32 keys: lane (mr, mg) holds 8 scores of
+  //      head mr; max and sum over them, then over the 4 lanes of the head
+  //      (lanes mr + 16 j, permlane butterflies).  Probabilities go to LDS as
+  //      [head][key] for the PV layout.
+  float pr[2][4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = sco[0][g];
+  for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-    for (int i = 1; i < kSteps; ++i) m = fmaxf(m, sco[i][g]);
-    m = rows4_max(m);
-    float l = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kSteps; ++i) {
-      const float pr = m == -INFINITY ? 0.0f : exp2f(sco[i][g] - m);
-      sco[i][g] = pr;
-      l += pr;
+    for (int v = 0; v < 4; ++v) {
+      const int key = wkey0 + 16 * blk + 4 * mg + v;
+      const float raw = (ROPE && key == pk) ? snew[v] : sacc[blk][v];
+      pr[blk][v] = key < len ? raw * a.scale_log2 : -INFINITY;
     }
-    mw[g] = m;
-    lw[g] = rows4_sum(l);
+  float mx = fmaxf(fmaxf(fmaxf(pr[0][0], pr[0][1]), fmaxf(pr[0][2], pr[0][3])),
+                   fmaxf(fmaxf(pr[1][0], pr[1][1]), fmaxf(pr[1][2], pr[1][3])));
+  mx = rows4_max(mx);
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)   // exp2 of a non-positive argument (-inf for keys past the prefix)
+      pr[blk][v] = mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pr[blk][v] - mx);
+  const float ls = rows4_sum(((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) +
+                             ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3])));
+  if (mr < G) {
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+      *reinterpret_cast<v4f*>(&pl[wave][mr][16 * blk + 4 * mg]) = v4f{pr[blk][0], pr[blk][1], pr[blk][2], pr[blk][3]};
+    if (mg == 0) {
+      wml[wave][mr][0] = mx;
+      wml[wave][mr][1] = ls;
+    }
   }
+  // the probabilities are read back by other lanes of the same wave: LDS
+  // executes a wave's accesses in order, so waiting for the writes suffices
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+
+  // ---- PV: lane (kl, ch) takes keys 8 kl .. 8 kl + 7 of the wave, 8
+  //      dimensions of each value row (16 lanes per 256-byte row)
   float o[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  float pg[G][kSteps];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const v4f p0 = *reinterpret_cast<const v4f*>(&pl[wave][g][8 * kl]);
+    const v4f p1 = *reinterpret_cast<const v4f*>(&pl[wave][g][8 * kl + 4]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      pg[g][v] = p0[v];
+      pg[g][4 + v] = p1[v];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) {
     float vf[8];
-    const int key = key0 + wave * (4 * kSteps) + 4 * i + kl;
-    unpack8<XT>((ROPE && key == pk) ? vnw : vw[i], vf);
+    unpack8<XT>((ROPE && wkey0 + 8 * kl + i == pk) ? vnw : vw[i], vf);
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = fmaf(sco[i][g], vf[e], o[g][e]);
+      for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pg[g][i], vf[e], o[g][e]);
   }
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = rows4_sum(o[g][e]);
       if (kl == 0) wo[wave][g][ch * 8 + e] = x;
     }
-    if (lane == 0) {
-      wml[wave][g][0] = mw[g];
-      wml[wave][g][1] = lw[g];
-    }
-  }
   __syncthreads();
   // ---- combine the waves in wave order, rescaled to the chunk max; one
   //      partial record per query head: o[D], m, l (m in log2 units)
@@ -320,36 +366,43 @@ attn_split_kernel(AttnArgs a) {
 }
 
 // Merge of the split partials of one (b, h) for dimension d: online over
-// batches of kMergeBatch splits, every load of a batch issued before its
-// first use.  With at most kMergeBatch splits this is the plain two-pass
-// formula (global max, then the weighted sums in split order).
-constexpr int kMergeBatch = 32;
+// batches of NB splits (NB = the split count rounded up to 8, at most
+// kMergeBatch), every load of a batch issued before its first use.  Within
+// one batch this is the plain two-pass formula (batch max, then the weighted
+// sums in split order).  Each split's (m, l) pair is the same for every lane;
+// it is read with a vector load all the same (an offset the compiler cannot
+// see is zero): as scalar loads, which may return out of order, the 24 or
+// more pairs of a batch took more than one round trip (measured 1.6 us slower).
+constexpr int kMergeBatch = 64;
 
+template <int NB>
 __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d) {
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
   float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  for (int s0 = 0; s0 < a.n_splits; s0 += kMergeBatch) {
-    float m[kMergeBatch], l[kMergeBatch], o[kMergeBatch];
+  for (int s0 = 0; s0 < a.n_splits; s0 += NB) {
+    float m[NB], l[NB], o[NB];
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int sj = min(s0 + j, a.n_splits - 1);
       const float* r = rec + (int64_t)sj * (kAttnD + 2);
-      m[j] = r[kAttnD];
-      l[j] = r[kAttnD + 1];
+      const float2 ml = *reinterpret_cast<const float2*>(r + kAttnD + vzero);
+      m[j] = s0 + j < a.n_splits ? ml.x : -INFINITY;
+      l[j] = ml.y;
       o[j] = r[d];
-      if (s0 + j >= a.n_splits) m[j] = -INFINITY;
     }
     // Branch-free (an early exit here made the compiler load l and o only
     // after m had arrived: two round trips): empty splits and padding get
     // weight 0, which adds an exact 0 to the finite partial sums.
     float Mb = M;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) Mb = fmaxf(Mb, m[j]);
+    for (int j = 0; j < NB; ++j) Mb = fmaxf(Mb, m[j]);
     const bool any = Mb != -INFINITY;
     const float r = any ? exp2f(M - Mb) : 1.0f;   // 0 while nothing has been accumulated (M = -inf)
     L *= r;
     acc *= r;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const float w = m[j] == -INFINITY ? 0.0f : exp2f(m[j] - Mb);
       L = fmaf(w, l[j], L);
       acc = fmaf(w, o[j], acc);
@@ -359,44 +412,50 @@ __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d)
   return L > 0.0f ? acc / L : 0.0f;
 }
 
-template <class XT>
+template <class XT, int NB>
 __global__ void __launch_bounds__(kAttnD)
 attn_merge_kernel(AttnArgs a) {
   const int bh = blockIdx.x, d = threadIdx.x;
   const int b = bh / a.q_heads, h = bh - (bh / a.q_heads) * a.q_heads;
   const float* rec = a.part + (int64_t)bh * a.n_splits * (kAttnD + 2);
-  a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(merge_splits(a, rec, d));
+  a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(merge_splits<NB>(a, rec, d));
 }
 
 // Merge + INT8 quantization of the attention output for the next projection:
 // workgroup h = query head h for ALL batch rows (b < batch <= 16), 4 row
-// groups x 128 dimensions.  Dimensions 0..63 / 64..127 of the head are column
-// tiles 2h / 2h + 1 of the [batch, q_heads * 128] projection input, so both
-// tiles are whole inside the workgroup: absmax over the batch rows, scale,
-// codes -- the closed form of tq_act_quant, bit for bit.
+// groups x 128 dimensions (a row group is two whole waves).  Dimensions
+// 0..63 / 64..127 of the head are column tiles 2h / 2h + 1 of the
+// [batch, q_heads * 128] projection input, so both tiles are whole inside the
+// workgroup: absmax over the batch rows, scale, codes -- the closed form of
+// tq_act_quant, bit for bit.
 constexpr int kMergeQuantMaxRows = 16;
 constexpr int kMergeQuantThreads = 512;   // 4 row groups x 128 dimensions
 
-template <class XT>
+template <class XT, int NB>
 __global__ void __launch_bounds__(kMergeQuantThreads)
 attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
   __shared__ float red[kMergeQuantThreads / kWave];
-  const int h = blockIdx.x, t = threadIdx.x, d = t & (kAttnD - 1), rg = t / kAttnD;   // row group rg
+  const int h = blockIdx.x, t = threadIdx.x, d = t & (kAttnD - 1);
+  const int rg = t / kAttnD;   // row group
   constexpr int kGroups = kMergeQuantThreads / kAttnD;
   constexpr int kPer = kMergeQuantMaxRows / kGroups;
   float y[kPer];
   float am = 0.0f;
+  // every row merged before the first store: no store can alias a partial still to be read
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int b = rg + kGroups * i;
     y[i] = 0.0f;
     if (b < a.batch) {
       const float* rec = a.part + (int64_t)(b * a.q_heads + h) * a.n_splits * (kAttnD + 2);
-      const uint16_t o = XT::from_f32(merge_splits(a, rec, d));
-      a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = o;
-      y[i] = XT::to_f32(o);
+      y[i] = XT::round(merge_splits<NB>(a, rec, d));
       am = fmaxf(am, fabsf(y[i]));
     }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = rg + kGroups * i;
+    if (b < a.batch) a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(y[i]);
   }
   // column tile 2h + (d >= 64): waves with the same parity hold the same half
   const float wm = wave_max_nonneg(am);
@@ -413,6 +472,31 @@ attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* 
     if (b < a.batch) q[(int64_t)b * ldq + h * kAttnD + d] = (int8_t)cs.code(y[i]);
   }
   if (t < kAttnD && (d & 63) == 0) sx[2 * h + (d >> 6)] = s;
+}
+
+// Merge launches: NB = splits rounded up to 8 (at most kMergeBatch), so no
+// load of a batch is wasted on padding below kMergeBatch splits.
+template <class XT, int NB>
+static void launch_merge_nb(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, hipStream_t s) {
+  if (q_out)
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB>), dim3(a.q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out,
+                       ldq, sx);
+  else
+    hipLaunchKernelGGL((attn_merge_kernel<XT, NB>), dim3(a.batch * a.q_heads), dim3(kAttnD), 0, s, a);
+}
+
+template <class XT>
+static void launch_merge(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, hipStream_t s) {
+  switch ((min(a.n_splits, kMergeBatch) + 7) / 8) {
+    case 1: launch_merge_nb<XT, 8>(a, q_out, ldq, sx, s); break;
+    case 2: launch_merge_nb<XT, 16>(a, q_out, ldq, sx, s); break;
+    case 3: launch_merge_nb<XT, 24>(a, q_out, ldq, sx, s); break;
+    case 4: launch_merge_nb<XT, 32>(a, q_out, ldq, sx, s); break;
+    case 5: launch_merge_nb<XT, 40>(a, q_out, ldq, sx, s); break;
+    case 6: launch_merge_nb<XT, 48>(a, q_out, ldq, sx, s); break;
+    case 7: launch_merge_nb<XT, 56>(a, q_out, ldq, sx, s); break;
+    default: launch_merge_nb<XT, 64>(a, q_out, ldq, sx, s); break;
+  }
 }
 
 static int attn_splits(int max_len) { return (max_len + kAttnChunk - 1) / kAttnChunk; }
@@ -482,13 +566,13 @@ extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
                             scale, workspace, workspace_elems);
   if (rc != 1) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 g1(a.n_splits, batch * kv_heads), g2(batch * q_heads);
+  const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16>(a, g1, s);
-    hipLaunchKernelGGL(attn_merge_kernel<Bf16>, g2, dim3(kAttnD), 0, s, a);
+    launch_merge<Bf16>(a, nullptr, 0, nullptr, s);
   } else {
     launch_split<Fp16>(a, g1, s);
-    hipLaunchKernelGGL(attn_merge_kernel<Fp16>, g2, dim3(kAttnD), 0, s, a);
+    launch_merge<Fp16>(a, nullptr, 0, nullptr, s);
   }
   return (int)hipGetLastError();
 }
@@ -507,13 +591,13 @@ extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int6
                             scale, workspace, workspace_elems);
   if (rc != 1) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 g1(a.n_splits, batch * kv_heads), g2(q_heads);
+  const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16>(a, g1, s);
-    hipLaunchKernelGGL(attn_merge_quant_kernel<Bf16>, g2, dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, s);
   } else {
     launch_split<Fp16>(a, g1, s);
-    hipLaunchKernelGGL(attn_merge_quant_kernel<Fp16>, g2, dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
+    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, s);
   }
   return (int)hipGetLastError();
 }
@@ -544,12 +628,10 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
   const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16, true>(a, g1, s);
-    if (q_out) hipLaunchKernelGGL(attn_merge_quant_kernel<Bf16>, dim3(q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
-    else hipLaunchKernelGGL(attn_merge_kernel<Bf16>, dim3(batch * q_heads), dim3(kAttnD), 0, s, a);
+    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, s);
   } else {
     launch_split<Fp16, true>(a, g1, s);
-    if (q_out) hipLaunchKernelGGL(attn_merge_quant_kernel<Fp16>, dim3(q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out, q_out_stride_b, sx_out);
-    else hipLaunchKernelGGL(attn_merge_kernel<Fp16>, dim3(batch * q_heads), dim3(kAttnD), 0, s, a);
+    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, s);
   }
   return (int)hipGetLastError();
 }

@@ -57,6 +57,22 @@ struct Fp16 {
   __device__ static inline float round(float f) { return to_f32(from_f32(f)); }
 };
 
+// 16x16x32 MFMA on 16-bit operands (8 per lane: row / column lane % 16, k
+// 8 (lane / 16) .. + 7), fp32 accumulators; D[4 (lane / 16) + v][lane % 16].
+template <class XT>
+__device__ inline v4f mfma16(v4i av, v4i bv, v4f c);
+
+template <>
+__device__ inline v4f mfma16<Bf16>(v4i av, v4i bv, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av),
+                                                 __builtin_bit_cast(v8bf, bv), c, 0, 0, 0);
+}
+template <>
+__device__ inline v4f mfma16<Fp16>(v4i av, v4i bv, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
+                                                __builtin_bit_cast(v8h, bv), c, 0, 0, 0);
+}
+
 // ---- quantization closed forms -----------------------------------------
 
 // Activation scale of one 64-column tile from its absmax a (already |x| max,

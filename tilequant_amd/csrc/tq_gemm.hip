@@ -122,20 +122,6 @@ __device__ inline v4i load_xf(const GemmArgs& a, int row, int col) {
   return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
 
-template <class XT>
-__device__ inline v4f mfma16(v4i av, v4i bv, v4f c);
-
-template <>
-__device__ inline v4f mfma16<Bf16>(v4i av, v4i bv, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av),
-                                                 __builtin_bit_cast(v8bf, bv), c, 0, 0, 0);
-}
-template <>
-__device__ inline v4f mfma16<Fp16>(v4i av, v4i bv, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, av),
-                                                __builtin_bit_cast(v8h, bv), c, 0, 0, 0);
-}
-
 // Column tile of a tile id owned by row tile r (id = r * n_tc + c).  Clamped so
 // that a malformed pack can never index sx / x out of range.
 __device__ inline int col_of(int id, int rbase, int n_tc) {
