@@ -176,9 +176,10 @@ int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int64_t q_strid
  * qkv_stride); cos_table / sin_table are [max_len, 128] (row stride 128) and
  * their rows at *position are the RoPE factors (the row index is clamped into
  * the table).  The split kernel applies RoPE to the q heads it reads, and the
- * workgroup whose 128-key chunk holds *position writes that token's rotated k
- * and its v into the caches (nothing is written when *position is outside
- * [0, max_len)) and uses them in registers.  Outputs, codes, scales and cache
+ * workgroup whose key chunk holds *position (the last one when *position is
+ * past seq_used) writes that token's rotated k and its v into the caches
+ * (nothing is written when *position is outside [0, max_len)) and uses them
+ * in registers.  Outputs, codes, scales and cache
  * contents are bitwise those of the two-launch sequence with the table rows.  No reference
  * counterpart: it fuses the Hugging Face rotary embedding and StaticCache
  * update that precede _cuda_graph_attention (src/runtime/graph_decode.py:56-71). */

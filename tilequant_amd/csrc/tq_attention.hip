@@ -8,10 +8,12 @@
 // decoder (src/runtime/graph_decode.py:56-71).
 //
 // Split-sequence schedule (flash decoding): workgroup (split s, b * kv_heads +
-// kvh) takes keys [s * kChunk, (s + 1) * kChunk) for the G query heads sharing
-// kv head kvh and writes a partial (running max m, sum l, unnormalised o[D])
-// per query head; a second kernel merges the splits of each (b, h) in split
-// order.  Splits past seq_used write m = -inf, l = 0.
+// kvh) takes keys [s C, (s + 1) C) of the sequence's seq_used[b] keys, C =
+// ceil(seq_used[b] / n_splits) <= 32 W (W waves of 32 keys; n_splits and W
+// from a host plan that gives every CU the same share), for the G query heads
+// sharing kv head kvh, and writes a partial (running max m, sum l,
+// unnormalised o[D]) per query head; a second kernel merges the splits of
+// each (b, h) in split order.  Empty splits write m = -inf, l = 0.
 //   loads: all K and V rows of a wave's 32 keys are issued at entry (8 + 8
 //       16-byte loads per lane), so the chunk costs one memory round trip.
 //   QK on the matrix cores: per 16-key block, 4 v_mfma_f32_16x16x32 with the
@@ -25,24 +27,25 @@
 //       within the wave) to the PV layout: a lane takes 8 keys x 8 dimensions
 //       of the value rows, fp32 FMAs; the 4 key groups of a wave are summed
 //       with the same butterflies.
-//   the 4 waves' partials (max, sum, o) are combined through LDS in wave
+//   the W waves' partials (max, sum, o) are combined through LDS in wave
 //       order, rescaled to the chunk max, with one barrier.
 // Everything accumulates in fp32; results are bitwise reproducible.
 //
 // RoPE form (tq_decode_attention_rope): the split kernel reads q from the
 // stacked q/k/v projection output and applies RoPE itself, each (head, 8-element
 // chunk) once, shared through LDS; the workgroup whose chunk holds the new
-// position writes that token's rotated k and its v into the caches and
-// substitutes them for the rows it loaded before writing.  This replaces a
-// separate RoPE + cache-write launch per layer, bit for bit.
+// position (the last split when the position is past seq_used) writes that
+// token's rotated k and its v into the caches and substitutes them for the
+// rows it loaded before writing.  This replaces a separate RoPE + cache-write
+// launch per layer, bit for bit.
 #include "tq_common.h"
 
 namespace tq {
 
-constexpr int kAttnD = 128;        // head dimension served
-constexpr int kAttnChunk = 128;    // keys per split
-constexpr int kAttnThreads = 256;  // 4 waves
-constexpr int kAttnMaxG = 8;       // query heads per kv head
+constexpr int kAttnD = 128;            // head dimension served
+constexpr int kAttnKeysPerWave = 32;   // keys per wave of the split kernel
+constexpr int kAttnMaxWaves = 4;       // waves per split workgroup (2..4)
+constexpr int kAttnMaxG = 8;           // query heads per kv head
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -56,6 +59,7 @@ struct AttnArgs {
   int64_t o_sb, o_sh;
   float* part;       // [batch * q_heads][n_splits][D + 2]
   int batch, q_heads, kv_heads, G, max_len, n_splits;
+  int waves;         // waves per split workgroup
   float scale_log2;  // scale * log2(e)
   // RoPE-fused form: q (= qkv rows) is the raw stacked projection output
   // [batch, (q_heads + 2 kv_heads) * D] with row stride q_sb; the new token's
@@ -151,13 +155,15 @@ __device__ inline void unpack8(u32x4 w, float (&f)[8]) {
   }
 }
 
-template <class XT, int G, bool ROPE>
-__global__ void __launch_bounds__(kAttnThreads)
+template <class XT, int G, bool ROPE, int W>
+__global__ void __launch_bounds__(W * kWave)
 attn_split_kernel(AttnArgs a) {
-  constexpr int kWaves = kAttnThreads / kWave;
-  constexpr int kKeysW = kAttnChunk / kWaves;   // keys per wave: two 16-key MFMA blocks
+  constexpr int kWaves = W;
+  constexpr int kThreads = W * kWave;
+  constexpr int kKeysW = kAttnKeysPerWave;      // keys per wave: two 16-key MFMA blocks
   constexpr int kSteps = kKeysW / 4;            // PV: 8 keys per lane
   static_assert(kKeysW == 32 && G <= 16, "two 16-key blocks per wave, at most 16 query heads");
+  static_assert(!ROPE || 16 * (G + 2) <= kThreads, "the RoPE prologue needs 16 (G + 2) threads");
   __shared__ float wo[kWaves][G][kAttnD];   // per-wave unnormalised o
   __shared__ float wml[kWaves][G][2];       // per-wave max, sum
   __shared__ __align__(16) float pl[kWaves][G][kKeysW];   // per-wave probabilities [head][key]
@@ -165,7 +171,11 @@ attn_split_kernel(AttnArgs a) {
   const int s = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads, kvh = blockIdx.y - (blockIdx.y / a.kv_heads) * a.kv_heads;
   const int len = min(max(a.seq_used[b], 0), a.max_len);
-  const int key0 = s * kAttnChunk, wkey0 = key0 + wave * kKeysW;
+  // this split's keys: [key0, hi), the sequence cut into n_splits chunks of
+  // C <= 32 W keys (so every split has work and the CUs get equal shares)
+  const int C = max(1, (len + a.n_splits - 1) / a.n_splits);
+  const int key0 = s * C, hi = min(key0 + C, len);
+  const int wkey0 = key0 + wave * kKeysW;
   const int kl = lane >> 4, ch = lane & 15;   // PV layout: keys 8 kl .. 8 kl + 7, 8-element chunk ch
   const int mr = lane & 15, mg = lane >> 4;   // MFMA layout: row / column index, k group
 
@@ -214,7 +224,7 @@ attn_split_kernel(AttnArgs a) {
   const __amdgpu_buffer_rsrc_t krs = row_rsrc(a.k + kv_base, span);
   const __amdgpu_buffer_rsrc_t vrs = row_rsrc(a.v + kv_base, span);
   // a key past the prefix gets an offset past the span (rows are not always packed: kv_sl >= D)
-  auto kv_off = [&](int key, int chunk) { return key < len ? (int)(((int64_t)key * a.kv_sl + chunk * 8) * 2) : span; };
+  auto kv_off = [&](int key, int chunk) { return key < hi ? (int)(((int64_t)key * a.kv_sl + chunk * 8) * 2) : span; };
   u32x4 kb[2][4], vw[kSteps];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
@@ -236,7 +246,8 @@ attn_split_kernel(AttnArgs a) {
   u32x4 kn[4], vnw{};
   int pk = -1;
   if constexpr (ROPE) {
-    const bool mine = pos >= 0 && pos < a.max_len && pos / kAttnChunk == s;
+    // the split whose chunk holds the position (the last one past the length)
+    const bool mine = pos >= 0 && pos < a.max_len && min(pos / C, (int64_t)a.n_splits - 1) == s;
     if (it < G + 2) {
       const u32x4 r = it <= G ? rope8<XT>(own, partner, cw, sw, ich < 8) : own;
       rq[it][ich] = r;
@@ -280,7 +291,7 @@ attn_split_kernel(AttnArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int key = wkey0 + 16 * blk + 4 * mg + v;
       const float raw = (ROPE && key == pk) ? snew[v] : sacc[blk][v];
-      pr[blk][v] = key < len ? raw * a.scale_log2 : -INFINITY;
+      pr[blk][v] = key < hi ? raw * a.scale_log2 : -INFINITY;
     }
   float mx = fmaxf(fmaxf(fmaxf(pr[0][0], pr[0][1]), fmaxf(pr[0][2], pr[0][3])),
                    fmaxf(fmaxf(pr[1][0], pr[1][1]), fmaxf(pr[1][2], pr[1][3])));
@@ -343,7 +354,7 @@ attn_split_kernel(AttnArgs a) {
   __syncthreads();
   // ---- combine the waves in wave order, rescaled to the chunk max; one
   //      partial record per query head: o[D], m, l (m in log2 units)
-  for (int e = t; e < G * kAttnD; e += kAttnThreads) {
+  for (int e = t; e < G * kAttnD; e += kThreads) {
     const int g = e / kAttnD, d = e - g * kAttnD;
     float M = wml[0][g][0];
 #pragma unroll
@@ -499,20 +510,80 @@ static void launch_merge(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* s
   }
 }
 
-static int attn_splits(int max_len) { return (max_len + kAttnChunk - 1) / kAttnChunk; }
+// Split plan.  Workgroups are dealt evenly to the compute units, so the
+// split kernel ends when the most loaded CU is done: pick the waves per
+// workgroup W and the split count S (each split <= 32 W keys) that minimise
+// that CU's keys, ceil(pairs S / CUs) * ceil(max_len / S); ties go to fewer
+// splits (a cheaper merge), then fewer waves.  B = 4 x 8 kv heads at 2304
+// keys: 3 waves x 24 splits (768 workgroups, 3 per CU) instead of 18 splits of
+// 128 keys (576 workgroups: a quarter of the CUs carried a third one and
+// finished last).  The split count is capped (at most 64 below 2048 keys),
+// which bounds the workspace.
+static int attn_split_cap(int max_len) {
+  const int s_big = (max_len + kAttnMaxWaves * kAttnKeysPerWave - 1) / (kAttnMaxWaves * kAttnKeysPerWave);
+  return max(s_big, min(64, (max_len + kAttnKeysPerWave - 1) / kAttnKeysPerWave));
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
+struct AttnPlan {
+  int S, W;
+};
+
+static AttnPlan attn_plan(int max_len, int pairs, int G, bool rope, int cus) {
+  AttnPlan best{attn_split_cap(max_len), kAttnMaxWaves};
+  int64_t best_load = -1;
+  const int cap = attn_split_cap(max_len);
+  for (int W = 2; W <= kAttnMaxWaves; ++W) {
+    if (rope && 16 * (G + 2) > W * kWave) continue;
+    const int per = W * kAttnKeysPerWave;
+    for (int S = (max_len + per - 1) / per; S <= cap; ++S) {
+      const int64_t rounds = ((int64_t)pairs * S + cus - 1) / cus;
+      const int64_t load = rounds * ((max_len + S - 1) / S);
+      if (best_load < 0 || load < best_load || (load == best_load && (S < best.S || (S == best.S && W < best.W)))) {
+        best = AttnPlan{S, W};
+        best_load = load;
+      }
+    }
+  }
+  return best;
+}
+
+template <class XT, int G, bool ROPE, int W>
+static void launch_split_gw(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (!ROPE || 16 * (G + 2) <= W * kWave)
+    hipLaunchKernelGGL((attn_split_kernel<XT, G, ROPE, W>), grid, dim3(W * kWave), 0, s, a);
+}
+
+template <class XT, int G, bool ROPE>
+static void launch_split_g(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  switch (a.waves) {
+    case 2: launch_split_gw<XT, G, ROPE, 2>(a, grid, s); break;
+    case 3: launch_split_gw<XT, G, ROPE, 3>(a, grid, s); break;
+    default: launch_split_gw<XT, G, ROPE, 4>(a, grid, s); break;
+  }
+}
 
 template <class XT, bool ROPE = false>
 static void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
-  const dim3 block(kAttnThreads);
   switch (a.G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<XT, 1, ROPE>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<XT, 2, ROPE>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((attn_split_kernel<XT, 3, ROPE>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<XT, 4, ROPE>), grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL((attn_split_kernel<XT, 5, ROPE>), grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL((attn_split_kernel<XT, 6, ROPE>), grid, block, 0, s, a); break;
-    case 7: hipLaunchKernelGGL((attn_split_kernel<XT, 7, ROPE>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<XT, 8, ROPE>), grid, block, 0, s, a); break;
+    case 1: launch_split_g<XT, 1, ROPE>(a, grid, s); break;
+    case 2: launch_split_g<XT, 2, ROPE>(a, grid, s); break;
+    case 3: launch_split_g<XT, 3, ROPE>(a, grid, s); break;
+    case 4: launch_split_g<XT, 4, ROPE>(a, grid, s); break;
+    case 5: launch_split_g<XT, 5, ROPE>(a, grid, s); break;
+    case 6: launch_split_g<XT, 6, ROPE>(a, grid, s); break;
+    case 7: launch_split_g<XT, 7, ROPE>(a, grid, s); break;
+    default: launch_split_g<XT, 8, ROPE>(a, grid, s); break;
   }
 }
 
@@ -522,14 +593,14 @@ using namespace tq;
 
 extern "C" int64_t tq_decode_attention_workspace_elems(int batch, int q_heads, int max_len) {
   if (batch <= 0 || q_heads <= 0 || max_len <= 0) return 0;
-  return (int64_t)batch * q_heads * attn_splits(max_len) * (kAttnD + 2);
+  return (int64_t)batch * q_heads * attn_split_cap(max_len) * (kAttnD + 2);
 }
 
 static int attn_setup(AttnArgs& a, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
                       const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
                       const int32_t* seq_used, void* out, int64_t out_stride_b, int64_t out_stride_h, int dtype,
                       int batch, int q_heads, int kv_heads, int head_dim, int max_len, float scale,
-                      float* workspace, int64_t workspace_elems) {
+                      float* workspace, int64_t workspace_elems, bool rope) {
   if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || max_len < 0) return TQ_ERR_ARG;
   if (head_dim != kAttnD || q_heads % kv_heads != 0 || q_heads / kv_heads > kAttnMaxG) return TQ_ERR_ARG;
@@ -549,7 +620,10 @@ static int attn_setup(AttnArgs& a, const void* q, int64_t q_stride_b, int64_t q_
   a.out = static_cast<uint16_t*>(out); a.o_sb = out_stride_b; a.o_sh = out_stride_h;
   a.part = workspace;
   a.batch = batch; a.q_heads = q_heads; a.kv_heads = kv_heads; a.G = q_heads / kv_heads;
-  a.max_len = max_len; a.n_splits = attn_splits(max_len);
+  a.max_len = max_len;
+  const AttnPlan plan = attn_plan(max_len, batch * kv_heads, a.G, rope, device_cus());
+  a.n_splits = plan.S;
+  a.waves = plan.W;
   a.scale_log2 = scale * kLog2e;
   return 1;   // ready to launch
 }
@@ -563,7 +637,7 @@ extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
   AttnArgs a{};
   const int rc = attn_setup(a, q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_l, kv_stride_h, seq_used,
                             out, out_stride_b, out_stride_h, dtype, batch, q_heads, kv_heads, head_dim, max_len,
-                            scale, workspace, workspace_elems);
+                            scale, workspace, workspace_elems, false);
   if (rc != 1) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 g1(a.n_splits, batch * kv_heads);
@@ -588,7 +662,7 @@ extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int6
   AttnArgs a{};
   const int rc = attn_setup(a, q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_l, kv_stride_h, seq_used,
                             out, out_stride_b, out_stride_h, dtype, batch, q_heads, kv_heads, head_dim, max_len,
-                            scale, workspace, workspace_elems);
+                            scale, workspace, workspace_elems, false);
   if (rc != 1) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 g1(a.n_splits, batch * kv_heads);
@@ -617,7 +691,7 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
   AttnArgs a{};
   const int rc = attn_setup(a, qkv, qkv_stride, head_dim, k_cache, v_cache, cache_stride_b, cache_stride_l,
                             cache_stride_h, seq_used, out, out_stride_b, out_stride_h, dtype, batch, q_heads,
-                            kv_heads, head_dim, max_len, scale, workspace, workspace_elems);
+                            kv_heads, head_dim, max_len, scale, workspace, workspace_elems, true);
   if (rc != 1) return rc;
   a.cos = static_cast<const uint16_t*>(cos_table);
   a.sin = static_cast<const uint16_t*>(sin_table);
