@@ -309,13 +309,14 @@ def test_rope_cache_matches_module_ops():
     assert int(kc[:, :, :pos].abs().sum()) == 0 and int(vc[:, :, pos + 1:].abs().sum()) == 0
 
 
-def test_attention_quant_equals_attention_then_quantizer():
-    B, Hq, Hkv, L, D = 4, 24, 8, 700, 128
-    g = torch.Generator().manual_seed(9)
+@pytest.mark.parametrize("B,L", [(4, 700), (7, 700), (13, 300), (16, 9000)])
+def test_attention_quant_equals_attention_then_quantizer(B, L):
+    Hq, Hkv, D = 24, 8, 128
+    g = torch.Generator().manual_seed(9 + B)
     q = torch.randn((B, Hq, D), generator=g).to(torch.bfloat16).to(DEV)
     k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
     v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
-    seq = torch.tensor([700, 1, 129, 400], dtype=torch.int32, device=DEV)
+    seq = torch.tensor(([L, 1, 129, 400] * 4)[:B], dtype=torch.int32, device=DEV)
     ref = decode_attention(q, k, v, seq, scale=D ** -0.5)
     out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=DEV)
     qo = torch.empty((B, Hq * D), dtype=torch.int8, device=DEV)

@@ -433,67 +433,128 @@ attn_merge_kernel(AttnArgs a) {
 }
 
 // Merge + INT8 quantization of the attention output for the next projection:
-// workgroup h = query head h for ALL batch rows (b < batch <= 16), 4 row
-// groups x 128 dimensions (a row group is two whole waves).  Dimensions
-// 0..63 / 64..127 of the head are column tiles 2h / 2h + 1 of the
-// [batch, q_heads * 128] projection input, so both tiles are whole inside the
-// workgroup: absmax over the batch rows, scale, codes -- the closed form of
-// tq_act_quant, bit for bit.
+// workgroup (h, half) = column tile 2h + half of the [batch, q_heads * 128]
+// projection input (dimensions 64 half .. 64 half + 63 of query head h) for
+// ALL batch rows (b < batch <= 16): wave rg takes rows rg, rg + 4, ... (RPW
+// per wave), lane = dimension.  The tile is whole inside the workgroup:
+// absmax over the batch rows, scale, codes -- the closed form of
+// tq_act_quant, bit for bit.  Per batch of NB splits every load goes out at
+// once: the lanes' o values first, then each (row, split)'s (m, l) pair once
+// per workgroup (into LDS), so one round trip serves the batch and no lane
+// re-reads the pairs.
 constexpr int kMergeQuantMaxRows = 16;
-constexpr int kMergeQuantThreads = 512;   // 4 row groups x 128 dimensions
+constexpr int kMergeQuantThreads = 256;   // 4 waves (row groups) x 64 dimensions
 
-template <class XT, int NB>
+template <class XT, int NB, int RPW>
 __global__ void __launch_bounds__(kMergeQuantThreads)
 attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
-  __shared__ float red[kMergeQuantThreads / kWave];
-  const int h = blockIdx.x, t = threadIdx.x, d = t & (kAttnD - 1);
-  const int rg = t / kAttnD;   // row group
-  constexpr int kGroups = kMergeQuantThreads / kAttnD;
-  constexpr int kPer = kMergeQuantMaxRows / kGroups;
-  float y[kPer];
-  float am = 0.0f;
-  // every row merged before the first store: no store can alias a partial still to be read
+  constexpr int kGroups = kMergeQuantThreads / kWave;
+  __shared__ float2 mls[kGroups * RPW][NB];
+  __shared__ float red[kGroups];
+  const int h = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const int t = threadIdx.x, lane = t & 63, rg = t >> 6;
+  const int d = half * 64 + lane;
+  const int S = a.n_splits;
+  const int64_t rec_elems = (int64_t)S * (kAttnD + 2);   // one (b, h)'s records
+  __amdgpu_buffer_rsrc_t rs[RPW];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int b = rg + kGroups * i;
-    y[i] = 0.0f;
-    if (b < a.batch) {
-      const float* rec = a.part + (int64_t)(b * a.q_heads + h) * a.n_splits * (kAttnD + 2);
-      y[i] = XT::round(merge_splits<NB>(a, rec, d));
-      am = fmaxf(am, fabsf(y[i]));
+  for (int i = 0; i < RPW; ++i) {
+    const int b = rg + kGroups * i;   // rows past the batch: empty range, loads read 0
+    rs[i] = row_rsrc(a.part + (int64_t)(min(b, a.batch - 1) * a.q_heads + h) * rec_elems,
+                     b < a.batch ? (int)(rec_elems * 4) : 0);
+  }
+  const int n_ml = a.batch * NB;
+  float M[RPW], L[RPW], acc[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    M[i] = -INFINITY;
+    L[i] = 0.0f;
+    acc[i] = 0.0f;
+  }
+  for (int s0 = 0; s0 < S; s0 += NB) {
+    float o[RPW][NB];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        o[i][j] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rs[i], (int)(((int64_t)min(s0 + j, S - 1) * (kAttnD + 2) + d) * 4), 0, 0));
+    // (m, l) of entries e = (row b, split s0 + j), issued after the o loads
+    // (the wait for them then covers those too); padding splits get m = -inf
+    constexpr int kML = (kGroups * RPW * NB + kMergeQuantThreads - 1) / kMergeQuantThreads;
+    float2 ml[kML];
+#pragma unroll
+    for (int u = 0; u < kML; ++u) {
+      const int e = min(t + u * kMergeQuantThreads, n_ml - 1), eb = e / NB, ej = e - eb * NB;
+      ml[u] = *reinterpret_cast<const float2*>(a.part + (int64_t)(eb * a.q_heads + h) * rec_elems +
+                                               (int64_t)min(s0 + ej, S - 1) * (kAttnD + 2) + kAttnD);
     }
-  }
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int b = rg + kGroups * i;
-    if (b < a.batch) a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(y[i]);
+    for (int u = 0; u < kML; ++u) {
+      const int e = t + u * kMergeQuantThreads, eb = e / NB, ej = e - eb * NB;
+      if (e < n_ml) mls[eb][ej] = float2{s0 + ej < S ? ml[u].x : -INFINITY, ml[u].y};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int b = min(rg + kGroups * i, a.batch - 1);
+      // the same arithmetic as merge_splits: batch max, rescale, weighted sums in split order
+      float Mb = M[i];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) Mb = fmaxf(Mb, mls[b][j].x);
+      const bool any = Mb != -INFINITY;
+      const float r = any ? exp2f(M[i] - Mb) : 1.0f;
+      L[i] *= r;
+      acc[i] *= r;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const float2 mj = mls[b][j];
+        const float w = mj.x == -INFINITY ? 0.0f : exp2f(mj.x - Mb);
+        L[i] = fmaf(w, mj.y, L[i]);
+        acc[i] = fmaf(w, o[i][j], acc[i]);
+      }
+      M[i] = any ? Mb : M[i];
+    }
+    __syncthreads();   // the next batch rewrites mls
   }
-  // column tile 2h + (d >= 64): waves with the same parity hold the same half
+  float y[RPW];
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const bool live = rg + kGroups * i < a.batch;
+    y[i] = live ? XT::round(L[i] > 0.0f ? acc[i] / L[i] : 0.0f) : 0.0f;
+    am = fmaxf(am, fabsf(y[i]));
+  }
   const float wm = wave_max_nonneg(am);
-  const int wave = t >> 6, lane = t & 63;
-  if (lane == 0) red[wave] = wm;
+  if (lane == 0) red[rg] = wm;
   __syncthreads();
-  float tm = 0.0f;
-  for (int w = (wave & 1); w < kMergeQuantThreads / kWave; w += 2) tm = fmaxf(tm, red[w]);
+  const float tm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float s = act_scale_from_absmax<XT>(tm);
   const CodeScale cs(s);
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
+  for (int i = 0; i < RPW; ++i) {
     const int b = rg + kGroups * i;
-    if (b < a.batch) q[(int64_t)b * ldq + h * kAttnD + d] = (int8_t)cs.code(y[i]);
+    if (b < a.batch) {
+      a.out[(int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d] = XT::from_f32(y[i]);
+      q[(int64_t)b * ldq + h * kAttnD + d] = (int8_t)cs.code(y[i]);
+    }
   }
-  if (t < kAttnD && (d & 63) == 0) sx[2 * h + (d >> 6)] = s;
+  if (t == 0) sx[2 * h + half] = s;
 }
 
 // Merge launches: NB = splits rounded up to 8 (at most kMergeBatch), so no
 // load of a batch is wasted on padding below kMergeBatch splits.
 template <class XT, int NB>
 static void launch_merge_nb(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, hipStream_t s) {
-  if (q_out)
-    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB>), dim3(a.q_heads), dim3(kMergeQuantThreads), 0, s, a, q_out,
-                       ldq, sx);
-  else
+  const dim3 gq(a.q_heads * 2), bq(kMergeQuantThreads);
+  if (!q_out)
     hipLaunchKernelGGL((attn_merge_kernel<XT, NB>), dim3(a.batch * a.q_heads), dim3(kAttnD), 0, s, a);
+  else if (a.batch <= 4)
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 1>), gq, bq, 0, s, a, q_out, ldq, sx);
+  else if (a.batch <= 8)
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 2>), gq, bq, 0, s, a, q_out, ldq, sx);
+  else
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 4>), gq, bq, 0, s, a, q_out, ldq, sx);
 }
 
 template <class XT>
