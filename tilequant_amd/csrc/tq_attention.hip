@@ -164,7 +164,11 @@ attn_split_kernel(AttnArgs a) {
   constexpr int kSteps = kKeysW / 4;            // PV: 8 keys per lane
   static_assert(kKeysW == 32 && G <= 16, "two 16-key blocks per wave, at most 16 query heads");
   static_assert(!ROPE || 16 * (G + 2) <= kThreads, "the RoPE prologue needs 16 (G + 2) threads");
-  __shared__ float wo[kWaves][G][kAttnD];   // per-wave unnormalised o
+  // per-wave unnormalised o; for G <= 4 per key group kl as well (summed in
+  // the combine instead of by cross-lane butterflies in every wave)
+  constexpr bool kLdsSum = G <= 4;
+  constexpr int KG = kLdsSum ? 4 : 1;
+  __shared__ __align__(16) float wo[kWaves][KG][G][kAttnD];
   __shared__ float wml[kWaves][G][2];       // per-wave max, sum
   __shared__ __align__(16) float pl[kWaves][G][kKeysW];   // per-wave probabilities [head][key]
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -344,13 +348,21 @@ attn_split_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pg[g][i], vf[e], o[g][e]);
   }
+  if constexpr (kLdsSum) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = rows4_sum(o[g][e]);
-      if (kl == 0) wo[wave][g][ch * 8 + e] = x;
+    for (int g = 0; g < G; ++g) {
+      *reinterpret_cast<v4f*>(&wo[wave][kl][g][ch * 8]) = v4f{o[g][0], o[g][1], o[g][2], o[g][3]};
+      *reinterpret_cast<v4f*>(&wo[wave][kl][g][ch * 8 + 4]) = v4f{o[g][4], o[g][5], o[g][6], o[g][7]};
     }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = rows4_sum(o[g][e]);
+        if (kl == 0) wo[wave][0][g][ch * 8 + e] = x;
+      }
+  }
   __syncthreads();
   // ---- combine the waves in wave order, rescaled to the chunk max; one
   //      partial record per query head: o[D], m, l (m in log2 units)
@@ -364,7 +376,11 @@ attn_split_kernel(AttnArgs a) {
     for (int w = 0; w < kWaves; ++w) {
       const float mwv = wml[w][g][0];
       const float c = mwv == -INFINITY ? 0.0f : exp2f(mwv - M);
-      O = fmaf(c, wo[w][g][d], O);
+      // the wave's key groups in the association of the butterflies: (0 + 1) + (2 + 3)
+      const float ow = kLdsSum ? (wo[w][0][g][d] + wo[w][KG > 1 ? 1 : 0][g][d]) +
+                                     (wo[w][KG > 2 ? 2 : 0][g][d] + wo[w][KG > 3 ? 3 : 0][g][d])
+                               : wo[w][0][g][d];
+      O = fmaf(c, ow, O);
       L = fmaf(c, wml[w][g][1], L);
     }
     float* rec = a.part + ((int64_t)(b * a.q_heads + kvh * G + g) * a.n_splits + s) * (kAttnD + 2);
