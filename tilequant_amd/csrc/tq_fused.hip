@@ -80,6 +80,21 @@ __device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const void* p, int64_t ld, in
 
 // workgroup c: every row's sum of squares over all k columns (each wave takes
 // rows wave, wave + 4, ...), then the 64 columns of tile c for every row.
+// acc + lo^2 + hi^2 of a packed pair of 16-bit values (v_dot2_f32_bf16 /
+// v_dot2_f32_f16: exact products, fp32 sums)
+template <class XT>
+__device__ inline float dot2sq(uint32_t w, float acc) {
+  if constexpr (std::is_same<XT, Bf16>::value) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 v = __builtin_bit_cast(bf2, w);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = __builtin_bit_cast(h2, w);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+}
+
 template <class XT>
 __global__ void __launch_bounds__(kFuseThreads)
 add_rmsnorm_quant_kernel(NormArgs a) {
@@ -132,10 +147,14 @@ add_rmsnorm_quant_kernel(NormArgs a) {
 #pragma unroll
       for (int j = 0; j < kNormBatch; ++j) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float xf = XT::to_f32((uint16_t)(xv[j][i >> 1] >> (16 * (i & 1))));
-          const float hv = has_delta ? XT::round(xf + XT::to_f32((uint16_t)(dv[j][i >> 1] >> (16 * (i & 1))))) : xf;
-          ssj[j] = fmaf(hv, hv, ssj[j]);
+        for (int i = 0; i < 4; ++i) {
+          // h of two elements, rounded as a pair (one v_cvt_pk_*), then both
+          // squares in one v_dot2 (exact products, fp32 sums)
+          const uint32_t xw = xv[j][i], dw = dv[j][i];
+          const uint32_t hp = has_delta ? XT::pack2(XT::to_f32((uint16_t)xw) + XT::to_f32((uint16_t)dw),
+                                                    XT::to_f32((uint16_t)(xw >> 16)) + XT::to_f32((uint16_t)(dw >> 16)))
+                                        : xw;
+          ssj[j] = dot2sq<XT>(hp, ssj[j]);
         }
       }
     }
