@@ -40,6 +40,8 @@
 // launch per layer, bit for bit.
 #include "tq_common.h"
 
+#include <atomic>
+
 namespace tq {
 
 constexpr int kAttnD = 128;            // head dimension served
@@ -601,14 +603,19 @@ static int attn_split_cap(int max_len) {
   return max(s_big, min(64, (max_len + kAttnKeysPerWave - 1) / kAttnKeysPerWave));
 }
 
+// CU count of the current device, cached per device (threads may launch
+// concurrently; they store the same value)
 static int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  if (dev < 64) cached[dev] = n;
+  if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
