@@ -152,6 +152,22 @@ def test_all_int8_all_bf16_and_half(frac):
     assert_gemm_close(y, acc, sab, pack.n_tc)
 
 
+@pytest.mark.parametrize("m,k,frac,n", [(256, 8192, 1.0, 1), (256, 8192, 1.0, 4), (320, 8192, 0.9, 16),
+                                        (12288, 1024, 0.9, 12), (512, 18944, 0.97, 4)])
+def test_decode_rows_with_many_16bit_tiles(m, k, frac, n):
+    """Row tiles that are (almost) all 16-bit: each wave takes dozens of 16-bit
+    tiles past its first ones (batched loads; one-j-block and whole-tile
+    workgroups)."""
+    W, pack, ids16 = _case(m, k, frac, seed=m + k + n)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=m + n)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y = _gemm(pack, xd, xq, sx)
+    acc, sab = _oracle_f64(pack, op, x, *nm.act_quant(values(x)))
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
 def test_bias_fp16_output_and_out_slices():
     W, pack, ids16 = _case(384, 640, 0.05, seed=500)
     op = oracle_pack(W, ids16)

@@ -858,10 +858,43 @@ gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
   for (int u = 0; u < U16; ++u)
     if (first16 + u * W < n16) tile16(b16p[u], __builtin_amdgcn_readlane(id16l, u));
-  for (int q = first16 + U16 * W; q < n16; q += W) {
-    v4i b16[JBW][2];
-    load_w16_at(b16, q);
-    tile16(b16, __builtin_amdgcn_raw_buffer_load_b32(i16rs, q * 4, 0, 0));
+  // The wave's remaining 16-bit tiles (positions q0 + i W, ascending: the
+  // same order as one at a time): the ids of up to 64 come with one vector
+  // load, then each batch of U16B tiles issues its weights and activation
+  // operands together -- one round trip per batch instead of two per tile
+  // (rows that are mostly 16-bit, as clustered masks give, have dozens).
+  // Rows past n read row n - 1: their products land in output rows that are
+  // never stored.
+  constexpr int U16B = JBW == 1 ? 4 : 2;
+  for (int q0 = first16 + U16 * W; q0 < n16; q0 += 64 * W) {
+    const int idv = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (q0 + lane * W) * 4, 0, 0);
+    const int cnt = min(64, (n16 - q0 + W - 1) / W);
+    for (int i0 = 0; i0 < cnt; i0 += U16B) {
+      v4i bb[U16B][JBW][2], ab[U16B][TB][2];
+#pragma unroll
+      for (int u = 0; u < U16B; ++u) {
+        const int i = min(i0 + u, cnt - 1);   // past the end: the last tile again, not used
+        load_w16_at(bb[u], q0 + i * W);
+        const int c = col_of(__builtin_amdgcn_readlane(idv, i), rbase, n_tc);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            ab[u][tb][h] = *reinterpret_cast<const v4i*>(a.xf + (int64_t)min(tb * 16 + arow, a.n - 1) * a.ldx +
+                                                          c * 64 + h * 32 + akq * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < U16B; ++u)
+        if (i0 + u < cnt) {
+#pragma unroll
+          for (int j = 0; j < JBW; ++j)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+              acc[j][tb] = mfma16<XT>(ab[u][tb][0], bb[u][j][0], acc[j][tb]);
+              acc[j][tb] = mfma16<XT>(ab[u][tb][1], bb[u][j][1], acc[j][tb]);
+            }
+        }
+    }
   }
 
   // ---- waves -> LDS (reusing the code area) -> sum in wave order -> store
