@@ -151,6 +151,14 @@ int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
  * Replaces the torch.ops.aten._flash_attention_forward(..., seqused_k=...)
  * call of _cuda_graph_attention (src/runtime/graph_decode.py:56-71). */
 int64_t tq_decode_attention_workspace_elems(int batch, int q_heads, int max_len);
+/* The split plan the attention entry points use for a device with `cus`
+ * compute units (no GPU needed): *n_splits chunks of each sequence, *waves
+ * waves of 32 keys per split workgroup, chosen so every CU gets the same
+ * keys.  No reference counterpart (flash-decoding's split heuristic lives
+ * inside aten._flash_attention_forward, src/runtime/graph_decode.py:56-71);
+ * exposed for tests and capacity planning. */
+int tq_decode_attention_plan(int batch, int q_heads, int kv_heads, int max_len, int rope, int cus,
+                             int* n_splits, int* waves);
 int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
                         const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
                         const int32_t* seq_used, void* out, int64_t out_stride_b, int64_t out_stride_h,

@@ -74,3 +74,42 @@ def test_workspace_sizing(lib):
     assert lib.tq_gemm_workspace_elems(16, 16384, 256, 48, 8) == 4096 + 256 * 8 * 16 * 64
     assert lib.tq_gemm_workspace_elems(4, 1 << 20, 1 << 14, 48, 8) == 0   # beyond the counter cap
     assert lib.tq_gemm_workspace_elems(100, 3072, 48, 48, 0) == 0     # general kernel: none
+
+
+def _attention_plan(lib, batch, q_heads, kv_heads, max_len, rope, cus):
+    s, w = ctypes.c_int(0), ctypes.c_int(0)
+    rc = lib.tq_decode_attention_plan(batch, q_heads, kv_heads, max_len, int(rope), cus, ctypes.byref(s),
+                                      ctypes.byref(w))
+    assert rc == 0
+    return s.value, w.value
+
+
+@pytest.mark.parametrize("batch,q_heads,kv_heads,max_len,rope", [
+    (4, 24, 8, 2304, True), (4, 24, 8, 2304, False), (1, 24, 8, 2304, True), (4, 28, 4, 2304, True),
+    (4, 40, 8, 2304, True), (2, 7, 1, 300, True), (1, 8, 1, 64, False), (3, 40, 8, 513, True),
+    (2, 8, 2, 8400, False), (16, 24, 8, 9000, False), (1, 8, 2, 131072, False), (5, 8, 8, 1, True)])
+def test_decode_attention_plan_invariants(lib, batch, q_heads, kv_heads, max_len, rope):
+    """The split plan (host logic of tq_decode_attention*): every split fits its
+    workgroup (<= 32 keys per wave), the RoPE prologue has its 16 (G + 2)
+    threads, the workspace covers the plan, and no other (waves, splits) choice
+    gives the most loaded CU fewer keys."""
+    cus = 256
+    S, W = _attention_plan(lib, batch, q_heads, kv_heads, max_len, rope, cus)
+    G = q_heads // kv_heads
+    assert 2 <= W <= 4 and S >= 1
+    assert -(-max_len // S) <= 32 * W
+    if rope:
+        assert 16 * (G + 2) <= 64 * W
+    assert lib.tq_decode_attention_workspace_elems(batch, q_heads, max_len) >= batch * q_heads * S * 130
+    cap = max(-(-max_len // 128), min(64, -(-max_len // 32)))
+    assert S <= cap
+    load = lambda s: -(-(batch * kv_heads * s) // cus) * -(-max_len // s)
+    best = min(load(s) for w in (2, 3, 4) if not (rope and 16 * (G + 2) > 64 * w)
+               for s in range(-(-max_len // (32 * w)), cap + 1))
+    assert load(S) == best
+
+
+def test_decode_attention_plan_balances_the_llama_decode_shape(lib):
+    # B = 4 x 8 kv heads at 2304 keys: 24 splits of 3 waves = 768 workgroups, 3 per CU
+    assert _attention_plan(lib, 4, 24, 8, 2304, True, 256) == (24, 3)
+    assert lib.tq_decode_attention_plan(0, 24, 8, 2304, 1, 256, None, None) != 0

@@ -51,6 +51,7 @@ _SIGNATURES = {
                                    _i, _i, _p, _i64, _p]),
     "tq_gemm_tile_products_i32": (_i, [_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
     "tq_decode_attention_workspace_elems": (_i64, [_i, _i, _i]),
+    "tq_decode_attention_plan": (_i, [_i, _i, _i, _i, _i, _i, _p, _p]),
     "tq_decode_attention": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                  _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
     "tq_decode_attention_quant": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,

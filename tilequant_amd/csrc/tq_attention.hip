@@ -675,6 +675,17 @@ static void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
 
 using namespace tq;
 
+extern "C" int tq_decode_attention_plan(int batch, int q_heads, int kv_heads, int max_len, int rope, int cus,
+                                        int* n_splits, int* waves) {
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || max_len <= 0 || cus <= 0 || q_heads % kv_heads != 0 ||
+      q_heads / kv_heads > kAttnMaxG || n_splits == nullptr || waves == nullptr)
+    return TQ_ERR_ARG;
+  const AttnPlan p = attn_plan(max_len, batch * kv_heads, q_heads / kv_heads, rope != 0, cus);
+  *n_splits = p.S;
+  *waves = p.W;
+  return TQ_OK;
+}
+
 extern "C" int64_t tq_decode_attention_workspace_elems(int batch, int q_heads, int max_len) {
   if (batch <= 0 || q_heads <= 0 || max_len <= 0) return 0;
   return (int64_t)batch * q_heads * attn_split_cap(max_len) * (kAttnD + 2);
