@@ -44,7 +44,7 @@ def _attention_reference(q, k, v, lens, scale):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,L", [(4, 24, 8, 2304), (2, 7, 1, 300), (1, 8, 1, 64), (3, 40, 8, 513),
-                                          (2, 8, 2, 8400)])
+                                          (2, 8, 2, 8400), (3, 6, 3, 500), (2, 6, 1, 700), (1, 4, 4, 1000)])
 @pytest.mark.parametrize("token_major", [False, True])
 def test_decode_attention_matches_reference(B, Hq, Hkv, L, token_major):
     g = torch.Generator().manual_seed(B * 1000 + L)
@@ -336,7 +336,9 @@ def test_attention_quant_equals_attention_then_quantizer(B, L):
 
 @pytest.mark.parametrize("B,hq,hkv,L,pos,quant", [(4, 24, 8, 2304, 2047, True), (4, 24, 8, 700, 128, False),
                                                     (2, 7, 1, 300, 0, True), (3, 40, 8, 513, 127, True),
-                                                    (1, 8, 2, 256, 255, False), (2, 24, 8, 300, 300, True)])
+                                                    (1, 8, 2, 256, 255, False), (2, 24, 8, 300, 300, True),
+                                                    (3, 6, 3, 500, 411, True), (2, 6, 1, 700, 650, False),
+                                                    (5, 4, 4, 1000, 999, True)])
 def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, quant):
     """tq_decode_attention_rope against tq_rope_cache followed by
     tq_decode_attention(_quant): outputs, codes, scales and both caches
