@@ -162,4 +162,7 @@ def test_fused_decode_option_is_bitwise_identical():
         x = make_x(n, 3072, seed=81 + n).cuda()
         y = lin(x)
         assert torch.equal(lin_f(x), y)
-        assert torch.equal(lin_a(x), y)   # "auto": fused up to FUSED_AUTO_MAX_ROWS rows
+        assert torch.equal(lin_a(x), y)   # "auto": fused up to 4 rows here (narrow input, 64 workgroups)
+    assert lin_a._fused_rows_for_cfg() == 4
+    wide, _, _, _ = _linear(256, 8192, 0.01, 82, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    assert wide._fused_rows_for_cfg() == 2   # 8192 columns: quantization repeated per workgroup is too dear

@@ -23,7 +23,8 @@ workgroup quantizes the whole activation into LDS while its weights stream
 in.  That saves a launch (~2.5 us on MI355X) but repeats the quantization in
 every workgroup, so it pays off only for very few rows.  ``cfg.fused_decode``
 selects it: ``None`` / ``"auto"`` (default) for inputs of at most
-``FUSED_AUTO_MAX_ROWS`` rows, ``True`` for every size the fused launch takes
+``FUSED_AUTO_MAX_ROWS`` rows (``FUSED_AUTO_NARROW_ROWS`` for narrow inputs
+whose grid fits the CUs once), ``True`` for every size the fused launch takes
 (at most 16 rows, fewer for very wide inputs), ``False`` never.
 
 The extra state records the packed tiles' storage order (``tile_layout``) so a
@@ -50,6 +51,25 @@ DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 16384
 # Rows up to which cfg.fused_decode = "auto" fuses quantization into the GEMM
 # (measured on MI355X: 1 row saves ~2 us per projection, 4 rows break even).
 FUSED_AUTO_MAX_ROWS = 2
+# ... and up to this many rows when the repeated quantization is cheap: inputs
+# of at most FUSED_AUTO_NARROW_K columns whose decode grid (four workgroups
+# per 64-row output tile) gives no CU a second workgroup.  At 4 rows on MI355X
+# the O projection (3072 x 3072, 192 workgroups) runs fused in 7.4-7.5 us
+# instead of 7.8-8.1 us for quantize + GEMM; Q/K/V (320 workgroups), Gate/Up
+# (1024) and Down (8192 columns) are slower fused.
+FUSED_AUTO_NARROW_ROWS = 4
+FUSED_AUTO_NARROW_K = 4096
+
+
+def _device_cus(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    cus = _CU_COUNT.get(idx)
+    if cus is None:
+        cus = _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return cus
+
+
+_CU_COUNT: Dict[int, int] = {}
 # Sibling projections reuse one activation quantization for inputs of at least
 # this many rows (mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
@@ -188,7 +208,12 @@ class MixedLinear(nn.Module):
         if mode is False:
             return 0
         if mode is None or mode == "auto":
-            return min(FUSED_AUTO_MAX_ROWS, self._fused_limit())
+            rows = FUSED_AUTO_MAX_ROWS
+            dev = self.int8_tiles.device
+            if (dev.type == "cuda" and self.K_orig <= FUSED_AUTO_NARROW_K
+                    and 4 * self.n_tr <= _device_cus(dev)):
+                rows = FUSED_AUTO_NARROW_ROWS
+            return min(rows, self._fused_limit())
         return self._fused_limit()
 
     def _fused_decode(self, x_fp: torch.Tensor) -> torch.Tensor:
