@@ -75,6 +75,19 @@ int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64_t x_stride
                              int x_dtype, int n, int k, const float* sx, int8_t* q,
                              int64_t q_stride_n, void* stream);
 
+/* tq_act_absmax_scales followed by tq_act_quant_with_scales for inputs that
+ * need the two-level scales (more than 512 rows), in two launches instead of
+ * three: the codes kernel reduces its column's absmax partials itself (the
+ * finalize step folded in).  Unit column stride, 16-byte aligned rows, k a
+ * multiple of 64, 8-byte aligned code rows (TQ_ERR_ALIGN otherwise);
+ * workspace = tq_act_absmax_workspace_elems(n, k) floats.  Codes and scales
+ * are bitwise those of the two calls.  No reference counterpart: the
+ * reference's dispatcher (quant_utils.py:119-134) runs the scales kernel and
+ * the codes kernel one after the other. */
+int tq_act_quant_two_level(const void* x, int64_t x_stride_n, int x_dtype, int n, int k, int8_t* q,
+                           int64_t q_stride_n, float* sx, float* workspace, int64_t workspace_elems,
+                           void* stream);
+
 /* ---- mixed INT8/BF16 tile GEMM -----------------------------------------
  * out[n, m] = sum over the INT8 tiles t of output row tile r = m / 64:
  *               f32(int32 dot(x_int8[n, 64c:64c+64], tile_t[m % 64, :])) * (sx[c] * sw[t])

@@ -8,9 +8,11 @@ import torch
 from helpers import make_x, values
 from oracle import numerics as nm
 from tilequant_amd import quant_utils
+from tilequant_amd import _native as nat
 from tilequant_amd.quantize_activation import (
     activation_tile_absmax_scales_64_fused,
     quantize_activation_tile_absmax_fused,
+    quantize_activation_tile_absmax_two_level,
     quantize_activation_tile_with_scales_64_fused,
 )
 
@@ -137,3 +139,37 @@ def test_exact_half_integer_quotients_round_half_even(dtype):
     assert int(qq[0, 64]) == 0 and int(qq[0, 65]) == -2 and int(qq[0, 128]) == 64  # -1.5->-2, 63.5->64
     sx2 = activation_tile_absmax_scales_64_fused(xt.cuda())
     assert torch.equal(quantize_activation_tile_with_scales_64_fused(xt.cuda(), sx2), q)
+
+
+@pytest.mark.parametrize("n,k,dtype", [(513, 64, torch.bfloat16), (1000, 3072, torch.float16),
+                                       (8192, 8192, torch.bfloat16), (4353, 1024, torch.float16)])
+def test_two_level_launch_equals_scales_then_codes(n, k, dtype):
+    """tq_act_quant_two_level (the codes kernel reduces the absmax partials
+    itself) against the oracle and the two-call path, bitwise."""
+    x = make_x(n, k, seed=3000 + n + k, dtype=dtype)
+    xd = x.cuda()
+    q, sx = quantize_activation_tile_absmax_two_level(xd)
+    _check(x, q, sx)
+    sx2 = activation_tile_absmax_scales_64_fused(xd)
+    q2 = quantize_activation_tile_with_scales_64_fused(xd, sx2)
+    assert torch.equal(q, q2) and torch.equal(sx, sx2)
+
+
+def test_two_level_argument_errors():
+    TQ_ERR_ALIGN, TQ_ERR_WORKSPACE = -3, -4   # include/tilequant.h
+    lib = nat.lib()
+    x = torch.zeros((600, 100), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((600, 100), dtype=torch.int8, device="cuda")
+    sx = torch.empty((2,), dtype=torch.float32, device="cuda")
+    ws = torch.empty((1 << 14,), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    # width not a multiple of 64
+    assert lib.tq_act_quant_two_level(x.data_ptr(), 100, 0, 600, 100, q.data_ptr(), 100, sx.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), stream) == TQ_ERR_ALIGN
+    x = torch.zeros((600, 128), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((600, 128), dtype=torch.int8, device="cuda")
+    # too small a workspace, and too few rows for the two-level scales
+    assert lib.tq_act_quant_two_level(x.data_ptr(), 128, 0, 600, 128, q.data_ptr(), 128, sx.data_ptr(),
+                                      ws.data_ptr(), 1, stream) == TQ_ERR_WORKSPACE
+    assert lib.tq_act_quant_two_level(x.data_ptr(), 128, 0, 500, 128, q.data_ptr(), 128, sx.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), stream) == nat.TQ_ERR_ARG

@@ -140,6 +140,44 @@ __global__ void act_scales_finalize_kernel(const float* __restrict__ partial, in
   sx[c] = act_scale_from_absmax<T>(a);
 }
 
+// Codes of rows [rb * kPartialRows, ...) of column tile c, the tile's scale
+// taken from the absmax partials of every row block (the finalize step folded
+// in: every workgroup reduces its column's partials; block 0 stores sx[c]).
+// The row loads go out before the partials are read, so both arrive in one
+// round trip.  Vector layout only (unit column stride, 16-byte aligned rows,
+// k a multiple of 64, 8-byte aligned code rows).  Same closed forms as
+// act_scales_finalize_kernel + act_quant_scaled_kernel, bit for bit.
+template <class T>
+__global__ void __launch_bounds__(kQuantThreads)
+act_quant_block_kernel(XView v, const float* __restrict__ partial, int n_rb, int8_t* __restrict__ q, int64_t ldq,
+                       float* __restrict__ sx) {
+  __shared__ float scale;
+  const int c = blockIdx.x, rb = blockIdx.y, t = threadIdx.x, n_tc = gridDim.x;
+  const int row0 = rb * kPartialRows, row1 = min(v.n, row0 + kPartialRows);
+  const int col = c * kTile + (t % 8) * 8;
+  constexpr int kPer = kPartialRows / kRowsPerPass;
+  u32x4 w[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) w[i] = load8(v, min(row0 + t / 8 + i * kRowsPerPass, row1 - 1), col);
+  if (t < kWave) {
+    float a = 0.0f;
+    for (int i = t; i < n_rb; i += kWave) a = fmaxf(a, partial[(int64_t)i * n_tc + c]);
+    a = wave_max_nonneg(a);
+    if (t == 0) {
+      const float s = act_scale_from_absmax<T>(a);
+      scale = s;
+      if (rb == 0) sx[c] = s;
+    }
+  }
+  __syncthreads();
+  const CodeScale cs(scale);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int row = row0 + t / 8 + i * kRowsPerPass;
+    if (row < row1) *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = codes8<T>(w[i], cs);
+  }
+}
+
 template <class T>
 __global__ void __launch_bounds__(kQuantThreads)
 act_quant_scaled_kernel(XView v, const float* __restrict__ sx, int8_t* __restrict__ q, int64_t ldq,
@@ -261,5 +299,32 @@ extern "C" int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64
     hipLaunchKernelGGL(act_quant_scaled_kernel<Bf16>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, s, v, sx, q, q_stride_n, vec);
   else
     hipLaunchKernelGGL(act_quant_scaled_kernel<Fp16>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, s, v, sx, q, q_stride_n, vec);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_act_quant_two_level(const void* x, int64_t x_stride_n, int x_dtype, int n, int k, int8_t* q,
+                                      int64_t q_stride_n, float* sx, float* workspace, int64_t workspace_elems,
+                                      void* stream) {
+  int rc = check_x(x, x_stride_n, 1, x_dtype, n, k);
+  if (rc) return rc;
+  if (k == 0 || n == 0) return TQ_OK;
+  if (sx == nullptr || q == nullptr || q_stride_n < k) return TQ_ERR_ARG;
+  if ((k % kTile) != 0 || (x_stride_n % 8) != 0 || !aligned16(x) || (q_stride_n % 8) != 0 ||
+      ((uintptr_t)q & 7u) != 0)
+    return TQ_ERR_ALIGN;
+  const int64_t need = tq_act_absmax_workspace_elems(n, k);
+  if (need == 0) return TQ_ERR_ARG;   // few rows: tq_act_quant_fused / single-pass scales
+  if (workspace == nullptr || workspace_elems < need) return TQ_ERR_WORKSPACE;
+  const int n_tc = n_tiles_of(k), n_rb = (n + kPartialRows - 1) / kPartialRows;
+  XView v{static_cast<const uint16_t*>(x), x_stride_n, 1, n, k};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(n_tc, n_rb);
+  if (x_dtype == TQ_DTYPE_BF16) {
+    hipLaunchKernelGGL(act_absmax_partial_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, workspace, kPartialRows, 0);
+    hipLaunchKernelGGL(act_quant_block_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, workspace, n_rb, q, q_stride_n, sx);
+  } else {
+    hipLaunchKernelGGL(act_absmax_partial_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, workspace, kPartialRows, 0);
+    hipLaunchKernelGGL(act_quant_block_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, workspace, n_rb, q, q_stride_n, sx);
+  }
   return (int)hipGetLastError();
 }

@@ -16,7 +16,9 @@ import torch
 from .quantize_activation import (
     activation_tile_absmax_scales_64_fused,
     quantize_activation_tile_absmax_fused,
+    quantize_activation_tile_absmax_two_level,
     quantize_activation_tile_with_scales_64_fused,
+    two_level_ok,
 )
 
 INT8_MAX = 127.0
@@ -55,6 +57,8 @@ def quantize_activation_tile_absmax(x_fp: torch.Tensor, tile_n: int = 64) -> Tup
     _check_tile(x_fp, tile_n)
     if int(x_fp.shape[0]) <= FUSED_MAX_ROWS:
         return quantize_activation_tile_absmax_fused(x_fp)
+    if x_fp.is_cuda and two_level_ok(x_fp):
+        return quantize_activation_tile_absmax_two_level(x_fp)   # the same two steps in two launches
     sx = activation_tile_absmax_scales(x_fp, tile_n=tile_n)
     return quantize_activation_tile_with_scales(x_fp, sx=sx, tile_n=tile_n), sx
 

@@ -84,3 +84,31 @@ def quantize_activation_tile_with_scales_64_fused(x_fp: torch.Tensor, sx: torch.
         nat.ptr(sx), nat.ptr(x_q), x_q.stride(0), nat.stream_handle(x_fp.device))
     nat.check(rc, "tq_act_quant_with_scales")
     return x_q
+
+
+def quantize_activation_tile_absmax_two_level(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Scales over all rows, then codes, for inputs of more than 512 rows in
+    two launches (``tq_act_quant_two_level``): bitwise the result of
+    ``activation_tile_absmax_scales_64_fused`` followed by
+    ``quantize_activation_tile_with_scales_64_fused`` (the reference's
+    two-kernel path, quant_utils.py:119-134).  Needs unit column stride,
+    16-byte aligned rows and a width that is a multiple of 64
+    (``two_level_ok``)."""
+    _check_x(x_fp)
+    n, k = x_fp.shape
+    n_tc = int(k) // 64
+    x_q = torch.empty((n, k), device=x_fp.device, dtype=torch.int8)
+    sx = torch.empty((n_tc,), device=x_fp.device, dtype=torch.float32)
+    ws = _absmax_workspace(x_fp, int(n), int(k))
+    rc = nat.lib().tq_act_quant_two_level(
+        nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype), int(n), int(k), nat.ptr(x_q), x_q.stride(0),
+        nat.ptr(sx), nat.ptr(ws), ws.numel(), nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_act_quant_two_level")
+    return x_q, sx
+
+
+def two_level_ok(x_fp: torch.Tensor) -> bool:
+    """Whether ``quantize_activation_tile_absmax_two_level`` takes this input."""
+    n, k = x_fp.shape
+    return (int(n) > 512 and int(k) > 0 and int(k) % 64 == 0 and x_fp.stride(1) == 1 and x_fp.stride(0) % 8 == 0
+            and x_fp.data_ptr() % 16 == 0)
