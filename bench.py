@@ -61,6 +61,10 @@ def parse():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the decode GEMM launches (3 eager steps) and a 256 MiB copy: the workload of "
                          "the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic")
+    ap.add_argument("--attention-traffic-probe", action="store_true",
+                    help="run only three eager decode-attention calls (RoPE form with the INT8 merge; B=4, 24/8 "
+                         "heads, 2304 keys) and a 256 MiB copy: the workload of the FETCH_SIZE pass behind "
+                         "profiles/decode_attention_traffic.md")
     ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="read the two --pmc passes' counter_collection.csv and write " + TRAFFIC_FILE)
     ap.add_argument("--e2e-batch", type=int, default=4)
@@ -588,6 +592,43 @@ def cpu_baseline(args, layers, xs):
             "ms_per_sample": t * 1e3}
 
 
+def attention_traffic_probe(device) -> None:
+    """Three eager calls of the fused decode step's attention (RoPE form, INT8 merge) at the configs[4]
+    decode shape with every key valid, then a 256 MiB elementwise copy for the counter calibration."""
+    import torch
+    from tilequant_amd import _native
+    from tilequant_amd.attention import decode_attention_workspace
+
+    B, hq, hkv, D, L = 4, 24, 8, 128, 2304
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(device)
+    cos = torch.randn((L, D), generator=g).to(torch.bfloat16).to(device)
+    sin = torch.randn((L, D), generator=g).to(torch.bfloat16).to(device)
+    kc = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(device)
+    vc = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(device)
+    out = torch.empty((B, hq * D), dtype=torch.bfloat16, device=device)
+    qo = torch.empty((B, hq * D), dtype=torch.int8, device=device)
+    sx = torch.empty((hq * D // 64,), dtype=torch.float32, device=device)
+    ws = decode_attention_workspace(B, hq, L, device)
+    pos = torch.tensor([L - 1], dtype=torch.int64, device=device)
+    seq = torch.full((B,), L, device=device, dtype=torch.int32)
+    for _ in range(3):
+        rc = _native.lib().tq_decode_attention_rope(
+            qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), kc.data_ptr(),
+            vc.data_ptr(), kc.stride(0), kc.stride(2), kc.stride(1), seq.data_ptr(), out.data_ptr(), out.stride(0),
+            D, qo.data_ptr(), qo.stride(0), sx.data_ptr(), 0, B, hq, hkv, D, L, D ** -0.5, ws.data_ptr(),
+            ws.numel(), torch.cuda.current_stream().cuda_stream)
+        _native.check(rc, "tq_decode_attention_rope")
+    torch.cuda.synchronize()
+    src = torch.ones(TRAFFIC_COPY_BYTES // 4, device=device, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"attention_traffic_probe": "done", "kv_bytes": 2 * B * hkv * L * D * 2,
+                      "copy_bytes": TRAFFIC_COPY_BYTES}), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_summarize:
@@ -613,6 +654,9 @@ def main():
         return
     if args.qwen_only:
         print(json.dumps({"qwen": qwen_measure(args, device)}), flush=True)
+        return
+    if args.attention_traffic_probe:
+        attention_traffic_probe(device)
         return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)
