@@ -30,7 +30,11 @@ enum { TQ_DTYPE_BF16 = 0, TQ_DTYPE_FP16 = 1 };
 
 /* Storage order of the 64x64 elements inside one packed tile.
  * ROW_MAJOR: tile[j][k] at j*64+k (the reference packer's order, pack.py:115-175).
- * MFMA: operand-major order of the gfx950 MFMA B operand. */
+ * MFMA: operand-major order of the gfx950 MFMA B operand: 16-row block jb of the
+ *   tile is one contiguous 1 KiB run in which lane l (kq = l / 16, j = l % 16)
+ *   holds W[16 jb + j][16 kq .. 16 kq + 15] (INT8) -- one 16-byte load per lane.
+ *   16-bit tiles: 512-element runs per (jb, K half h), lane l holding
+ *   W[16 jb + j][32 h + 8 kq .. + 7]. */
 enum { TQ_LAYOUT_ROW_MAJOR = 0, TQ_LAYOUT_MFMA = 1 };
 
 enum {

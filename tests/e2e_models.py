@@ -87,3 +87,17 @@ def write_tile_maps(config, keep_dir: Path, frac: float = 0.1, seed: int = 0, mo
         masks[mask_io.layer_name_to_stem(name)] = mask
     mask_io.save_mask_keep_archive(keep_dir, masks)
     return masks
+
+
+# the Llama-3.2-3B architecture (28 layers, hidden 3072,
+# 24 q / 8 kv heads of 128, MLP 8192, vocab 128256, tied embeddings, RMSNorm,
+# RoPE theta 5e5), random-initialised -- the same dictionary bench.py uses.
+LLAMA32_3B = dict(vocab_size=128256, hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
+                  num_attention_heads=24, num_key_value_heads=8, head_dim=128, rope_theta=5e5, rms_norm_eps=1e-5,
+                  max_position_embeddings=131072, tie_word_embeddings=True)
+
+
+def llama32_3b_config():
+    from transformers import LlamaConfig
+
+    return LlamaConfig(**LLAMA32_3B, attn_implementation="sdpa")

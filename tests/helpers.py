@@ -71,3 +71,25 @@ def assert_gemm_close(y: torch.Tensor, acc64: np.ndarray, sumabs: np.ndarray, n_
         f"(tol there {tol.reshape(-1)[np.argmax(err)]:.3e})"
     )
     return float((err / nm.bf16_ulp(ref)).max())
+
+
+def clustered_weight(m: int, k: int, frac: float, seed: int):
+    """BASELINE configs[3] weights and masks: N(0, 0.02) with 3% of the
+    64-column input blocks x4 and 3% of the 64-row output blocks x3, BF16
+    tiles chosen by the reference's top-k rule on per-tile sum|W|
+    (k = max(1, ceil(frac * tiles)), src/quantization/decisions.py:174-183),
+    so the BF16 tiles cluster in those bands and row tiles get very uneven
+    BF16/INT8 mixes.  Returns (W bf16 [m, k], sorted BF16 tile ids)."""
+    from oracle import masks as om
+
+    g = gen(seed)
+    n_tr, n_tc = -(-m // 64), -(-k // 64)
+    W = torch.randn((m, k), generator=g, dtype=torch.float32) * 0.02
+    cb = torch.randperm(n_tc, generator=g)[: max(1, round(0.03 * n_tc))]
+    rb = torch.randperm(n_tr, generator=g)[: max(1, round(0.03 * n_tr))]
+    W4 = W.view(n_tr, 64, n_tc, 64)
+    W4[:, :, cb, :] *= 4
+    W4[rb] *= 3
+    W = W.to(torch.bfloat16)
+    scores = W.float().abs().view(n_tr, 64, n_tc, 64).sum(dim=(1, 3)).numpy()
+    return W, om.topk_ids(scores, frac)

@@ -219,6 +219,13 @@ def test_decoder_argument_errors():
         dec.prefill(torch.zeros((1, 9), dtype=torch.long))
     with pytest.raises(ValueError):
         dec.decode(5)
+    dec.prefill(torch.zeros((1, 8), dtype=torch.long))
+    assert dec.decode(1).shape == (1, 2)
+    with pytest.raises(ValueError, match="prepared bound"):
+        dec.decode(2)                  # 1 + 2 steps would pass the cache end (3 new tokens)
+    assert dec.decode(1).shape == (1, 3)
+    dec.prefill(torch.zeros((1, 8), dtype=torch.long))
+    assert dec.decode(2).shape == (1, 3)
     with pytest.raises(RuntimeError, match="already has"):
         CudaGraphGreedyDecoder(model, prompt_tokens=8, max_new_tokens=3, device=DEV)
     dec.close()

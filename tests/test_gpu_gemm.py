@@ -524,3 +524,48 @@ def test_prefill_rows_longer_than_one_metadata_chunk():
     y = _gemm(pack, xd, xq, sx)
     acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
     assert_gemm_close(y, acc, sab, pack.n_tc)
+
+
+@pytest.mark.parametrize("n,k", [(300, 64 * 320), (130, 64 * 512)])
+def test_prefill_wide_k_two_row_kernel(n, k):
+    """Inputs of 305..512 column tiles (K 19,520 - 32,768) are past the
+    v5 kernel's metadata capacity and take the two-row 4-stage DMA kernel
+    (gemm_prefill_v3_kernel): vs the oracle, and bitwise equal to the
+    register-staged kernel that unaligned rows select."""
+    m = 192
+    W, pack, ids16 = _case(m, k, 0.05, seed=k + 5)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=k + 6)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    y = _gemm(pack, xd, xq, sx)
+    rows = np.unique(np.r_[0:3, n - 3:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc)
+    xq_odd = torch.zeros((n, k + 8), dtype=torch.int8, device="cuda")[:, :k]
+    xq_odd.copy_(xq)
+    xf_odd = torch.zeros((n, k + 4), dtype=xd.dtype, device="cuda")[:, :k]
+    xf_odd.copy_(xd)
+    assert torch.equal(y, _gemm(pack, xf_odd, xq_odd, sx))
+
+
+@pytest.mark.parametrize("split_k", [2, 8])
+@pytest.mark.parametrize("n", [24, 48, 64])
+def test_split_k_reduction_two_and_four_token_blocks(n, split_k):
+    """The cross-workgroup split-K reduction with 32- and 64-token blocks
+    (17..64 rows), including a plan whose reduction buffer is the whole 64 KiB
+    of its LDS budget (n = 64, split_k = 2 at 64 column tiles): vs the oracle,
+    deterministic over repeated launches."""
+    m, k = 512, 4096
+    W, pack, ids16 = _case(m, k, 0.02, seed=n * 10 + split_k)
+    op = oracle_pack(W, ids16)
+    x = make_x(n, k, seed=n + split_k)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    y = _gemm(pack, xd, xq, sx, split_k=split_k)
+    acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
+    assert_gemm_close(y, acc, sab, pack.n_tc)
+    for _ in range(3):
+        assert torch.equal(_gemm(pack, xd, xq, sx, split_k=split_k), y)

@@ -184,3 +184,94 @@ def test_fuse_projection_groups_structure_on_cpu():
     assert isinstance(parent.q_proj, MixedLinearSlice)
     assert parent.tilequant_qkv.bounds == ((0, 128), (128, 192), (192, 256))
     assert parent.tilequant_qkv.linear.n_tr == 4
+
+
+def test_serve_once_hands_each_consumer_one_copy_and_releases():
+    """The memo behind the sibling-quantization cache and projection groups:
+    a hit needs the same live tensor, the same view/version and a consumer
+    that has not taken the value; a full set of consumers, a miss or the
+    source's death release it."""
+    import gc
+
+    from tilequant_amd.mixed_linear import ServeOnce, _view_key
+
+    memo = ServeOnce(consumers=3)
+    x = torch.zeros(4, 8)
+    key = _view_key(x)
+    assert memo.take(x, key, 0) is None
+    memo.put(x, key, 0, "y")
+    assert memo.take(x, key, 0) is None              # consumer 0 again: a new pass
+    memo.put(x, key, 0, "y2")
+    assert memo.take(x, key, 1) == "y2" and memo.take(x, key, 2) == "y2"
+    assert memo.take(x, key, 1) is None              # all three served: released
+    memo.put(x, key, 0, "y3")
+    x.add_(1)                                        # in-place update bumps the version: stale
+    assert memo.take(x, _view_key(x), 1) is None
+    memo.put(x, _view_key(x), 0, "y4")
+    assert memo.take(x[:2], _view_key(x[:2]), 1) is None   # another tensor (a view) is a miss
+    memo.put(x, _view_key(x), 0, "y5")
+    del x
+    gc.collect()
+    assert memo._value is None                       # the source died: the value went with it
+    unbounded = ServeOnce()
+    a = torch.ones(3)
+    unbounded.put(a, _view_key(a), "q", 1)
+    assert [unbounded.take(a, _view_key(a), c) for c in ("k", "v", "k")] == [1, 1, None]
+
+
+def test_state_dict_without_layout_record_loads_as_row_major():
+    """A state_dict written by the reference has row-major tiles and no
+    _extra_state: loading it into a module packed in the MFMA order must
+    switch the module to row-major (strict and non-strict)."""
+    cfg = SimpleNamespace(dtype_out="bf16")
+    p, _ = _cpu_pack(128, 192, 0.3, 40)
+    ref_sd = {k: v for k, v in MixedLinear(p, None, cfg).state_dict().items() if not k.endswith("_extra_state")}
+    for strict in (True, False):
+        p2, _ = _cpu_pack(128, 192, 0.3, 40)
+        p2.tile_layout = "mfma"
+        m = MixedLinear(p2, None, cfg)
+        assert m.tile_layout == "mfma"
+        res = m.load_state_dict(ref_sd, strict=strict)
+        assert m.tile_layout == "row_major" and not res.missing_keys and not res.unexpected_keys
+    # this build's own state_dicts keep their record
+    p3, _ = _cpu_pack(128, 192, 0.3, 40)
+    p3.tile_layout = "mfma"
+    sd = MixedLinear(p3, None, cfg).state_dict()
+    m = MixedLinear(_cpu_pack(128, 192, 0.3, 40)[0], None, cfg)
+    m.load_state_dict(sd)
+    assert m.tile_layout == "mfma"
+
+
+def test_fused_decode_refuses_architectures_it_does_not_compute():
+    """Qwen3 (per-head q/k RMSNorm), dynamic RoPE and partial rotary are
+    rejected; Llama-3.2 (llama3 RoPE) and Qwen2 are accepted."""
+    from accelerate import init_empty_weights
+    from transformers import AutoModelForCausalLM, LlamaConfig, Qwen2Config, Qwen3Config
+
+    from tilequant_amd.fused_decode import check_fused_architecture
+
+    def attn_of(cfg):
+        with init_empty_weights():
+            return AutoModelForCausalLM.from_config(cfg).model.layers[0].self_attn
+
+    small = dict(hidden_size=256, intermediate_size=512, num_hidden_layers=1, num_attention_heads=2,
+                 num_key_value_heads=1, vocab_size=64, head_dim=128)
+    q3 = Qwen3Config(**small)
+    with pytest.raises(ValueError, match="model_type"):
+        check_fused_architecture(q3, attn_of(q3))
+    q3.model_type = "qwen2"   # even under a permitted name, the per-head norms are refused
+    with pytest.raises(ValueError, match="q_norm"):
+        check_fused_architecture(q3, attn_of(Qwen3Config(**small)))
+    dyn = LlamaConfig(**small, rope_scaling={"rope_type": "dynamic", "factor": 2.0})
+    with pytest.raises(ValueError, match="rope_type"):
+        check_fused_architecture(dyn, attn_of(dyn))
+    llama32 = LlamaConfig(**small, max_position_embeddings=131072,
+                          rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                                        "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
+    check_fused_architecture(llama32, attn_of(llama32))
+    q2 = Qwen2Config(**small)
+    check_fused_architecture(q2, attn_of(q2))
+    part = LlamaConfig(**small)
+    part.partial_rotary_factor = 0.5
+    with pytest.raises(ValueError, match="partial"):
+        check_fused_architecture(part, attn_of(LlamaConfig(**small)))

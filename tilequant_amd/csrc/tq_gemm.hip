@@ -1909,22 +1909,45 @@ static int64_t split_workspace_elems(const SplitPlan& p, int n, int n_tr) {
   return p.S > 1 ? counter_elems((int)units) + units * p.S * n * 64 : 0;
 }
 
+// Dynamic LDS beyond the default per-kernel limit needs that limit raised
+// (gfx950 has 160 KiB per workgroup).  Done once per kernel instantiation; a
+// failure is returned so that the launch is not attempted.
+template <class Kern>
+static hipError_t allow_lds(Kern kern, size_t bytes) {
+  static bool raised = false;
+  if (bytes <= 32 * 1024 || raised) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e == hipSuccess) raised = true;
+  return e;
+}
+
+template <class Kern>
+static hipError_t launch_split_kernel(Kern kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                                      const GemmArgs& a) {
+  const hipError_t e = allow_lds(kern, lds + sizeof(int));   // + the static last-arriver flag
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
 template <class XT, bool FUSED, bool XVEC, int JBW>
-static void launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 grid, dim3 block, size_t lds,
-                           hipStream_t s) {
+static hipError_t launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 grid, dim3 block, size_t lds,
+                                 hipStream_t s) {
   constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 2 : 1;
   if constexpr (FUSED) {
     const int n = a.n;
-    if (n <= 1) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>), grid, block, lds, s, a);
-    else if (n <= 2) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>), grid, block, lds, s, a);
-    else if (n <= 4) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>), grid, block, lds, s, a);
-    else if (n <= 8) hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>), grid, block, lds, s, a);
-    else hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>), grid, block, lds, s, a);
+    if (n <= 1) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>, grid, block, lds, s, a);
+    if (n <= 2) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>, grid, block, lds, s, a);
+    if (n <= 4) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>, grid, block, lds, s, a);
+    if (n <= 8) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>, grid, block, lds, s, a);
+    return launch_split_kernel(gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>, grid, block, lds,
+                               s, a);
   } else {
     switch (p.tb) {
-      case 1: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
-      case 2: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
-      default: hipLaunchKernelGGL((gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>), grid, block, lds, s, a); break;
+      case 1: return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>, grid, block, lds, s, a);
+      case 2: return launch_split_kernel(gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>, grid, block, lds, s, a);
+      default: return launch_split_kernel(gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>, grid, block, lds, s, a);
     }
   }
 }
@@ -1943,14 +1966,11 @@ static hipError_t launch_split(GemmArgs a, const SplitPlan& p, float* ws, hipStr
   dim3 grid(units * p.S), block(p.W * kWave);
   size_t lds = (size_t)p.W * p.jbw * p.tb * 4 * 64 * sizeof(float);
   if (FUSED && fused_lds_bytes(a.n, a.n_tc) > lds) lds = fused_lds_bytes(a.n, a.n_tc);
-  if (p.jbw == 4) {
-    if (a.xvec) launch_split_v<XT, FUSED, true, 4>(a, p, grid, block, lds, s);
-    else launch_split_v<XT, FUSED, false, 4>(a, p, grid, block, lds, s);
-  } else {
-    if (a.xvec) launch_split_v<XT, FUSED, true, 1>(a, p, grid, block, lds, s);
-    else launch_split_v<XT, FUSED, false, 1>(a, p, grid, block, lds, s);
-  }
-  return hipGetLastError();
+  if (p.jbw == 4)
+    return a.xvec ? launch_split_v<XT, FUSED, true, 4>(a, p, grid, block, lds, s)
+                  : launch_split_v<XT, FUSED, false, 4>(a, p, grid, block, lds, s);
+  return a.xvec ? launch_split_v<XT, FUSED, true, 1>(a, p, grid, block, lds, s)
+                : launch_split_v<XT, FUSED, false, 1>(a, p, grid, block, lds, s);
 }
 
 // Chooses the split plan and checks the workspace; without a (large enough)
@@ -1997,50 +2017,40 @@ static DecodePlan plan_decode(int n, int k, int n_tr, int n_tc, bool quant) {
   return p;
 }
 
-// Launches one instantiation; dynamic LDS above 64 KiB needs the kernel's
-// limit raised once (gfx950 has 160 KiB per workgroup).
 template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
-static void launch_decode_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+static hipError_t launch_decode_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX>;
-  if (p.lds > 64 * 1024) {
-    static bool raised = false;
-    if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024) != hipSuccess)
-        return;   // the launch below is skipped; hipGetLastError reports the failure
-      raised = true;
-    }
-  }
+  const hipError_t e = allow_lds(kern, p.lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(a.n_tr * (4 / JBW)), dim3(p.W * kWave), p.lds, s, a);
+  return hipGetLastError();
 }
 
 template <class XT, int TB, int JBW, int UMAX, bool QUANT>
-static void launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+static hipError_t launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   switch (p.cmax) {
-    case 1: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 1>(a, p, s); break;
-    case 2: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 2>(a, p, s); break;
-    case 4: launch_decode_one<XT, TB, JBW, UMAX, QUANT, 4>(a, p, s); break;
+    case 1: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 1>(a, p, s);
+    case 2: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 2>(a, p, s);
+    case 4: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 4>(a, p, s);
     default:
-      if constexpr (!QUANT) launch_decode_one<XT, TB, JBW, UMAX, QUANT, 8>(a, p, s);   // QUANT plans stop at 4
-      break;
+      if constexpr (!QUANT) return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 8>(a, p, s);
+      return hipErrorInvalidValue;   // QUANT plans stop at 4 chunks
   }
 }
 
 template <class XT, bool QUANT>
 static hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   if (p.jbw == 4) {
-    if constexpr (QUANT) launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, true>(a, p, s);
-    else if (p.tb == 1) launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
-    else launch_decode_c<XT, 2, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
-  } else {
-    // p.umax is TQ_DEC_UMAX_JB1 except for many-unit grids with one token block
-    if (p.tb == 1 && p.umax == 12) launch_decode_c<XT, 1, 1, 12, QUANT>(a, p, s);
-    else if (p.tb == 1 && p.umax == 16) launch_decode_c<XT, 1, 1, 16, QUANT>(a, p, s);
-    else if constexpr (QUANT) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
-    else if (p.tb == 1) launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
-    else launch_decode_c<XT, 2, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
+    if constexpr (QUANT) return launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, true>(a, p, s);
+    else if (p.tb == 1) return launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
+    else return launch_decode_c<XT, 2, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
   }
-  return hipGetLastError();
+  // p.umax is TQ_DEC_UMAX_JB1 except for many-unit grids with one token block
+  if (p.tb == 1 && p.umax == 12) return launch_decode_c<XT, 1, 1, 12, QUANT>(a, p, s);
+  if (p.tb == 1 && p.umax == 16) return launch_decode_c<XT, 1, 1, 16, QUANT>(a, p, s);
+  if constexpr (QUANT) return launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
+  else if (p.tb == 1) return launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
+  else return launch_decode_c<XT, 2, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
 }
 
 }  // namespace tq

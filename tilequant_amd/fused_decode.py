@@ -72,11 +72,40 @@ class _Layer:
             raise ValueError(f"fused decode supports SiLU MLPs, got {act}")
 
 
+# Architectures whose decoder layer is exactly what the fused step computes:
+# pre-norm RMSNorm, full-width RoPE on q and k (no per-head q/k norm), grouped-
+# query attention, SiLU-gated MLP.  Anything else replays the model's own
+# forward (the decoder catches the ValueError).
+FUSED_MODEL_TYPES = ("llama", "qwen2")
+# RoPE variants whose factors depend on the position only, so one table of
+# every cache position serves all steps ("dynamic" / "longrope" rescale with
+# the sequence length).
+FUSED_ROPE_TYPES = ("default", "llama3", "linear")
+
+
+def check_fused_architecture(cfg, attention_module: nn.Module) -> None:
+    """Raise ValueError unless the fused step computes this model exactly."""
+    model_type = str(getattr(cfg, "model_type", ""))
+    if model_type not in FUSED_MODEL_TYPES:
+        raise ValueError(f"fused decode serves {FUSED_MODEL_TYPES}, got model_type={model_type!r}")
+    for name in ("q_norm", "k_norm"):
+        if getattr(attention_module, name, None) is not None:
+            raise ValueError(f"fused decode has no per-head {name}")
+    rope = getattr(cfg, "rope_scaling", None) or getattr(cfg, "rope_parameters", None) or {}
+    rope_type = str(rope.get("rope_type", rope.get("type", "default"))) if isinstance(rope, dict) else "default"
+    if rope_type not in FUSED_ROPE_TYPES:
+        raise ValueError(f"fused decode needs position-only RoPE factors, got rope_type={rope_type!r}")
+    partial = getattr(cfg, "partial_rotary_factor", 1.0)
+    if partial is not None and float(partial) != 1.0:
+        raise ValueError("fused decode rotates the whole head (partial_rotary_factor must be 1)")
+
+
 class FusedDecodeStep:
     """Decode forward for a bound model and static cache (batch fixed)."""
 
     def __init__(self, model: nn.Module, cache, batch: int, max_cache_len: int, device: torch.device) -> None:
         cfg = model.config.get_text_config(decoder=True)
+        check_fused_architecture(cfg, model.model.layers[0].self_attn)
         self.model = model
         self.text = model.model
         self.cache = cache

@@ -32,7 +32,9 @@ class _SplitKWorkspace:
     stream run in order and leave the counters at zero, so the buffer is
     reused without re-initialisation, also across HIP graph replays.  It only
     grows, and a replaced buffer is kept alive: a captured graph may still
-    hold its address."""
+    hold its address.  Growing it while the stream is being captured is an
+    error: the zero fill would only be recorded, so eager launches before the
+    first replay would find uninitialised arrival counters."""
 
     def __init__(self) -> None:
         self.buffers: Dict[Tuple[int, int], torch.Tensor] = {}
@@ -45,6 +47,10 @@ class _SplitKWorkspace:
         key = (index, nat.stream_handle(device))
         buf = self.buffers.get(key)
         if buf is None or buf.numel() < elems:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "the split-K workspace must grow during HIP graph capture; run the same call once "
+                    "eagerly before capturing")
             if buf is not None:
                 self.retired.append(buf)
             buf = torch.zeros((max(elems, 1 << 16),), device=device, dtype=torch.float32)

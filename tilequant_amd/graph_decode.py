@@ -195,6 +195,9 @@ class CudaGraphGreedyDecoder:
         self.last_logits: Optional[torch.Tensor] = None
         self.prefill_captured = False
         self._prepared = False
+        # decode steps replayed since the last prefill (the warm-up counts as
+        # a prefill and one step); bounds decode() to the prepared cache
+        self._steps_done = 0
 
     # ---- model binding ------------------------------------------------------
     def _install_attention_backend(self) -> None:
@@ -264,6 +267,7 @@ class CudaGraphGreedyDecoder:
                 self._graph = g
             torch.cuda.synchronize(self.device)
         self._prepared = True
+        self._steps_done = 1 if decodes else 0
 
     @torch.inference_mode()
     def _prefill_body(self) -> None:
@@ -335,6 +339,7 @@ class CudaGraphGreedyDecoder:
         if self._prefill_logits is None:
             raise RuntimeError("prefill graph did not retain logits")
         self.last_logits = self._prefill_logits
+        self._steps_done = 0
         return self._prefill_logits if self._prefill_only else self._token
 
     @torch.inference_mode()
@@ -351,13 +356,18 @@ class CudaGraphGreedyDecoder:
             raise ValueError(f"steps must be in [0, {self.max_new_tokens - 1}]")
         if steps and self._graph is None:
             raise RuntimeError("call CudaGraphGreedyDecoder.prepare() before decoding")
+        if self._steps_done + steps > self.max_new_tokens - 1:
+            # the kernels would clamp at the cache end and return stale ids
+            raise ValueError(f"{self._steps_done} decode steps since the last prefill; {steps} more would pass "
+                             f"the prepared bound of {self.max_new_tokens - 1} (call prefill() first)")
         for _ in range(steps):
             self._graph.replay()
+        self._steps_done += steps
         if steps:
             if self._decode_logits is None:
                 raise RuntimeError("decode graph did not retain logits")
             self.last_logits = self._decode_logits
-        return self._generated[:, : steps + 1]
+        return self._generated[:, : self._steps_done + 1]
 
     @torch.inference_mode()
     def generate(self, prompt_ids, *, new_tokens: Optional[int] = None) -> torch.Tensor:

@@ -33,7 +33,6 @@ The extra state records the packed tiles' storage order (``tile_layout``) so a
 from __future__ import annotations
 
 import weakref
-from dataclasses import dataclass
 from typing import Any, Dict, Optional, Tuple
 
 import torch
@@ -71,22 +70,8 @@ def _device_cus(device: torch.device) -> int:
 
 _CU_COUNT: Dict[int, int] = {}
 # Sibling projections reuse one activation quantization for inputs of at least
-# this many rows (mixed_linear.py:20-21).
+# this many rows (the reference's threshold, mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
-
-
-@dataclass
-class _ActivationQuantCacheEntry:
-    source_ref: "weakref.ReferenceType[torch.Tensor]"
-    signature: Tuple[Any, ...]
-    consumers: set
-    x_int8: torch.Tensor
-    sx: torch.Tensor
-
-
-# One inference-only entry per (device, stream): Q/K/V or Gate/Up siblings
-# that see the same activation tensor reuse its codes and scales.
-_ACTIVATION_QUANT_CACHE: Dict[Tuple[int, int], _ActivationQuantCacheEntry] = {}
 
 
 def _cfg_get(cfg: Any, key: str, default=None):
@@ -95,43 +80,93 @@ def _cfg_get(cfg: Any, key: str, default=None):
     return getattr(cfg, key, default)
 
 
-def _activation_version(x: torch.Tensor) -> Optional[int]:
+def _view_key(t: torch.Tensor) -> Tuple[Any, ...]:
+    """What makes two uses of a tensor see the same values: its storage view
+    and its version counter (inference tensors have none; they cannot be
+    modified in place outside inference mode either)."""
     try:
-        return int(x._version)
-    except RuntimeError:  # inference tensors have no version counter
-        return None
+        version = int(t._version)
+    except RuntimeError:
+        version = None
+    return (t.data_ptr(), t.storage_offset(), tuple(t.shape), tuple(t.stride()), t.dtype, t.device, version)
 
 
-def _quantize_shared_activation(source: torch.Tensor, x_work: torch.Tensor, tile_n: int,
-                                consumer_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Quantize ``x_work``, reusing a sibling's result for the same activation
-    (mixed_linear.py:54-111)."""
-    if int(x_work.shape[0]) < ACTIVATION_QUANT_CACHE_MIN_ROWS or not (
-        torch.is_inference_mode_enabled() and x_work.is_cuda
-    ):
-        return quantize_activation_tile_absmax(x_work, tile_n=tile_n)
-    slot = (int(x_work.device.index or 0), int(torch.cuda.current_stream(x_work.device).cuda_stream))
-    signature = (int(x_work.data_ptr()), int(x_work.storage_offset()), tuple(x_work.shape),
-                 tuple(x_work.stride()), x_work.dtype, int(tile_n), _activation_version(source))
-    cached = _ACTIVATION_QUANT_CACHE.get(slot)
-    if (cached is not None and cached.source_ref() is source and cached.signature == signature
-            and consumer_id not in cached.consumers):
-        cached.consumers.add(consumer_id)
-        return cached.x_int8, cached.sx
-    # drop the old entry first so an unrelated activation is not kept alive
-    _ACTIVATION_QUANT_CACHE.pop(slot, None)
-    x_int8, sx = quantize_activation_tile_absmax(x_work, tile_n=tile_n)
-    try:
-        def evict(dead):
-            cur = _ACTIVATION_QUANT_CACHE.get(slot)
-            if cur is not None and cur.source_ref is dead:
-                _ACTIVATION_QUANT_CACHE.pop(slot, None)
+class ServeOnce:
+    """Holds at most one value computed from one source tensor and hands it to
+    each consumer at most once.
 
-        ref = weakref.ref(source, evict)
-    except TypeError:
-        return x_int8, sx
-    _ACTIVATION_QUANT_CACHE[slot] = _ActivationQuantCacheEntry(ref, signature, {consumer_id}, x_int8, sx)
-    return x_int8, sx
+    The source is referenced weakly: when it dies the value is released.  A
+    lookup hits only for the same live tensor with the same view key (so an
+    in-place update in between is a miss) and a consumer that has not taken
+    the value yet; a consumer asking twice means a new forward pass, which
+    must recompute.  With ``consumers`` set, the value is also released once
+    that many distinct consumers have taken it.
+
+    Two uses: the INT8 codes + scales of one activation shared by the sibling
+    projections that read it (the reference's per-stream sibling cache,
+    mixed_linear.py:24-111), and the stacked output of a projection group
+    shared by its members (mixed_linear.py:257-333)."""
+
+    __slots__ = ("consumers", "_source", "_key", "_taken", "_value")
+
+    def __init__(self, consumers: Optional[int] = None) -> None:
+        self.consumers = consumers
+        self.clear()
+
+    def clear(self) -> None:
+        self._source = None
+        self._key = None
+        self._taken: frozenset = frozenset()
+        self._value = None
+
+    def take(self, source: torch.Tensor, key, consumer) -> Optional[Any]:
+        if self._source is None or self._source() is not source or self._key != key or consumer in self._taken:
+            return None
+        value = self._value
+        self._taken = self._taken | {consumer}
+        if self.consumers is not None and len(self._taken) >= self.consumers:
+            self.clear()
+        return value
+
+    def put(self, source: torch.Tensor, key, consumer, value) -> None:
+        self.clear()   # never keep the previous activation's value alive alongside the new one
+        if self.consumers is not None and self.consumers <= 1:
+            return
+
+        def released(ref, memo=self):
+            if memo._source is ref:
+                memo.clear()
+
+        try:
+            self._source = weakref.ref(source, released)
+        except TypeError:
+            return
+        self._key, self._taken, self._value = key, frozenset((consumer,)), value
+
+
+# One memo per (device, stream): kernels on one stream run in order, so codes
+# made there are complete for every later launch on it.
+_SHARED_QUANT: Dict[Tuple[int, int], ServeOnce] = {}
+
+
+def _quantize_for(module: nn.Module, x: torch.Tensor, x_work: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Codes and scales of ``x_work`` (the 2-D view of ``x``) for ``module``,
+    shared with its sibling projections under inference mode for inputs of at
+    least ACTIVATION_QUANT_CACHE_MIN_ROWS rows."""
+    if x_work.shape[0] < ACTIVATION_QUANT_CACHE_MIN_ROWS or not x_work.is_cuda \
+            or not torch.is_inference_mode_enabled():
+        return quantize_activation_tile_absmax(x_work, tile_n=module.tile_n)
+    slot = (x_work.device.index or 0, torch.cuda.current_stream(x_work.device).cuda_stream)
+    memo = _SHARED_QUANT.get(slot)
+    if memo is None:
+        memo = _SHARED_QUANT[slot] = ServeOnce()
+    key = (_view_key(x), module.tile_n)
+    hit = memo.take(x, key, id(module))
+    if hit is not None:
+        return hit
+    codes = quantize_activation_tile_absmax(x_work, tile_n=module.tile_n)
+    memo.put(x, key, id(module), codes)
+    return codes
 
 
 _BUFFERS = ("int8_tiles", "int8_scales", "int8_tile_ids", "int8_row_ptr", "int8_row_indices",
@@ -165,6 +200,18 @@ class MixedLinear(nn.Module):
     def set_extra_state(self, state):
         if isinstance(state, dict) and "tile_layout" in state:
             self.tile_layout = str(state["tile_layout"])
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        # A state_dict without the layout record was written by the reference
+        # (or a module packed in its order): its tiles are row-major.
+        key = prefix + "_extra_state"
+        if key not in state_dict:
+            self.tile_layout = "row_major"
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+        if key not in state_dict and key in missing_keys:
+            missing_keys.remove(key)
 
     def to_pack(self) -> Pack:
         return Pack(M_orig=self.M_orig, K_orig=self.K_orig, M=self.M, K=self.K, tile_m=self.tile_m,
@@ -246,8 +293,7 @@ class MixedLinear(nn.Module):
         if 0 < n_rows <= min(self._fused_rows_for_cfg(), chunk):
             y = self._fused_decode(x_work)
         elif n_rows <= chunk:
-            x_int8, sx = _quantize_shared_activation(source=x, x_work=x_work, tile_n=self.tile_n,
-                                                     consumer_id=id(self))
+            x_int8, sx = _quantize_for(self, x, x_work)
             y = self._gemm_bias(x_fp=x_work, x_int8=x_int8, sx=sx)
         else:
             sx = activation_tile_absmax_scales(x_work, tile_n=self.tile_n)
@@ -259,68 +305,49 @@ class MixedLinear(nn.Module):
         return y
 
 
-@dataclass
-class _PendingGroupOutput:
-    source_ref: "weakref.ReferenceType[torch.Tensor]"
-    signature: Tuple[Any, ...]
-    consumed: set
-    output: torch.Tensor
-
-
 class MixedLinearGroup(nn.Module):
-    """Sibling projections of one activation executed as one stacked GEMM
-    (mixed_linear.py:265-333).  Every output element comes from the same tile
-    sequence and arithmetic as the member's own MixedLinear."""
+    """Sibling projections of one activation run as ONE stacked MixedLinear
+    (mixed_linear.py:265-333): the members' packs concatenated along output
+    rows (``concat_packs_along_rows``), one quantization and one GEMM per
+    activation, each member served its column slice of the stacked output.
+    Every output element comes from the same tile sequence and arithmetic as
+    the member's own MixedLinear, so slices equal the members bitwise."""
 
     def __init__(self, members):
         super().__init__()
         if len(members) < 2:
             raise ValueError("A projection group needs at least two members")
-        has_bias = [m.bias is not None for m in members]
-        if any(has_bias) and not all(has_bias):
+        biased = {m.bias is not None for m in members}
+        if len(biased) > 1:
             raise ValueError("Projection group members must all have or all lack bias")
-        bias = torch.cat([m.bias.detach() for m in members]) if all(has_bias) else None
+        bias = torch.cat([m.bias.detach() for m in members]) if True in biased else None
         self.linear = MixedLinear(concat_packs_along_rows([m.to_pack() for m in members]), bias, members[0].cfg)
-        bounds, start = [], 0
-        for m in members:
-            bounds.append((start, start + m.M_orig))
-            start += m.M_orig
-        self.bounds = tuple(bounds)
-        self._pending: Optional[_PendingGroupOutput] = None
-
-    def _signature(self, x: torch.Tensor) -> Tuple[Any, ...]:
-        return (int(x.data_ptr()), int(x.storage_offset()), tuple(x.shape), tuple(x.stride()), x.dtype,
-                x.device, _activation_version(x))
+        ends = torch.tensor([m.M_orig for m in members]).cumsum(0).tolist()
+        self.bounds = tuple(zip([0] + ends[:-1], ends))
+        self._shared = ServeOnce(consumers=len(members))
 
     def output_for(self, x: torch.Tensor, index: int) -> torch.Tensor:
-        pending = self._pending
-        signature = self._signature(x)
-        if (pending is not None and pending.source_ref() is x and pending.signature == signature
-                and index not in pending.consumed):
-            pending.consumed.add(index)
-            out = pending.output
-            if len(pending.consumed) == len(self.bounds):
-                self._pending = None
-            return out
-        self._pending = None
-        out = self.linear(x)
-        try:
-            ref = weakref.ref(x)
-        except TypeError:
-            return out
-        self._pending = _PendingGroupOutput(ref, signature, {index}, out)
+        """Stacked output for ``x``: computed when member ``index`` is the
+        first to ask for this activation (or asks again), reused otherwise."""
+        key = _view_key(x)
+        out = self._shared.take(x, key, index)
+        if out is None:
+            out = self.linear(x)
+            self._shared.put(x, key, index, out)
         return out
 
     def reset_pending(self) -> None:
-        self._pending = None
+        self._shared.clear()
 
 
 class MixedLinearSlice(nn.Module):
-    """One member projection served from its MixedLinearGroup output."""
+    """Member ``index`` of a MixedLinearGroup: its column slice of the group's
+    stacked output.  The group itself is registered on the parent module (so
+    its buffers are counted once); the slice keeps a plain attribute to it."""
 
     def __init__(self, group: MixedLinearGroup, index: int):
         super().__init__()
-        object.__setattr__(self, "group", group)  # owned (and counted) by the parent
+        self.__dict__["group"] = group   # plain attribute: bypasses submodule registration
         self.index = int(index)
         self.start, self.stop = group.bounds[self.index]
         self.out_features = self.stop - self.start
@@ -330,37 +357,46 @@ class MixedLinearSlice(nn.Module):
         return self.group.output_for(x, self.index)[..., self.start:self.stop]
 
 
+# (attribute the group is registered under, member attribute names), per parent module
 PROJECTION_GROUPS = (
     ("tilequant_qkv", ("q_proj", "k_proj", "v_proj")),
     ("tilequant_gate_up", ("gate_proj", "up_proj")),
 )
 
 
+def _stackable(members) -> bool:
+    """Members can share one stacked pack: same input width and tile shape,
+    whole output row tiles (so member boundaries are tile boundaries), one
+    device, one tile layout, bias on all or none."""
+    if not all(isinstance(m, MixedLinear) for m in members):
+        return False
+    first = members[0]
+    same = lambda f: len({f(m) for m in members}) == 1   # noqa: E731
+    return (same(lambda m: m.K_orig) and same(lambda m: (m.tile_m, m.tile_n)) and same(lambda m: m.tile_layout)
+            and same(lambda m: m.int8_tiles.device) and same(lambda m: m.bias is None)
+            and all(m.M_orig % first.tile_m == 0 for m in members))
+
+
 def fuse_projection_groups(model: nn.Module) -> int:
-    """Replace Q/K/V and Gate/Up MixedLinear siblings by stacked groups
-    (mixed_linear.py:359-386).  Returns the number of groups formed."""
-    fused = 0
-    for parent in list(model.modules()):
-        for group_name, names in PROJECTION_GROUPS:
+    """Stack the Q/K/V and Gate/Up MixedLinear siblings of every module into
+    MixedLinearGroups (mixed_linear.py:359-386); each member attribute becomes
+    a MixedLinearSlice.  Returns the number of groups formed."""
+    plan = []
+    for parent in model.modules():
+        for group_attr, names in PROJECTION_GROUPS:
             members = [getattr(parent, n, None) for n in names]
-            if not all(isinstance(m, MixedLinear) for m in members):
-                continue
-            first = members[0]
-            if any(m.K_orig != first.K_orig or m.M_orig % m.tile_m != 0 or m.tile_m != first.tile_m
-                   or m.tile_n != first.tile_n or m.int8_tiles.device != first.int8_tiles.device
-                   or m.tile_layout != first.tile_layout for m in members):
-                continue
-            if len({m.bias is None for m in members}) != 1:
-                continue
-            group = MixedLinearGroup(members)
-            parent.add_module(group_name, group)
-            for i, n in enumerate(names):
-                setattr(parent, n, MixedLinearSlice(group, i))
-            fused += 1
-    return fused
+            if _stackable(members):
+                plan.append((parent, group_attr, names, members))
+    for parent, group_attr, names, members in plan:
+        group = MixedLinearGroup(members)
+        parent.add_module(group_attr, group)
+        for i, n in enumerate(names):
+            setattr(parent, n, MixedLinearSlice(group, i))
+    return len(plan)
 
 
 def reset_projection_groups(model: nn.Module) -> None:
+    """Forget every group's shared output (e.g. between independent requests)."""
     for module in model.modules():
         if isinstance(module, MixedLinearGroup):
             module.reset_pending()
