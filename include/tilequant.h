@@ -182,6 +182,24 @@ int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, c
                         int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
                         float scale, float* workspace, int64_t workspace_elems, void* stream);
 
+/* No reference counterpart: tq_decode_attention without a workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  The split records live
+ * in a fixed 16 MiB device array of the library, one per GPU, held until the
+ * process ends; shapes needing more
+ * (tq_decode_attention_workspace_elems(batch, q_heads, max_len) > 4 Mi floats,
+ * e.g. batch * q_heads > 504 at long lengths) return TQ_ERR_WORKSPACE.  The
+ * stream must belong to the current device.  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (different streams, threads or
+ * processes) race and must be serialized by the caller.  Nothing in it needs
+ * clearing between calls (each call writes every record it reads).  Results
+ * are bitwise those of tq_decode_attention. */
+int tq_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                                const void* v, int64_t kv_stride_b, int64_t kv_stride_l, int64_t kv_stride_h,
+                                const int32_t* seq_used, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
+                                float scale, void* stream);
+
 /* As tq_decode_attention, and the attention output (the [batch, q_heads *
  * head_dim] input of the next projection) is also quantized like
  * tq_act_quant_fused: q_out int8 with row stride q_out_stride_b, sx_out

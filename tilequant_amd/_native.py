@@ -55,6 +55,8 @@ _SIGNATURES = {
     "tq_decode_attention_plan": (_i, [_i, _i, _i, _i, _i, _i, _p, _p]),
     "tq_decode_attention": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                  _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
+    "tq_decode_attention_noalloc": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+                                         _i, _i, _i, _i, _i, _i, ctypes.c_float, _p]),
     "tq_decode_attention_quant": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                        _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
     "tq_decode_attention_rope": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,

@@ -804,3 +804,58 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
   }
   return (int)hipGetLastError();
 }
+
+// ---- allocation-free variant -------------------------------------------------
+// tq_decode_attention with the split records in a file-scope device array
+// instead of a caller workspace, for callers that cannot allocate.  Every GPU
+// the library runs on holds its own copy of the array from module load until
+// the process ends.  On the host the array's name is only a stand-in: its
+// device address comes from hipGetSymbolAddress, looked up once per device
+// (with that device current) and cached.
+constexpr int64_t kAttnScratchFloats = (int64_t)4 << 20;   // 16 MiB
+static __device__ __align__(256) float scratch[kAttnScratchFloats];
+
+// Address of this device's scratch array; nullptr (and *err set) on failure.
+static float* attn_scratch_for(int dev, hipError_t* err) {
+  static std::atomic<float*> cached[64];
+  if (dev < 0 || dev >= 64) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  float* p = cached[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* addr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || addr == nullptr) {
+    *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+    return nullptr;
+  }
+  p = static_cast<float*>(addr);
+  cached[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+extern "C" int tq_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                                           const void* v, int64_t kv_stride_b, int64_t kv_stride_l,
+                                           int64_t kv_stride_h, const int32_t* seq_used, void* out,
+                                           int64_t out_stride_b, int64_t out_stride_h, int dtype, int batch,
+                                           int q_heads, int kv_heads, int head_dim, int max_len, float scale,
+                                           void* stream) {
+  if (batch > 0 && q_heads > 0 && max_len > 0 &&
+      tq_decode_attention_workspace_elems(batch, q_heads, max_len) > kAttnScratchFloats)
+    return TQ_ERR_WORKSPACE;   // beyond the fixed scratch: use tq_decode_attention with a workspace
+  int dev = 0;
+  TQ_RETURN_IF_HIP_ERROR(hipGetDevice(&dev));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (s != nullptr) {   // the scratch looked up is the current device's: the stream must be on it
+    hipDevice_t sdev = 0;
+    TQ_RETURN_IF_HIP_ERROR(hipStreamGetDevice(s, &sdev));
+    if (sdev != dev) return TQ_ERR_ARG;
+  }
+  hipError_t err = hipSuccess;
+  float* ws = attn_scratch_for(dev, &err);
+  if (ws == nullptr) return (int)err;
+  return tq_decode_attention(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_l, kv_stride_h, seq_used, out,
+                             out_stride_b, out_stride_h, dtype, batch, q_heads, kv_heads, head_dim, max_len, scale,
+                             ws, kAttnScratchFloats, stream);
+}
