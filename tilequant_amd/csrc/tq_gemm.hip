@@ -33,6 +33,8 @@
 // accepted (same 1 KiB run, permuted 16-byte chunks).
 #include "tq_common.h"
 
+#include <atomic>
+
 namespace tq {
 
 struct GemmArgs {
@@ -1910,24 +1912,24 @@ static int64_t split_workspace_elems(const SplitPlan& p, int n, int n_tr) {
 }
 
 // Dynamic LDS beyond the default per-kernel limit needs that limit raised
-// (gfx950 has 160 KiB per workgroup).  Done once per kernel instantiation; a
-// failure is returned so that the launch is not attempted.
-template <class Kern>
-static hipError_t allow_lds(Kern kern, size_t bytes) {
-  static bool raised = false;
-  if (bytes <= 32 * 1024 || raised) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (e == hipSuccess) raised = true;
+// (gfx950: 160 KiB per workgroup, static + dynamic).  Raised per kernel (the
+// kernel is the template argument) to the largest dynamic size requested so
+// far; a failure is returned so that the launch is not attempted.
+template <auto Kern>
+static hipError_t allow_lds(size_t dyn_bytes) {
+  static std::atomic<size_t> raised{0};
+  if (dyn_bytes <= 32 * 1024 || dyn_bytes <= raised.load(std::memory_order_relaxed)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn_bytes);
+  if (e == hipSuccess) raised.store(dyn_bytes, std::memory_order_relaxed);
   return e;
 }
 
-template <class Kern>
-static hipError_t launch_split_kernel(Kern kern, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                                      const GemmArgs& a) {
-  const hipError_t e = allow_lds(kern, lds + sizeof(int));   // + the static last-arriver flag
+template <auto Kern>
+static hipError_t launch_split_kernel(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemmArgs& a) {
+  const hipError_t e = allow_lds<Kern>(lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+  hipLaunchKernelGGL(Kern, grid, block, lds, s, a);
   return hipGetLastError();
 }
 
@@ -1937,17 +1939,17 @@ static hipError_t launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 gri
   constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 2 : 1;
   if constexpr (FUSED) {
     const int n = a.n;
-    if (n <= 1) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>, grid, block, lds, s, a);
-    if (n <= 2) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>, grid, block, lds, s, a);
-    if (n <= 4) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>, grid, block, lds, s, a);
-    if (n <= 8) return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>, grid, block, lds, s, a);
-    return launch_split_kernel(gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>, grid, block, lds,
-                               s, a);
+    if (n <= 1) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>>(grid, block, lds, s, a);
+    if (n <= 2) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>>(grid, block, lds, s, a);
+    if (n <= 4) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>>(grid, block, lds, s, a);
+    if (n <= 8) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>>(grid, block, lds, s, a);
+    return launch_split_kernel<gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>>(grid, block, lds,
+                                                                                                   s, a);
   } else {
     switch (p.tb) {
-      case 1: return launch_split_kernel(gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>, grid, block, lds, s, a);
-      case 2: return launch_split_kernel(gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>, grid, block, lds, s, a);
-      default: return launch_split_kernel(gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>, grid, block, lds, s, a);
+      case 1: return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
+      case 2: return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
+      default: return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
     }
   }
 }
@@ -2019,8 +2021,8 @@ static DecodePlan plan_decode(int n, int k, int n_tr, int n_tc, bool quant) {
 
 template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
 static hipError_t launch_decode_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
-  auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX>;
-  const hipError_t e = allow_lds(kern, p.lds);
+  constexpr auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX>;
+  const hipError_t e = allow_lds<kern>(p.lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(a.n_tr * (4 / JBW)), dim3(p.W * kWave), p.lds, s, a);
   return hipGetLastError();
