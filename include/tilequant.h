@@ -146,6 +146,41 @@ int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
                           int split_k, int tile_layout, float* workspace, int64_t workspace_elems,
                           void* stream);
 
+/* One MixedLinear forward at decode sizes from a prebuilt descriptor: the
+ * activation quantization (tq_act_quant_fused into x_int8 / sx) followed by
+ * tq_gemm_mixed_rows, or, with fused = 1, tq_linear_mixed_fused -- the same
+ * launches, arguments and results as calling those entry points.  Everything
+ * but x, out and stream stays fixed between calls, so a caller builds the
+ * descriptor once (validating shapes, dtypes, alignment and scratch sizes
+ * then) and each call patches three fields and makes one foreign call.
+ * Replaces the launch-overhead removal of the reference's CachedLauncher
+ * (src/kernels/triton/launch.py:9-79, used at gemm_rows_splitk_64x64.py:275-322
+ * and quantize_activation.py:115-155). */
+typedef struct tq_linear_desc {
+  /* per call */
+  const void* x;          /* [n, k] activations, x_dtype, row stride x_stride */
+  void* out;              /* [n, m] out_dtype, row stride out_stride */
+  void* stream;
+  /* fixed */
+  int64_t x_stride, out_stride;
+  int n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout;
+  int fused;              /* 1: one-launch quantize + GEMM (n <= tq_linear_mixed_fused_max_tokens(k)) */
+  int8_t* x_int8;         /* [n, k] scratch codes (unused when fused) */
+  float* sx;              /* [ceil(k/64)] scratch scales (unused when fused) */
+  const int8_t* int8_tiles;
+  const float* int8_scales;
+  const int32_t* int8_tile_ids;
+  const int32_t* int8_row_ptr;
+  const void* fp16_tiles; /* NULL when the pack has no 16-bit tiles */
+  const int32_t* fp16_tile_ids;
+  const int32_t* fp16_row_ptr;
+  const void* bias;       /* out_dtype [m] or NULL */
+  float* workspace;       /* split-K workspace (NULL: automatic plan) */
+  int64_t workspace_elems;
+} tq_linear_desc;
+
+int tq_linear_forward(const tq_linear_desc* d);
+
 /* TEST-ONLY.  Writes the exact INT32 product of every INT8 tile with every
  * token row, products[t][row][j] (int32 [T8, n, 64]), computed by the same
  * device tile routine the GEMM uses.  No reference counterpart: it exposes

@@ -166,3 +166,54 @@ def test_fused_decode_option_is_bitwise_identical():
     assert lin_a._fused_rows_for_cfg() == 4
     wide, _, _, _ = _linear(256, 8192, 0.01, 82, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
     assert wide._fused_rows_for_cfg() == 2   # 8192 columns: quantization repeated per workgroup is too dear
+
+
+@pytest.mark.parametrize("fused_mode", ["auto", False, True])
+@pytest.mark.parametrize("bias,dtype_out", [(False, "bf16"), (True, "fp16")])
+def test_cached_launch_path_equals_uncached_calls(fused_mode, bias, dtype_out):
+    """Eager decode-size forwards run through a cached tq_linear_forward
+    descriptor: bitwise equal to the quantizer + GEMM entry points called
+    directly, on the first call and on cache hits, after the input moves to
+    another buffer, on another stream, and after .to() rebuilds the tensors."""
+    from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk, linear_mixed_fused
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    cfg = SimpleNamespace(quant_style="gi", dtype_out=dtype_out, fused_decode=fused_mode)
+    lin, W, ids16, b = _linear(640, 3072, 0.02, seed=71, cfg=cfg, bias=bias)
+    out_dtype = torch.float16 if dtype_out == "fp16" else torch.bfloat16
+
+    def direct(x):
+        bias_t = lin._out_bias(out_dtype)
+        if 0 < x.shape[0] <= lin._fused_rows_for_cfg():
+            return linear_mixed_fused(x_fp=x, int8_tiles=lin.int8_tiles, int8_scales=lin.int8_scales,
+                                      int8_tile_ids=lin.int8_tile_ids, int8_row_ptr=lin.int8_row_ptr,
+                                      fp16_tiles=lin.fp16_tiles, fp16_tile_ids=lin.fp16_tile_ids,
+                                      fp16_row_ptr=lin.fp16_row_ptr, M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr,
+                                      n_tc=lin.n_tc, out_dtype=out_dtype, bias=bias_t, tile_layout=lin.tile_layout)
+        xq, sx = quantize_activation_tile_absmax(x)
+        return gemm_mixed_rows_splitk(x_fp=x, x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                      int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                      int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                      fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr, M=lin.M_orig,
+                                      K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc, out_dtype=out_dtype, bias=bias_t,
+                                      tile_layout=lin.tile_layout)
+
+    for n in (1, 2, 4, 7, 16, 31):
+        for rep in range(3):
+            x = make_x(n, 3072, seed=100 * n + rep).cuda()
+            y = lin(x)
+            assert y.dtype == out_dtype and torch.equal(y, direct(x)), (n, rep)
+        assert sum(1 for key in lin._launches if key[0] == n) == 1   # one descriptor per row count
+    x = make_x(4, 3072, seed=5).cuda()
+    ref = direct(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        y_side = lin(x)
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(y_side, ref)
+    before = len(lin._launches)
+    assert before > 0
+    lin.to(torch.device("cuda", 0))   # _apply rebuilds nothing here, but the cache is dropped
+    assert len(lin._launches) == 0
+    assert torch.equal(lin(x), ref) and torch.equal(lin(x.view(1, 4, 3072)).view(4, -1), ref)

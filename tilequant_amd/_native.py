@@ -73,6 +73,25 @@ _SIGNATURES = {
     "tq_tiles_relayout": (_i, [_p, _p, _i64, _i, _i, _i, _p]),
 }
 
+
+
+class LinearDesc(ctypes.Structure):
+    """Mirror of tq_linear_desc (include/tilequant.h)."""
+
+    _fields_ = [
+        ("x", _p), ("out", _p), ("stream", _p),
+        ("x_stride", _i64), ("out_stride", _i64),
+        ("n", _i), ("m", _i), ("k", _i), ("n_tr", _i), ("n_tc", _i), ("x_dtype", _i), ("out_dtype", _i),
+        ("tile_layout", _i), ("fused", _i),
+        ("x_int8", _p), ("sx", _p),
+        ("int8_tiles", _p), ("int8_scales", _p), ("int8_tile_ids", _p), ("int8_row_ptr", _p),
+        ("fp16_tiles", _p), ("fp16_tile_ids", _p), ("fp16_row_ptr", _p),
+        ("bias", _p), ("workspace", _p), ("workspace_elems", _i64),
+    ]
+
+
+_SIGNATURES["tq_linear_forward"] = (_i, [ctypes.POINTER(LinearDesc)])
+
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
 

@@ -2193,6 +2193,21 @@ extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, in
   return (int)e;
 }
 
+extern "C" int tq_linear_forward(const tq_linear_desc* d) {
+  if (d == nullptr) return TQ_ERR_ARG;
+  if (d->fused)
+    return tq_linear_mixed_fused(d->x, d->x_stride, d->x_dtype, d->int8_tiles, d->int8_scales, d->int8_tile_ids,
+                                 d->int8_row_ptr, d->fp16_tiles, d->fp16_tile_ids, d->fp16_row_ptr, d->out,
+                                 d->out_stride, d->out_dtype, d->bias, d->n, d->m, d->k, d->n_tr, d->n_tc, 0,
+                                 d->tile_layout, d->workspace, d->workspace_elems, d->stream);
+  const int rc = tq_act_quant_fused(d->x, d->x_stride, 1, d->x_dtype, d->n, d->k, d->x_int8, d->k, d->sx, d->stream);
+  if (rc != 0) return rc;
+  return tq_gemm_mixed_rows(d->x_int8, d->k, d->sx, d->int8_tiles, d->int8_scales, d->int8_tile_ids, d->int8_row_ptr,
+                            d->x, d->x_stride, d->x_dtype, d->fp16_tiles, d->fp16_tile_ids, d->fp16_row_ptr, d->out,
+                            d->out_stride, d->out_dtype, d->bias, d->n, d->m, d->k, d->n_tr, d->n_tc, 0,
+                            d->tile_layout, d->workspace, d->workspace_elems, d->stream);
+}
+
 extern "C" int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
                                          const int8_t* int8_tiles, const int32_t* int8_tile_ids,
                                          const int32_t* int8_row_ptr, int n, int k, int n_tr, int n_tc,

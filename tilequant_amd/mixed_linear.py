@@ -32,12 +32,14 @@ The extra state records the packed tiles' storage order (``tile_layout``) so a
 """
 from __future__ import annotations
 
+import ctypes
 import weakref
 from typing import Any, Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
 
+from . import _native as nat
 from .gemm_rows_splitk_64x64 import fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused
 from .pack import Pack, concat_packs_along_rows
 from .quant_utils import (
@@ -72,6 +74,16 @@ _CU_COUNT: Dict[int, int] = {}
 # Sibling projections reuse one activation quantization for inputs of at least
 # this many rows (the reference's threshold, mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
+
+
+def _linear_forward():
+    fn = _LINEAR_FORWARD[0]
+    if fn is None:
+        fn = _LINEAR_FORWARD[0] = nat.lib().tq_linear_forward
+    return fn
+
+
+_LINEAR_FORWARD = [None]
 
 
 def _cfg_get(cfg: Any, key: str, default=None):
@@ -169,6 +181,23 @@ def _quantize_for(module: nn.Module, x: torch.Tensor, x_work: torch.Tensor) -> T
     return codes
 
 
+# Eager inputs of fewer rows than this (and below the sibling-cache threshold,
+# so sharing semantics are unchanged) run through a cached launch descriptor.
+LAUNCH_CACHE_MAX_ROWS = ACTIVATION_QUANT_CACHE_MIN_ROWS - 1
+
+
+class _Launch:
+    """A validated tq_linear_desc for one (rows, layout, stream, weights) key
+    and the scratch it points to; per call only x, out change."""
+
+    __slots__ = ("desc", "ref", "keep")
+
+    def __init__(self, desc, keep) -> None:
+        self.desc = desc
+        self.ref = ctypes.byref(desc)
+        self.keep = keep   # tensors the descriptor points to
+
+
 _BUFFERS = ("int8_tiles", "int8_scales", "int8_tile_ids", "int8_row_ptr", "int8_row_indices",
             "fp16_tiles", "fp16_tile_ids", "fp16_row_ptr", "fp16_row_indices")
 
@@ -192,6 +221,11 @@ class MixedLinear(nn.Module):
             self.bias = nn.Parameter(bias.detach().clone(), requires_grad=False)
         else:
             self.register_parameter("bias", None)
+        self._launches: Dict[Tuple[Any, ...], _Launch] = {}
+
+    def _apply(self, fn, recurse=True):
+        self._launches = {}   # descriptors point at the old tensors
+        return super()._apply(fn, recurse)
 
     # the tile storage order travels with the state_dict
     def get_extra_state(self):
@@ -208,6 +242,7 @@ class MixedLinear(nn.Module):
         key = prefix + "_extra_state"
         if key not in state_dict:
             self.tile_layout = "row_major"
+        self._launches = {}
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
         if key not in state_dict and key in missing_keys:
@@ -273,6 +308,65 @@ class MixedLinear(nn.Module):
             tile_layout=self.tile_layout,
         )
 
+    def _build_launch(self, x_work: torch.Tensor, stream: int, out_dtype: torch.dtype, fused: bool) -> _Launch:
+        """Validate once and fill the descriptor (the checks of the two-launch
+        path: dtypes, contiguity, 16-byte aligned tiles)."""
+        n, k = x_work.shape
+        dev = x_work.device
+        if x_work.dtype not in nat.TQ_DTYPE or x_work.stride(1) != 1:
+            raise ValueError("x must be a bf16 / fp16 tensor with unit column stride")
+        for name in ("int8_tiles", "fp16_tiles"):
+            t = getattr(self, name)
+            if t.numel() and (not t.is_contiguous() or t.data_ptr() % 16):
+                raise ValueError(f"{name} must be contiguous and 16-byte aligned")
+        has16 = self.fp16_tiles.numel() != 0
+        if has16 and self.fp16_tiles.dtype != x_work.dtype:
+            raise ValueError(f"fp16_tiles must have dtype {x_work.dtype}, got {self.fp16_tiles.dtype}")
+        bias = self._out_bias(out_dtype)
+        keep = [bias]
+        d = nat.LinearDesc()
+        d.stream = stream
+        d.x_stride, d.out_stride = x_work.stride(0), self.M_orig
+        d.n, d.m, d.k, d.n_tr, d.n_tc = n, self.M_orig, self.K_orig, self.n_tr, self.n_tc
+        d.x_dtype, d.out_dtype = nat.dtype_code(x_work.dtype), nat.dtype_code(out_dtype)
+        d.tile_layout, d.fused = nat.TQ_LAYOUT[self.tile_layout], int(fused)
+        if not fused:
+            x_int8 = torch.empty((n, k), device=dev, dtype=torch.int8)
+            sx = torch.empty((self.n_tc,), device=dev, dtype=torch.float32)
+            keep += [x_int8, sx]
+            d.x_int8, d.sx = x_int8.data_ptr(), sx.data_ptr()
+        d.int8_tiles, d.int8_scales = self.int8_tiles.data_ptr(), self.int8_scales.data_ptr()
+        d.int8_tile_ids, d.int8_row_ptr = self.int8_tile_ids.data_ptr(), self.int8_row_ptr.data_ptr()
+        if has16:
+            d.fp16_tiles, d.fp16_tile_ids = self.fp16_tiles.data_ptr(), self.fp16_tile_ids.data_ptr()
+            d.fp16_row_ptr = self.fp16_row_ptr.data_ptr()
+        d.bias = None if bias is None else bias.data_ptr()
+        return _Launch(d, keep)
+
+    def _cached_forward(self, x_work: torch.Tensor) -> torch.Tensor:
+        """Decode-size eager forward through a cached launch descriptor: one
+        foreign call per forward, no per-call validation or argument
+        marshalling (the role of the reference's CachedLauncher)."""
+        n = x_work.shape[0]
+        dev = x_work.device
+        stream = torch._C._cuda_getCurrentRawStream(dev.index)
+        out_dtype = self._out_dtype()
+        bias = self.bias
+        fused = 0 < n <= min(self._fused_rows_for_cfg(), self._activation_row_chunk_size())
+        key = (n, x_work.stride(0), x_work.dtype, dev.index, stream, self.int8_tiles.data_ptr(),
+               0 if bias is None else bias.data_ptr(), out_dtype, self.tile_layout, fused)
+        launch = self._launches.get(key)
+        if launch is None:
+            launch = self._launches[key] = self._build_launch(x_work, stream, out_dtype, fused)
+        out = torch.empty((n, self.M_orig), device=dev, dtype=out_dtype)
+        desc = launch.desc
+        desc.x = x_work.data_ptr()
+        desc.out = out.data_ptr()
+        rc = _linear_forward()(launch.ref)
+        if rc:
+            nat.check(rc, "tq_linear_forward")
+        return out
+
     def _forward_chunk(self, x_chunk: torch.Tensor, sx: torch.Tensor, out: torch.Tensor) -> None:
         x_int8 = quantize_activation_tile_with_scales(x_chunk, sx=sx, tile_n=self.tile_n)
         self._gemm_bias(x_fp=x_chunk, x_int8=x_int8, sx=sx, out=out)
@@ -289,6 +383,10 @@ class MixedLinear(nn.Module):
         if k_in != self.K_orig:
             raise ValueError(f"Input K mismatch: got {k_in}, expected {self.K_orig}")
         x_work = x2d.contiguous()
+        if (0 < n_rows <= LAUNCH_CACHE_MAX_ROWS and x_work.is_cuda and self.int8_tiles.is_cuda
+                and not torch.cuda.is_current_stream_capturing()):
+            y = self._cached_forward(x_work)
+            return y.reshape(in_shape[0], in_shape[1], self.M_orig) if x.dim() == 3 else y
         chunk = self._activation_row_chunk_size()
         if 0 < n_rows <= min(self._fused_rows_for_cfg(), chunk):
             y = self._fused_decode(x_work)
