@@ -37,6 +37,12 @@ HBM_PEAK_GBPS = 8000.0
 # projection groups of one decoder layer: (name, member output widths, K)
 GROUPS = (("qkv", (HIDDEN, KV, KV), HIDDEN), ("o", (HIDDEN,), HIDDEN),
           ("gate_up", (MLP, MLP), HIDDEN), ("down", (HIDDEN,), MLP))
+# the decoder-layer modules of each group's members (Decision/ stems: model.layers.<i>.<member>)
+MEMBERS = (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"), ("self_attn.o_proj",),
+           ("mlp.gate_proj", "mlp.up_proj"), ("mlp.down_proj",))
+# released Llama-3.2-3B gi tile maps (Decision/meta-llama_Llama-3.2-3B-Instruct/gi/tile_masks/keepXX,
+# committed as test fixtures)
+RELEASED_MAPS = ROOT / "tests" / "golden"
 
 
 def parse():
@@ -67,6 +73,9 @@ def parse():
                          "profiles/decode_attention_traffic.md")
     ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="read the two --pmc passes' counter_collection.csv and write " + TRAFFIC_FILE)
+    ap.add_argument("--released-maps", type=int, default=1,
+                    help="also measure decode and prefill with the released Llama-3.2-3B gi tile maps; 0 = skip")
+    ap.add_argument("--released-only", action="store_true", help="run only the released-maps section")
     ap.add_argument("--e2e-batch", type=int, default=4)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-output", type=int, default=256)
@@ -147,10 +156,13 @@ def keep_ids(n_tr, n_tc, frac, rng):
     return np.sort(rng.choice(n, size=k, replace=False)).astype(np.int64)
 
 
-def build_layers(args, device):
-    """Pack every projection of every layer with the HIP packer (weights made on the GPU)."""
+def build_layers(args, device, keep_dir=None, first_layer=0):
+    """Pack every projection of every layer with the HIP packer (weights made on
+    the GPU).  Tile maps: seeded uniform at args.keep, or the Decision/ archive
+    in keep_dir (module names model.layers.<i>.<member>)."""
     import numpy as np
     import torch
+    from tilequant_amd.mask_io import load_fp16_keep_ids_for_layer
     from tilequant_amd.mixed_linear import MixedLinear
     from tilequant_amd.pack import concat_packs_along_rows, pack_weight_from_tile_ids
 
@@ -159,14 +171,19 @@ def build_layers(args, device):
     gen = torch.Generator(device=device)
     gen.manual_seed(args.seed)
     layers, packed_bytes, ops, t16_total, t8_total, max_row16 = [], 0, 0, 0, 0, 0
-    for _ in range(args.layers):
+    for li in range(first_layer, first_layer + args.layers):
         mods = {}
-        for name, widths, k in GROUPS:
+        for (name, widths, k), members in zip(GROUPS, MEMBERS):
             packs = []
-            for m in widths:
+            for m, member in zip(widths, members):
                 W = (torch.randn((m, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
                 n_tr, n_tc = m // 64, k // 64
-                ids16 = keep_ids(n_tr, n_tc, args.keep, rng)
+                if keep_dir is None:
+                    ids16 = keep_ids(n_tr, n_tc, args.keep, rng)
+                else:
+                    ids, grid = load_fp16_keep_ids_for_layer(keep_dir, f"model.layers.{li}.{member}")
+                    assert tuple(grid) == (n_tr, n_tc), (member, grid)
+                    ids16 = ids.numpy().astype(np.int64)
                 mask = np.zeros(n_tr * n_tc, bool)
                 mask[ids16] = True
                 ids8 = np.flatnonzero(~mask)
@@ -187,6 +204,13 @@ def build_layers(args, device):
         layers.append(mods)
     torch.cuda.synchronize()
     return layers, dict(packed_bytes=packed_bytes, ops=ops, t8=t8_total, t16=t16_total, max_bf16_per_row=max_row16)
+
+
+def _one_layer_of(args, device, keep_dir, layer_index):
+    """build_layers for one decoder layer with the archive's maps of layer layer_index."""
+    a2 = argparse.Namespace(**vars(args))
+    a2.layers = 1
+    return build_layers(a2, device, keep_dir=keep_dir, first_layer=layer_index)
 
 
 def make_inputs(args, device):
@@ -361,16 +385,32 @@ def qwen_measure(args, device):
     return out
 
 
-def prefill_measure(args, device):
+def prefill_measure(args, device, keep_dir=None):
     """one Llama-3.2-3B layer's QKV/O/GateUp/Down at
     prefill_tokens rows (MixedLinear: whole-input scales, default row chunk),
-    keep05 uniform masks.  Compute-bound: reported against INT8 MFMA peak."""
+    keep05 uniform masks (or, with keep_dir, the released map of the layer
+    whose row tiles carry the most BF16 tiles).  Compute-bound: reported
+    against INT8 MFMA peak."""
     import numpy as np
     import torch
 
     a2 = argparse.Namespace(**vars(args))
     a2.layers, a2.keep, a2.tokens = 1, args.prefill_keep, args.prefill_tokens
-    layers, info = build_layers(a2, device)
+    if keep_dir is None:
+        layers, info = build_layers(a2, device)
+    else:
+        best = None
+        for li in range(args.layers):   # pick the layer with the most BF16 tiles in one row tile
+            from tilequant_amd.mask_io import load_fp16_keep_ids_for_layer
+
+            worst = 0
+            for members in MEMBERS:
+                for member in members:
+                    ids, (n_tr, n_tc) = load_fp16_keep_ids_for_layer(keep_dir, f"model.layers.{li}.{member}")
+                    worst = max(worst, int(np.bincount(ids.numpy() // n_tc, minlength=n_tr).max()) if ids.numel() else 0)
+            if best is None or worst > best[1]:
+                best = (li, worst)
+        layers, info = _one_layer_of(a2, device, keep_dir, best[0])
     g = torch.Generator(device="cpu")
     g.manual_seed(args.seed + 7)
     xs = {name: torch.randn((args.prefill_tokens, k), generator=g).to(torch.bfloat16).to(device)
@@ -391,7 +431,8 @@ def prefill_measure(args, device):
             times.append(e0.elapsed_time(e1))
         per[name] = statistics.median(times)
     total_ms = sum(per.values())
-    return {"tokens": args.prefill_tokens, "keep": args.prefill_keep, "layer_ms": total_ms,
+    return {"tokens": args.prefill_tokens, "keep": args.prefill_keep if keep_dir is None else f"released {keep_dir.name}",
+            "max_bf16_tiles_per_row_tile": info["max_bf16_per_row"], "layer_ms": total_ms,
             "tops": info["ops"] / (total_ms / 1e3) / 1e12,
             "frac_int8_peak": info["ops"] / (total_ms / 1e3) / 1e12 / INT8_PEAK_TOPS,
             "group_ms": per, "ops_per_layer": info["ops"], "bf16_tiles": info["t16"],
@@ -430,6 +471,28 @@ def _dense_model(config, device, seed, dtype):
     return model.eval()
 
 
+def _energy_reader():
+    """Function returning the GPU's accumulated energy in microjoules (amdsmi,
+    the counterpart of the reference's NVML counter), or None when amdsmi is
+    unavailable on this host."""
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+        handle = amdsmi.amdsmi_get_processor_handles()[0]
+
+        def read():
+            try:
+                e = amdsmi.amdsmi_get_energy_count(handle)
+                return float(e["energy_accumulator"]) * float(e["counter_resolution"])
+            except Exception:
+                return None
+
+        return read if read() is not None else (lambda: None)
+    except Exception:
+        return lambda: None
+
+
 def e2e_measure(args, device):
     """BASELINE configs[4] / the reference's benchmark protocol
     (examples/benchmark_generation.py:74-155): random-init Llama-3.2-3B
@@ -454,21 +517,27 @@ def e2e_measure(args, device):
     g = torch.Generator().manual_seed(args.seed + 99)
     prompt = torch.randint(0, config.vocab_size, (B, P), generator=g)
 
+    energy_uj = _energy_reader()
+
     def graph_request(dec):
         torch.cuda.synchronize()
+        e_start = energy_uj()
         t0 = time.perf_counter()
         dec.prefill(prompt)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         dec.decode(O - 1)
         torch.cuda.synchronize()
-        return t0, t1, time.perf_counter()
+        t2 = time.perf_counter()
+        e_end = energy_uj()
+        return t0, t1, t2, (None if e_start is None or e_end is None else e_end - e_start)
 
     @torch.inference_mode()
     def eager_request(model):
         # the reference's dense loop (benchmark_generation.py:74-88), fused SDPA backends only
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             torch.cuda.synchronize()
+            e_start = energy_uj()
             t0 = time.perf_counter()
             out = model(input_ids=prompt.to(device), use_cache=True, logits_to_keep=1)
             cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
@@ -478,13 +547,19 @@ def e2e_measure(args, device):
                 out = model(input_ids=cur, past_key_values=cache, use_cache=True, logits_to_keep=1)
                 cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
             torch.cuda.synchronize()
-            return t0, t1, time.perf_counter()
+            t2 = time.perf_counter()
+            e_end = energy_uj()
+            return t0, t1, t2, (None if e_start is None or e_end is None else e_end - e_start)
 
     def summarize(rows):
-        ttft = statistics.median((t1 - t0) * 1e3 for t0, t1, _ in rows)
-        tpot = statistics.median((t2 - t1) * 1e3 / max(O - 1, 1) for _, t1, t2 in rows)
-        tps = statistics.median(B * O / (t2 - t0) for t0, _, t2 in rows)
-        return {"ttft_ms": ttft, "tpot_ms": tpot, "output_tok_s": tps, "requests": len(rows)}
+        ttft = statistics.median((t1 - t0) * 1e3 for t0, t1, _, _ in rows)
+        tpot = statistics.median((t2 - t1) * 1e3 / max(O - 1, 1) for _, t1, t2, _ in rows)
+        tps = statistics.median(B * O / (t2 - t0) for t0, _, t2, _ in rows)
+        res = {"ttft_ms": ttft, "tpot_ms": tpot, "output_tok_s": tps, "requests": len(rows)}
+        if all(r[3] is not None for r in rows):
+            # J per 1K tokens = mJ per token (the reference's figure, benchmark_generation.py:148-155)
+            res["energy_j_per_1k_tokens"] = statistics.median(r[3] / 1e3 / (B * O) for r in rows)
+        return res
 
     def run(fn, target):
         for _ in range(args.e2e_warmup):
@@ -504,6 +579,16 @@ def e2e_measure(args, device):
     res["tilequant_graph"]["decode_step"] = "fused (9 launches per layer)" if dec._fused else "model forward"
     dec.close()
     del dec
+    if args.released_maps:
+        # the same model with the released Llama-3.2-3B gi keep01 tile maps
+        rmodel, _ = build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), device,
+                                                keep_dir=RELEASED_MAPS / "llama32_3b_gi_keep01", seed=args.seed)
+        dec = CudaGraphGreedyDecoder.prepare(rmodel, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device)
+        res["tilequant_graph_released_keep01"] = run(graph_request, dec)
+        dec.close()
+        del dec, rmodel
+        gc.collect()
+        torch.cuda.empty_cache()
     if args.e2e_module_path:
         # the reference's structure: the model's own modules replayed in the decode graph
         dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device,
@@ -546,14 +631,34 @@ def e2e_measure(args, device):
     return res
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(args, layers, xs):
-    """Time the CPU oracle (reference arithmetic, OpenMP) on the first cpu_layers layers."""
+    """The reference's CPU path on a bounded sample of the same workload: the
+    activation quantization with the reference's own torch ops
+    (oracle/torch_ref.py = src/kernels/quant_utils.py:61-74, 103-115) and the
+    mixed tile GEMM in the reference's order (oracle/tq_oracle.c, OpenMP: the
+    reference has no CPU tile GEMM, so its GPU kernel's arithmetic is ported).
+    Threads: the process's OMP_NUM_THREADS (16 on the GPU box) for both legs."""
     import numpy as np
     import torch
     from oracle import native as onat
     from oracle import numerics as nm
     from oracle import packing as opk
+    from oracle import torch_ref
 
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch_threads_before = torch.get_num_threads()
+    torch.set_num_threads(threads)
     onat.lib()
     work = []
     ops = 0
@@ -562,34 +667,131 @@ def cpu_baseline(args, layers, xs):
             lin = layers[li][name]
             w8 = opk.from_mfma_int8(lin.int8_tiles.cpu().numpy())
             w16 = nm.bf16_bits_to_f32(opk.from_mfma_16bit(lin.fp16_tiles.cpu().view(torch.int16).numpy().view(np.uint16)))
-            work.append(dict(x=xs[name].float().cpu().numpy(), w8=w8, sw=lin.int8_scales.cpu().numpy(),
+            work.append(dict(x=xs[name].cpu(), w8=w8, sw=lin.int8_scales.cpu().numpy(),
                              ids8=lin.int8_tile_ids.cpu().numpy(), rp8=lin.int8_row_ptr.cpu().numpy(), w16=w16,
                              ids16=lin.fp16_tile_ids.cpu().numpy(), rp16=lin.fp16_row_ptr.cpu().numpy(),
                              n_tr=lin.n_tr, n_tc=lin.n_tc, M=lin.M_orig, K=lin.K_orig))
             ops += 2 * args.tokens * lin.M_orig * lin.K_orig
+    legs = {"quant_s": 0.0, "gemm_s": 0.0}
 
     def run():
         for w in work:
-            sx = onat.act_scales(w["x"])
-            xq = onat.act_quant(w["x"], sx)
-            onat.gemm_mixed(xq, sx, w["x"], w["w8"], w["sw"], w["ids8"], w["rp8"], w["w16"], w["ids16"],
-                            w["rp16"], w["n_tr"], w["n_tc"], w["M"], w["K"])
+            t0 = time.perf_counter()
+            xq, sx = torch_ref.act_quant(w["x"])
+            t1 = time.perf_counter()
+            onat.gemm_mixed(xq.numpy(), sx.numpy(), w["x"].float().numpy(), w["w8"], w["sw"], w["ids8"], w["rp8"],
+                            w["w16"], w["ids16"], w["rp16"], w["n_tr"], w["n_tc"], w["M"], w["K"])
+            legs["quant_s"] += t1 - t0
+            legs["gemm_s"] += time.perf_counter() - t1
 
-    run()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or time.perf_counter() - t_start < args.cpu_seconds:
-        t0 = time.perf_counter()
+    try:
         run()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 30.0:
-            break
+        legs["quant_s"] = legs["gemm_s"] = 0.0
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or time.perf_counter() - t_start < args.cpu_seconds:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > 30.0:
+                break
+    finally:
+        torch_threads = torch.get_num_threads()
+        torch.set_num_threads(torch_threads_before)
     t = statistics.median(times)
-    return {"value": ops / t / 1e12, "unit": "TOPS", "cores": onat.num_threads(), "kind": "port",
+    reps = len(times)
+    return {"value": ops / t / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": f"{min(args.cpu_layers, len(layers))} of {len(layers)} layers of the same linear set at "
-                      f"{args.tokens} tokens (act quant + tile GEMM, reference-order fp32, oracle/tq_oracle.c, "
-                      f"OpenMP), median of {len(times)} reps over {sum(times):.1f} s, {t * 1e3:.1f} ms per sample",
-            "ms_per_sample": t * 1e3}
+                      f"{args.tokens} tokens: activation quantization with the reference's torch CPU ops "
+                      "(quant_utils.py:61-74, 103-115) + tile GEMM in reference order (oracle/tq_oracle.c, "
+                      f"OpenMP); median of {reps} reps over {sum(times):.1f} s, {t * 1e3:.1f} ms per sample",
+            "ms_per_sample": t * 1e3,
+            "quant_ms_per_sample": legs["quant_s"] / reps * 1e3, "gemm_ms_per_sample": legs["gemm_s"] / reps * 1e3,
+            "host": {"cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch_threads,
+                     "omp_threads": onat.num_threads()}}
+
+
+def released_maps_measure(args, device):
+    """The released Llama-3.2-3B gi tile maps (keep01 for decode, keep05 for
+    prefill) instead of seeded uniform ones: the decode linear set at
+    args.tokens tokens (HIP-graph step of quant + GEMM, and GEMM launches alone
+    per group) and one prefill layer at prefill_tokens.  The released maps
+    cluster BF16 tiles (down_proj row tiles up to 59 of 62 in keep05)."""
+    import torch
+    from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    out = {"maps": "tests/golden/llama32_3b_gi_keep01 (decode), llama32_3b_gi_keep05 (prefill): "
+                   "Decision/meta-llama_Llama-3.2-3B-Instruct/gi/tile_masks"}
+    layers, info = build_layers(args, device, keep_dir=RELEASED_MAPS / "llama32_3b_gi_keep01")
+    xs = make_inputs(args, device)
+
+    def step():
+        return [mods[name](xs[name]) for mods in layers for name, _, _ in GROUPS]
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        g.replay()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in GROUPS}
+    group_us = {}
+    for gname, _, _ in GROUPS:
+        items = []
+        for mods in layers:
+            lin = mods[gname]
+            items.append((lin, torch.empty((args.tokens, lin.M_orig), device=device, dtype=torch.bfloat16)))
+
+        def gemms():
+            for lin, o in items:
+                xq, sx = quant[gname]
+                gemm_mixed_rows_splitk(x_fp=xs[gname], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                       int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                       int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                       fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
+                                       M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
+                                       out_dtype=torch.bfloat16, out=o, tile_layout=lin.tile_layout)
+
+        with torch.cuda.stream(s):
+            gemms()
+        torch.cuda.synchronize()
+        gg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gg, stream=s):
+            gemms()
+        with torch.cuda.stream(s):
+            gg.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(args.steps):
+                gg.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        group_us[gname] = e0.elapsed_time(e1) * 1e3 / (args.steps * len(items))
+        del gg
+    out["decode"] = {"tokens": args.tokens, "keep": "released keep01", "ms_per_step": step_s * 1e3,
+                     "tops": info["ops"] / step_s / 1e12, "gbps_packed_weights": info["packed_bytes"] / step_s / 1e9,
+                     "hbm_frac_step": info["packed_bytes"] / step_s / 1e9 / HBM_PEAK_GBPS,
+                     "packed_weight_bytes": info["packed_bytes"], "bf16_tiles": info["t16"],
+                     "max_bf16_tiles_per_row_tile": info["max_bf16_per_row"], "gemm_group_avg_us": group_us}
+    del layers, g
+    torch.cuda.empty_cache()
+    if args.prefill_tokens > 0:
+        out["prefill"] = prefill_measure(args, device, keep_dir=RELEASED_MAPS / "llama32_3b_gi_keep05")
+    return out
 
 
 def attention_traffic_probe(device) -> None:
@@ -651,6 +853,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_measure(args, device)}), flush=True)
+        return
+    if args.released_only:
+        print(json.dumps({"released_maps": released_maps_measure(args, device)}), flush=True)
         return
     if args.qwen_only:
         print(json.dumps({"qwen": qwen_measure(args, device)}), flush=True)
@@ -821,6 +1026,8 @@ def main():
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
     torch.cuda.empty_cache()
+    released = released_maps_measure(args, device) if args.released_maps else None
+    torch.cuda.empty_cache()
     qwen = qwen_measure(args, device) if args.qwen else None
     torch.cuda.empty_cache()
     e2e = e2e_measure(args, device) if args.e2e else None
@@ -858,6 +1065,7 @@ def main():
         "dense_bf16": dense,
         "prefill": prefill,
         "qwen": qwen,
+        "released_maps": released,
         "e2e": e2e,
         "cpu_baseline": cpu,
     }

@@ -15,6 +15,9 @@ Contents:
   MFMA operand-major tile re-layout used by the HIP kernels.
 * ``oracle.masks`` -- the Decision/ tile-map archive format and the top-k
   mask rule.
+* ``oracle.torch_ref`` -- the reference's CPU quantization branch as torch
+  ops (quant_utils.py:61-74, 103-115): checker, and the quantization leg of
+  the CPU baseline.
 * ``oracle.native`` -- ctypes wrapper of ``tq_oracle.c`` (same closed forms in
   C, OpenMP over row tiles) for the larger cases and the CPU baseline.
 

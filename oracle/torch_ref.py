@@ -1,0 +1,51 @@
+"""torch-CPU restatement of the reference's CPU quantization branch.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): the checker in the
+tests and the quantization leg of ``bench.py``'s CPU baseline.
+
+The reference's ``quant_utils`` computes activation scales and codes with
+torch ops when the input is not a CUDA bf16/fp16 tensor
+(src/kernels/quant_utils.py:61-74 for the scales, :103-115 for the codes):
+zero-pad K to whole 64-column tiles, absmax per tile over all rows, scale =
+absmax / 127 in the input dtype (1.0 for an all-zero tile), codes =
+clamp(round(x / scale), -127, 127) with the division in fp32.  These
+functions are those steps, op for op, on CPU tensors.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+INT8_MAX = 127.0
+TILE = 64
+
+
+def _tiles(x: torch.Tensor) -> torch.Tensor:
+    n, k = x.shape
+    n_tc = (k + TILE - 1) // TILE
+    if k % TILE:
+        padded = x.new_zeros((n, n_tc * TILE))
+        padded[:, :k] = x
+        x = padded
+    return x.view(n, n_tc, TILE)
+
+
+def act_tile_scales(x: torch.Tensor) -> torch.Tensor:
+    """quant_utils.py:61-74: one fp32 scale per 64-column tile, over all rows."""
+    max_abs = _tiles(x).abs().amax(dim=(0, 2))
+    return torch.where(max_abs > 0, max_abs / INT8_MAX,
+                       torch.ones_like(max_abs, dtype=torch.float32)).to(torch.float32).contiguous()
+
+
+def act_codes_with_scales(x: torch.Tensor, sx: torch.Tensor) -> torch.Tensor:
+    """quant_utils.py:103-115: int8 codes of x under the given tile scales."""
+    n, k = x.shape
+    t = _tiles(x)
+    q = torch.clamp(torch.round(t / sx.view(1, t.shape[1], 1)), -127, 127).to(torch.int8)
+    return q.view(n, -1)[:, :k].contiguous()
+
+
+def act_quant(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    sx = act_tile_scales(x)
+    return act_codes_with_scales(x, sx), sx

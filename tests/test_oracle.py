@@ -96,14 +96,11 @@ def test_act_quant_numpy_c_torch_agree(n, k, dtype):
     x = make_x(n, k, seed=n * 7 + k, dtype=dtype)
     xv = values(x)
     q, sx = nm.act_quant(xv, dtype == torch.bfloat16)
-    # torch-CPU statement of the reference CPU branch (quant_utils.py:61-74, 103-115)
-    n_tc = (k + 63) // 64
-    xw = torch.zeros((n, n_tc * 64), dtype=dtype)
-    xw[:, :k] = x
-    t = xw.view(n, n_tc, 64)
-    ma = t.abs().amax(dim=(0, 2))
-    sx_t = torch.where(ma > 0, ma / 127.0, torch.ones_like(ma, dtype=torch.float32)).to(torch.float32)
-    q_t = torch.clamp(torch.round(t / sx_t.view(1, n_tc, 1)), -127, 127).to(torch.int8).view(n, -1)[:, :k]
+    # torch-CPU statement of the reference CPU branch (quant_utils.py:61-74, 103-115):
+    # oracle.torch_ref, also the quantization leg of bench.py's CPU baseline
+    from oracle import torch_ref
+
+    q_t, sx_t = torch_ref.act_quant(x)
     assert np.array_equal(sx, sx_t.numpy())
     assert np.array_equal(q, q_t.numpy())
     sx_c = onat.act_scales(xv, dtype == torch.bfloat16)
