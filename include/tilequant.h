@@ -126,6 +126,36 @@ int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const floa
                        int n_tc, int split_k, int tile_layout, float* workspace,
                        int64_t workspace_elems, void* stream);
 
+/* tq_gemm_mixed_rows with a work plan for its prefill kernel (n > 64):
+ * prefill_units[0 .. n_units) from tq_gemm_prefill_plan for the same row
+ * pointers, the first n_first of them dispatched before the others.  The
+ * outputs are bitwise those of tq_gemm_mixed_rows; only the order and grouping
+ * of the workgroups change.  Ignored for n <= 64.  No reference counterpart:
+ * the reference's grid is one program per (row tile, split)
+ * (gemm_rows_splitk_64x64.py:275-322). */
+int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                               const int8_t* int8_tiles, const float* int8_scales,
+                               const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                               const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                               const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                               const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                               int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                               int n_tc, int split_k, int tile_layout, float* workspace,
+                               int64_t workspace_elems, const int32_t* prefill_units, int n_units,
+                               int n_first, void* stream);
+
+/* Host function: the prefill work plan of one packed weight, from HOST copies
+ * of its row pointers and INT8 tile ids (fp16_row_ptr may be NULL).  Writes
+ * units (row tile | 1 << 30 for a single row tile, else a row-tile pair) into
+ * units[0 .. max_units), max_units >= n_tr, and the count of units to
+ * dispatch first into *n_first.  Returns the unit count, 0 when the plain pair
+ * order is balanced (no plan needed), or TQ_ERR_ARG.  Pairs whose 16-bit tiles
+ * make them cost well above the median pair are split into their two row
+ * tiles; units costing more than the median go first, heaviest first. */
+int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* int8_tile_ids,
+                         const int32_t* fp16_row_ptr, int n_tr, int n_tc, int32_t* units, int max_units,
+                         int* n_first);
+
 /* Largest n tq_linear_mixed_fused accepts for input width k: at most 16, and
  * the n x ceil(k/64)*64 int8 codes (+ scales) must fit 64 KiB of LDS. */
 int tq_linear_mixed_fused_max_tokens(int k);

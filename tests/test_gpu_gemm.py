@@ -16,7 +16,7 @@ from helpers import assert_gemm_close, bits, complement, make_w, make_x, oracle_
 from oracle import native as onat
 from oracle import numerics as nm
 from oracle import packing as opk
-from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk, gemm_tile_products_i32
+from tilequant_amd.gemm_rows_splitk_64x64 import PrefillPlan, gemm_mixed_rows_splitk, gemm_tile_products_i32, prefill_plan
 from tilequant_amd.pack import pack_weight_from_tile_ids, relayout_pack
 from tilequant_amd.quant_utils import quantize_activation_tile_absmax
 
@@ -569,3 +569,80 @@ def test_split_k_reduction_two_and_four_token_blocks(n, split_k):
     assert_gemm_close(y, acc, sab, pack.n_tc)
     for _ in range(3):
         assert torch.equal(_gemm(pack, xd, xq, sx, split_k=split_k), y)
+
+
+def _banded_case(m, k, heavy_rows, seed):
+    """A weight whose listed row tiles are entirely 16-bit (dict row -> 'all')
+    or have the given fraction of 16-bit tiles, over a 2% uniform background:
+    the row-tile pairs then differ several-fold in prefill work."""
+    n_tr, n_tc = -(-m // 64), -(-k // 64)
+    rng = np.random.default_rng(seed)
+    mask = rng.random((n_tr, n_tc)) < 0.02
+    for r, frac in heavy_rows.items():
+        mask[r] = True if frac == "all" else rng.random(n_tc) < frac
+    ids16 = np.flatnonzero(mask.ravel()).astype(np.int64)
+    W = make_w(m, k, seed=seed)
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(complement(ids16, n_tr * n_tc)),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=CFG, tile_layout="mfma")
+    return W, pack, ids16
+
+
+def _plan_of(units, n_first=0):
+    return PrefillPlan(torch.tensor(units, dtype=torch.int32, device="cuda"), n_first)
+
+
+@pytest.mark.parametrize("n,m,k,heavy", [
+    (300, 768, 4096, {3: "all", 8: 0.5}),            # one whole 16-bit row tile, one half
+    (513, 704, 2048, {2: "all", 3: "all", 10: 0.8}),  # a pair with no INT8 column at all; odd row-tile count
+    (2048, 1024, 8192, {5: "all"}),
+])
+def test_prefill_plans_change_nothing_but_the_order(n, m, k, heavy):
+    """The prefill kernel's work plans (row-tile pairs and single row tiles,
+    heavy units first) give bitwise the plain launch's outputs, which match the
+    oracle; hand-built plans cover every unit kind and dispatch order."""
+    W, pack, ids16 = _banded_case(m, k, heavy, seed=n + m)
+    x = make_x(n, k, seed=n + 1)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y = _gemm(pack, xd, xq, sx)
+    plan = prefill_plan(int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr,
+                        fp16_row_ptr=pack.fp16_row_ptr, n_tr=pack.n_tr, n_tc=pack.n_tc)
+    assert plan is not None
+    units = plan.units.cpu().tolist()
+    n_tr = pack.n_tr
+    assert any(u >> 30 for u in units) or plan.n_first >= 1   # a split, or units sent first
+    if plan.n_first:
+        r = units[0] & ((1 << 30) - 1)
+        first_rows = {r} if units[0] >> 30 or r + 1 >= n_tr else {r, r + 1}
+        assert first_rows & set(heavy)   # a heavy row's unit goes first
+    plans = [plan,
+             _plan_of([r | 1 << 30 for r in range(n_tr)]),                          # all single rows
+             _plan_of([r | 1 << 30 for r in reversed(range(n_tr))], n_first=3),      # reversed, three first
+             _plan_of(list(range(0, n_tr, 2))[::-1], n_first=1)]                     # pairs, reversed
+    for p in plans:
+        out = torch.full_like(y, float("nan"))
+        gemm_mixed_rows_splitk(
+            x_fp=xd, x_int8=xq, sx=sx, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales,
+            int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles,
+            fp16_tile_ids=pack.fp16_tile_ids, fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig,
+            n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=torch.bfloat16, out=out, tile_layout=pack.tile_layout,
+            prefill_plan=p)
+        assert torch.equal(out.view(torch.int16), y.view(torch.int16))
+    op = oracle_pack(W, ids16)
+    xq_ref, sx_ref = nm.act_quant(values(x))
+    rows = np.unique(np.r_[0:3, n // 2, n - 3:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc)
+
+
+def test_mixed_linear_builds_and_uses_the_prefill_plan():
+    from tilequant_amd.mixed_linear import MixedLinear
+
+    W, pack, _ = _banded_case(640, 3072, {4: "all"}, seed=77)
+    lin = MixedLinear(pack, None, CFG)
+    x = make_x(1000, 3072, seed=78).cuda()
+    y = lin(x)
+    assert lin._plan is not None and lin._plan[0] is not None
+    xq, sx = quantize_activation_tile_absmax(x)
+    assert torch.equal(y, _gemm(pack, x, xq, sx))
+    assert lin(x[:4]).shape == (4, 640)   # decode sizes run without it

@@ -275,3 +275,53 @@ def test_fused_decode_refuses_architectures_it_does_not_compute():
     part.partial_rotary_factor = 0.5
     with pytest.raises(ValueError, match="partial"):
         check_fused_architecture(part, attn_of(LlamaConfig(**small)))
+
+
+def _plan_from_ids16(ids16, n_tr, n_tc):
+    from tilequant_amd.gemm_rows_splitk_64x64 import prefill_plan
+
+    mask = np.zeros(n_tr * n_tc, bool)
+    mask[ids16] = True
+    ids8 = np.flatnonzero(~mask)
+    rp8 = np.r_[0, np.cumsum(np.bincount(ids8 // n_tc, minlength=n_tr))]
+    rp16 = np.r_[0, np.cumsum(np.bincount(np.asarray(ids16, np.int64) // n_tc, minlength=n_tr))]
+    return prefill_plan(int8_tile_ids=torch.tensor(ids8, dtype=torch.int32),
+                        int8_row_ptr=torch.tensor(rp8, dtype=torch.int32),
+                        fp16_row_ptr=torch.tensor(rp16, dtype=torch.int32), n_tr=n_tr, n_tc=n_tc, device="cpu")
+
+
+def _covered_rows(units, n_tr):
+    rows = []
+    for u in units:
+        r = u & ((1 << 30) - 1)
+        rows += [r] if u >> 30 or r + 1 >= n_tr else [r, r + 1]
+    return sorted(rows)
+
+
+def test_prefill_plan_splits_and_front_loads_the_released_heavy_row():
+    """Released keep05 map, layer 7 down_proj: row tile 47 holds 127 of its
+    128 tiles in 16 bits.  The plan (host code in the library) splits its pair
+    into single row tiles and dispatches row 47 among the first units, which
+    are ordered heaviest first; every row tile is covered exactly once; uniform
+    maps need no plan."""
+    ids, (n_tr, n_tc) = mask_io.load_fp16_keep_ids_for_layer(GOLDEN / "llama32_3b_gi_keep05",
+                                                              "model.layers.7.mlp.down_proj")
+    plan = _plan_from_ids16(ids.numpy(), n_tr, n_tc)
+    units = plan.units.tolist()
+    assert 47 | 1 << 30 in units[:plan.n_first] and 46 | 1 << 30 in units
+    assert 1 <= plan.n_first < len(units)
+    counts = np.bincount(ids.numpy() // n_tc, minlength=n_tr)
+    first = [u & ((1 << 30) - 1) for u in units[:plan.n_first]]
+    assert all(counts[r] + (0 if units[i] >> 30 else counts[r + 1]) >= 20 for i, r in enumerate(first))
+    assert _covered_rows(units, n_tr) == list(range(n_tr))
+    assert _plan_from_ids16(uniform_fp16_ids(48, 128, 0.05, seed=3), 48, 128) is None
+
+
+def test_prefill_plan_rejects_inconsistent_bookkeeping():
+    from tilequant_amd.gemm_rows_splitk_64x64 import prefill_plan
+
+    rp8 = torch.tensor([0, 2, 4], dtype=torch.int32)
+    ids8 = torch.tensor([0, 1, 2, 7], dtype=torch.int32)   # id 7 is not in row 1 (columns 2..3 of 2 x 2)
+    with pytest.raises(ValueError, match="tq_gemm_prefill_plan"):
+        prefill_plan(int8_tile_ids=ids8, int8_row_ptr=rp8, fp16_row_ptr=torch.zeros(0, dtype=torch.int32),
+                     n_tr=2, n_tc=2, device="cpu")

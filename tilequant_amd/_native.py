@@ -44,6 +44,15 @@ _SIGNATURES = {
                                 _i, _i, _i, _i, _i,
                                 _i, _i, _p, _i64, _p]),
     "tq_linear_mixed_fused_max_tokens": (_i, [_i]),
+    "tq_gemm_mixed_rows_planned": (_i, [_p, _i64, _p,
+                                        _p, _p, _p, _p,
+                                        _p, _i64, _i,
+                                        _p, _p, _p,
+                                        _p, _i64, _i, _p,
+                                        _i, _i, _i, _i, _i,
+                                        _i, _i, _p, _i64,
+                                        _p, _i, _i, _p]),
+    "tq_gemm_prefill_plan": (_i, [_p, _p, _p, _i, _i, _p, _i, ctypes.POINTER(_i)]),
     "tq_linear_mixed_fused": (_i, [_p, _i64, _i,
                                    _p, _p, _p, _p,
                                    _p, _p, _p,

@@ -33,7 +33,9 @@
 // accepted (same 1 KiB run, permuted 16-byte chunks).
 #include "tq_common.h"
 
+#include <algorithm>
 #include <atomic>
+#include <vector>
 
 namespace tq {
 
@@ -62,7 +64,14 @@ struct GemmArgs {
   int splits;       // split-K decode kernel: splits per row tile
   int32_t* counters;  // [n_tr] arrival counters (zero between launches)
   float* partials;    // [n_tr, splits, n, 64] fp32 split partials
+  // Prefill work plan (nullptr: row pairs in order).  units[u] = first row
+  // tile | kUnitSingle when the unit is that row tile alone; the first
+  // n_first units take all their token blocks before the others start.
+  const int32_t* units;
+  int n_units, n_first;
 };
+
+constexpr int32_t kUnitSingle = 1 << 30;
 
 constexpr int kMaxWaves = 16;
 constexpr int kDecodeMaxTokens = 64;  // token counts served by gemm_splitk_kernel
@@ -1501,8 +1510,14 @@ gemm_prefill_v3_kernel(GemmArgs a) {
 //                          + the tile's 64 x 32 half (4 KiB), 16 bf16/fp16
 //                          MFMAs into the row's accumulators
 // so the accumulation order per output is the reference's: INT8 tiles by
-// column, then 16-bit tiles by position, K halves in order.  The epilogue
-// stages the rounded outputs through LDS and writes 16-byte row chunks.
+// column, then 16-bit tiles by position, K halves in order.  Columns where no
+// row of the unit has an INT8 tile take no step.  The epilogue stages the
+// rounded outputs through LDS and writes 16-byte row chunks.
+// Work units: a 1-D grid over (unit, token block), the unit index fastest (on
+// MI355X 11% faster than the same pairs as a 2-D grid).  Units are row pairs,
+// or, with a plan (a.units), the plan's pairs and single row tiles, the units
+// carrying many 16-bit tiles first so that they do not finish last.  A unit's
+// per-output arithmetic is the same either way.
 constexpr int kP5Threads = 256;
 template <class T> struct TypeTag { using type = T; };
 constexpr int kP5Stages = 3;
@@ -1517,15 +1532,38 @@ gemm_prefill_v5_kernel(GemmArgs a) {
   __shared__ int pos8[2][kP5MaxCols];
   __shared__ float scl[2][kP5MaxCols];
   __shared__ int list16[2 * kP5MaxCols];   // (q << 10) | (row << 9) | column
+  __shared__ int wcount[8];
   constexpr int P = kP5Stages;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int r0 = blockIdx.x * 2;
-  const int n0 = blockIdx.y * kPfTokens;
+  int r0, n0;
+  bool has1;
+  const int ntb = (a.n + kPfTokens - 1) / kPfTokens;
+  if (a.units == nullptr) {   // row pairs, the pair index fastest
+    const int n_pairs = (a.n_tr + 1) / 2;
+    r0 = (blockIdx.x % n_pairs) * 2;
+    n0 = (blockIdx.x / n_pairs) * kPfTokens;
+    has1 = r0 + 1 < a.n_tr;   // odd row-tile count: the last pair has one row
+  } else {
+    int b = blockIdx.x, u, tbk;
+    if (b < a.n_first * ntb) {
+      u = b % a.n_first;
+      tbk = b / a.n_first;
+    } else {
+      b -= a.n_first * ntb;
+      const int rest = a.n_units - a.n_first;
+      u = a.n_first + b % rest;
+      tbk = b / rest;
+    }
+    const int w = a.units[u];
+    r0 = w & (kUnitSingle - 1);
+    n0 = tbk * kPfTokens;
+    has1 = !(w & kUnitSingle) && r0 + 1 < a.n_tr;
+    if (r0 >= a.n_tr) return;   // not a plan for this matrix
+  }
   const int arow = lane & 15, akq = lane >> 4;
   const int n_tc = a.n_tc;
-  const bool has1 = r0 + 1 < a.n_tr;   // odd row-tile count: the last pair has one row
-  const int n8s = a.rp8[a.n_tr] > 0 ? n_tc : 0;   // INT8 steps (none if the matrix has no INT8 tile)
+  int n8s = 0;   // INT8 steps: the columns where a row of the unit has an INT8 tile
   int n16 = 0, n16_0 = 0;
   if (a.w16 != nullptr) {
     const int lo0 = a.rp16[r0], c0 = a.rp16[r0 + 1] - lo0;
@@ -1543,12 +1581,60 @@ gemm_prefill_v5_kernel(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int rr = r0 + j;
-    if (rr >= a.n_tr || n8s == 0) continue;
+    if (j == 1 && !has1) continue;
     const int lo = a.rp8[rr], hi = a.rp8[rr + 1];
     for (int p = lo + t; p < hi; p += kP5Threads) {
       const int c = col_of(a.ids8[p], rr * n_tc, n_tc);
       pos8[j][c] = p;
       scl[j][c] = a.sx[c] * a.sw8[p];
+    }
+  }
+  __syncthreads();
+  // Compact the columns with an INT8 tile, in column order, in place: entry i
+  // becomes (position << 9) | column, or (-512 | column) for a row whose tile
+  // there is 16-bit (position < 2^22, column < 512).  All reads precede the
+  // count barrier; the writes follow it.
+  {
+    static_assert(kP5MaxCols <= 2 * kP5Threads && kP5MaxCols < 512, "two columns per thread");
+    int pv[2][2];
+    float sv[2][2];
+    bool keep[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = t + h * kP5Threads;
+      keep[h] = false;
+      if (c < n_tc) {
+        pv[h][0] = pos8[0][c]; pv[h][1] = pos8[1][c];
+        sv[h][0] = scl[0][c]; sv[h][1] = scl[1][c];
+        keep[h] = pv[h][0] >= 0 || pv[h][1] >= 0;
+      }
+    }
+    const uint64_t b0 = __ballot(keep[0]), b1 = __ballot(keep[1]);
+    if (lane == 0) {
+      wcount[wave] = __popcll(b0);
+      wcount[4 + wave] = __popcll(b1);
+    }
+    __syncthreads();
+    int base0 = 0, base1 = 0, tot0 = 0, tot1 = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      base0 += w < wave ? wcount[w] : 0;
+      base1 += w < wave ? wcount[4 + w] : 0;
+      tot0 += wcount[w];
+      tot1 += wcount[4 + w];
+    }
+    n8s = tot0 + tot1;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (!keep[h]) continue;
+      const int c = t + h * kP5Threads;
+      const int i = h == 0 ? base0 + __popcll(b0 & below) : tot0 + base1 + __popcll(b1 & below);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        pos8[j][i] = pv[h][j] >= 0 ? ((pv[h][j] << 9) | c) : (-512 | c);
+        scl[j][i] = sv[h][j];
+      }
     }
   }
   __syncthreads();
@@ -1595,11 +1681,12 @@ gemm_prefill_v5_kernel(GemmArgs a) {
       int8_t* sp = smem + st * kP3Stage;
       if (sn < n8s) {
         if (part < 2) {
+          const int col = meta & 511;
 #pragma unroll
           for (int i = 2 * part; i < 2 * part + 2; ++i)
-            __builtin_amdgcn_global_load_lds(a.xq + xrow8[i] + sn * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.xq + xrow8[i] + col * 64, sp + (4 * wave + i) * 1024, 16, 0, 0);
         } else {
-          const int pw = meta >= 0 ? meta : 0;   // a 16-bit tile here: any valid INT8 tile, unused
+          const int pw = meta >= 0 ? meta >> 9 : 0;   // a 16-bit tile here: any valid INT8 tile, unused
 #pragma unroll
           for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_global_load_lds(a.w8 + (int64_t)pw * 4096 + w_off[i],
@@ -2075,17 +2162,20 @@ static int check_gemm_common(int n, int m, int k, int n_tr, int n_tc, int x_dtyp
   return TQ_OK;
 }
 
-extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
-                                  const int8_t* int8_tiles, const float* int8_scales,
-                                  const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
-                                  const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
-                                  const void* fp16_tiles, const int32_t* fp16_tile_ids,
-                                  const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
-                                  int out_dtype, const void* bias, int n, int m, int k, int n_tr,
-                                  int n_tc, int split_k, int tile_layout, float* workspace,
-                                  int64_t workspace_elems, void* stream) {
+static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                           const int8_t* int8_tiles, const float* int8_scales,
+                           const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                           const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                           const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                           const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                           int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                           int n_tc, int split_k, int tile_layout, float* workspace,
+                           int64_t workspace_elems, const int32_t* units, int n_units, int n_first,
+                           void* stream) {
   int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
   if (rc) return rc;
+  if (units != nullptr && (n_units < 1 || n_units > n_tr || n_first < 0 || n_first > n_units))
+    return TQ_ERR_ARG;
   if (n == 0 || m == 0) return TQ_OK;
   if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_int8 == nullptr || sx == nullptr)
     return TQ_ERR_ARG;
@@ -2122,9 +2212,16 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                    : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
-    if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 22)) {
+    const int64_t v5_blocks = (int64_t)(units != nullptr ? n_units : (n_tr + 1) / 2) * ((n + kPfTokens - 1) / kPfTokens);
+    if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 22) &&
+        v5_blocks < (1ll << 31)) {
       // DMA ring, 64 x 128 wave tiles, 16-bit tiles in the ring
-      const dim3 g5((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
+      const int ntb = (n + kPfTokens - 1) / kPfTokens;
+      dim3 g5(((n_tr + 1) / 2) * ntb, 1);
+      if (units != nullptr) {
+        a.units = units; a.n_units = n_units; a.n_first = n_first;
+        g5 = dim3(n_units * ntb, 1);
+      }
       if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v5_kernel<Bf16>, g5, dim3(kP5Threads), 0, s, a);
       else hipLaunchKernelGGL(gemm_prefill_v5_kernel<Fp16>, g5, dim3(kP5Threads), 0, s, a);
     } else if (a.xvec && n_tc <= kP3MaxCols) {   // DMA path, two row tiles per workgroup
@@ -2141,6 +2238,120 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
     e = hipGetLastError();
   }
   return (int)e;
+}
+
+extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                                  const int8_t* int8_tiles, const float* int8_scales,
+                                  const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                                  const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                                  const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                                  const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                                  int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                                  int n_tc, int split_k, int tile_layout, float* workspace,
+                                  int64_t workspace_elems, void* stream) {
+  return gemm_mixed_rows(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+                         x_fp, x_fp_stride_n, x_dtype, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out,
+                         out_stride_n, out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
+                         workspace_elems, nullptr, 0, 0, stream);
+}
+
+extern "C" int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                                          const int8_t* int8_tiles, const float* int8_scales,
+                                          const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                                          const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                                          const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                                          const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                                          int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                                          int n_tc, int split_k, int tile_layout, float* workspace,
+                                          int64_t workspace_elems, const int32_t* prefill_units,
+                                          int n_units, int n_first, void* stream) {
+  return gemm_mixed_rows(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+                         x_fp, x_fp_stride_n, x_dtype, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out,
+                         out_stride_n, out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
+                         workspace_elems, prefill_units, n_units, n_first, stream);
+}
+
+// Prefill work plan (host code).  Cost of a unit in ring steps of a pair's
+// INT8 step: a fixed part for set-up and epilogue, an INT8 step per column
+// where a row of the unit has an INT8 tile (cheaper with one row: half the
+// MFMAs and epilogue), and two half steps per 16-bit tile.  Weights measured
+// on MI355X at 8192 tokens, K = 8192: single-row INT8 step 0.68, 16-bit half
+// step 0.63 of a pair's INT8 step.
+namespace {
+constexpr double kCostFixed = 8.0, kCostInt8Pair = 1.0, kCostInt8Single = 0.7, kCost16Half = 0.65;
+constexpr double kSplitAbove = 1.5;   // split pairs costing more than this x the median pair ...
+constexpr double kSplitGain = 0.9;    // ... when each single row costs less than this x the pair
+constexpr double kFirstAbove = 1.15;  // units costing more than this x the median pair go first
+}
+
+extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* int8_tile_ids,
+                                    const int32_t* fp16_row_ptr, int n_tr, int n_tc, int32_t* units,
+                                    int max_units, int* n_first) {
+  if (int8_row_ptr == nullptr || units == nullptr || n_first == nullptr || n_tr < 1 || n_tc < 1 ||
+      max_units < n_tr || n_tr >= kUnitSingle)
+    return TQ_ERR_ARG;
+  if (int8_row_ptr[n_tr] > 0 && int8_tile_ids == nullptr) return TQ_ERR_ARG;
+  std::vector<uint8_t> has8((size_t)n_tc);
+  struct Unit { int w; double cost; };
+  std::vector<Unit> pairs, singles;
+  for (int r = 0; r < n_tr; r += 2) {
+    const int rows = r + 1 < n_tr ? 2 : 1;
+    int n8[2] = {0, 0}, n16[2] = {0, 0}, n8u = 0;
+    std::fill(has8.begin(), has8.end(), 0);
+    for (int j = 0; j < rows; ++j) {
+      const int rr = r + j;
+      const int lo = int8_row_ptr[rr], hi = int8_row_ptr[rr + 1];
+      if (hi < lo) return TQ_ERR_ARG;
+      for (int q = lo; q < hi; ++q) {
+        const int64_t c = (int64_t)int8_tile_ids[q] - (int64_t)rr * n_tc;
+        if (c < 0 || c >= n_tc) return TQ_ERR_ARG;
+        n8u += has8[c] == 0;
+        has8[c] = 1;
+      }
+      n8[j] = hi - lo;
+      if (fp16_row_ptr != nullptr) {
+        n16[j] = fp16_row_ptr[rr + 1] - fp16_row_ptr[rr];
+        if (n16[j] < 0) return TQ_ERR_ARG;
+      }
+    }
+    pairs.push_back({r, kCostFixed + kCostInt8Pair * n8u + 2 * kCost16Half * (n16[0] + n16[1])});
+    singles.push_back({r | kUnitSingle, kCostFixed + kCostInt8Single * n8[0] + 2 * kCost16Half * n16[0]});
+    singles.push_back({(r + 1) | kUnitSingle,
+                       rows == 2 ? kCostFixed + kCostInt8Single * n8[1] + 2 * kCost16Half * n16[1] : 0.0});
+  }
+  std::vector<double> sorted;
+  for (const Unit& u : pairs) sorted.push_back(u.cost);
+  std::sort(sorted.begin(), sorted.end());
+  const double median = sorted[sorted.size() / 2];
+  std::vector<Unit> plan;
+  bool any = false;
+  for (size_t i = 0; i < pairs.size(); ++i) {
+    const Unit& pu = pairs[i];
+    const Unit& a0 = singles[2 * i];
+    const Unit& a1 = singles[2 * i + 1];
+    const bool two = (pu.w + 1) < n_tr;
+    if (two && pu.cost > kSplitAbove * median && std::max(a0.cost, a1.cost) < kSplitGain * pu.cost) {
+      plan.push_back(a0);
+      plan.push_back(a1);
+      any = true;
+    } else {
+      plan.push_back(pu);
+      any |= pu.cost > kFirstAbove * median;
+    }
+  }
+  if (!any) return 0;   // balanced: the plain pair order is the plan
+  std::stable_sort(plan.begin(), plan.end(), [&](const Unit& x, const Unit& y) {
+    const bool fx = x.cost > kFirstAbove * median, fy = y.cost > kFirstAbove * median;
+    if (fx != fy) return fx;
+    return fx && x.cost > y.cost;   // heavy units by cost, the rest in row order
+  });
+  int nf = 0;
+  for (size_t i = 0; i < plan.size(); ++i) {
+    units[i] = plan[i].w;
+    nf += plan[i].cost > kFirstAbove * median;
+  }
+  *n_first = nf;
+  return (int)plan.size();
 }
 
 extern "C" int tq_linear_mixed_fused_max_tokens(int k) {

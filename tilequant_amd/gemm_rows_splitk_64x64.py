@@ -9,6 +9,7 @@ or ``"mfma"`` (the operand-major order this build's packer writes).
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, List, Optional, Tuple
 
 import torch
@@ -67,6 +68,46 @@ def _workspace(device, n, M, n_tr, n_tc, split_k):
     return (nat.ptr(ws), ws.numel()) if ws is not None else (None, 0)
 
 
+class PrefillPlan:
+    """Work plan for the prefill GEMM over one packed weight: ``units`` (a
+    device int32 tensor) lists row-tile pairs and single row tiles, the
+    ``n_first`` units carrying the most 16-bit tiles first.  Built on the host
+    from the row pointers (``prefill_plan``); the outputs do not depend on it."""
+
+    __slots__ = ("units", "n_first")
+
+    def __init__(self, units: torch.Tensor, n_first: int):
+        self.units, self.n_first = units, int(n_first)
+
+
+def prefill_plan(*, int8_tile_ids: torch.Tensor, int8_row_ptr: torch.Tensor, fp16_row_ptr: torch.Tensor,
+                 n_tr: int, n_tc: int, device=None) -> Optional[PrefillPlan]:
+    """Plan the prefill GEMM's work units from the pack's tile bookkeeping:
+    row-tile pairs whose many 16-bit tiles would make them finish long after
+    the others are split into single row tiles, and the heaviest units are
+    dispatched first.  Returns None when the plain pair order is balanced.
+    Copies the row pointers and INT8 ids to the host (a synchronisation):
+    call it once per weight, outside graph capture."""
+    n_tr, n_tc = int(n_tr), int(n_tc)
+    rp8 = int8_row_ptr.detach().to("cpu", torch.int32).contiguous()
+    ids8 = int8_tile_ids.detach().to("cpu", torch.int32).contiguous()
+    rp16 = fp16_row_ptr.detach().to("cpu", torch.int32).contiguous() if fp16_row_ptr.numel() else None
+    if rp8.numel() < n_tr + 1 or (rp16 is not None and rp16.numel() < n_tr + 1):
+        raise ValueError("row pointers must have n_tr + 1 entries")
+    units = torch.empty(max(n_tr, 1), dtype=torch.int32)
+    n_first = ctypes.c_int(0)
+    rc = nat.lib().tq_gemm_prefill_plan(
+        rp8.data_ptr(), ids8.data_ptr() if ids8.numel() else None,
+        rp16.data_ptr() if rp16 is not None else None, n_tr, n_tc, units.data_ptr(), units.numel(),
+        ctypes.byref(n_first))
+    if rc < 0:   # a count otherwise
+        nat.check(rc, "tq_gemm_prefill_plan")
+    if rc == 0:
+        return None
+    dev = device if device is not None else int8_row_ptr.device
+    return PrefillPlan(units[:rc].to(dev), n_first.value)
+
+
 def _check_tiles(name: str, t: torch.Tensor, dtype) -> None:
     if t.dtype != dtype:
         raise ValueError(f"{name} must have dtype {dtype}, got {t.dtype}")
@@ -95,6 +136,7 @@ def gemm_mixed_rows_splitk(
     split_k: Optional[int] = None,
     out: Optional[torch.Tensor] = None,
     tile_layout: str = "row_major",
+    prefill_plan: Optional[PrefillPlan] = None,
 ) -> torch.Tensor:
     """Return x @ W^T (+ bias) for a packed mixed INT8/16-bit weight.
 
@@ -102,7 +144,9 @@ def gemm_mixed_rows_splitk(
     (optional) is an (N, M) tensor with unit column stride to write into.
     ``split_k`` (optional, >= 1) fixes how many partitions of each row tile's
     tile list are reduced per output tile (in fixed order); ``None`` picks it
-    from the shape.  Results are bitwise reproducible for fixed arguments.
+    from the shape.  ``prefill_plan`` (optional, from ``prefill_plan()`` for
+    this weight) orders the prefill kernel's work; it does not change the
+    result.  Results are bitwise reproducible for fixed arguments.
     """
     nat.require_device(x_fp, x_int8, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
                        fp16_tiles, fp16_tile_ids, fp16_row_ptr, bias, out)
@@ -135,16 +179,25 @@ def gemm_mixed_rows_splitk(
     if n == 0 or M == 0:
         return out
     ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
-    rc = nat.lib().tq_gemm_mixed_rows(
-        nat.ptr(x_int8), x_int8.stride(0), nat.ptr(sx),
-        nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
-        nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
-        nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
-        nat.ptr(fp16_row_ptr) if has16 else None,
-        nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
-        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems,
-        nat.stream_handle(x_fp.device))
-    nat.check(rc, "tq_gemm_mixed_rows")
+    args = (nat.ptr(x_int8), x_int8.stride(0), nat.ptr(sx),
+            nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
+            nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
+            nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
+            nat.ptr(fp16_row_ptr) if has16 else None,
+            nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
+            n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems)
+    if prefill_plan is not None:
+        units = prefill_plan.units
+        if units.device != x_fp.device or units.dtype != torch.int32 or not units.is_contiguous():
+            raise ValueError("prefill_plan.units must be a contiguous int32 tensor on the input's device")
+        if not 0 < units.numel() <= n_tr or not 0 <= prefill_plan.n_first <= units.numel():
+            raise ValueError("prefill_plan does not fit this weight")
+        rc = nat.lib().tq_gemm_mixed_rows_planned(*args, nat.ptr(units), units.numel(), prefill_plan.n_first,
+                                                  nat.stream_handle(x_fp.device))
+        nat.check(rc, "tq_gemm_mixed_rows_planned")
+    else:
+        rc = nat.lib().tq_gemm_mixed_rows(*args, nat.stream_handle(x_fp.device))
+        nat.check(rc, "tq_gemm_mixed_rows")
     return out
 
 

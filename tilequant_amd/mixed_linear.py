@@ -40,7 +40,8 @@ import torch
 import torch.nn as nn
 
 from . import _native as nat
-from .gemm_rows_splitk_64x64 import fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused
+from .gemm_rows_splitk_64x64 import (PrefillPlan, fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused,
+                                     prefill_plan)
 from .pack import Pack, concat_packs_along_rows
 from .quant_utils import (
     activation_tile_absmax_scales,
@@ -49,6 +50,9 @@ from .quant_utils import (
 )
 
 DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 16384
+# Above this many rows the GEMM runs its prefill kernel, which takes a work
+# plan (row-tile units ordered by their 16-bit load; see _prefill_plan).
+PLAN_MIN_ROWS = 64
 # Rows up to which cfg.fused_decode = "auto" fuses quantization into the GEMM
 # (measured on MI355X: 1 row saves ~2 us per projection, 4 rows break even).
 FUSED_AUTO_MAX_ROWS = 2
@@ -222,9 +226,11 @@ class MixedLinear(nn.Module):
         else:
             self.register_parameter("bias", None)
         self._launches: Dict[Tuple[Any, ...], _Launch] = {}
+        self._plan: Optional[Tuple[Optional[PrefillPlan]]] = None   # (plan,) once built
 
     def _apply(self, fn, recurse=True):
         self._launches = {}   # descriptors point at the old tensors
+        self._plan = None
         return super()._apply(fn, recurse)
 
     # the tile storage order travels with the state_dict
@@ -243,6 +249,7 @@ class MixedLinear(nn.Module):
         if key not in state_dict:
             self.tile_layout = "row_major"
         self._launches = {}
+        self._plan = None
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
         if key not in state_dict and key in missing_keys:
@@ -268,6 +275,20 @@ class MixedLinear(nn.Module):
             bias = bias.to(dtype=out_dtype).contiguous()
         return bias
 
+    def _prefill_plan(self, n_rows: int) -> Optional[PrefillPlan]:
+        """The prefill kernel's work plan for this weight (None: plain pair
+        order).  Built once, on the first call above the decode sizes outside
+        graph capture (it reads the row pointers on the host); until then, and
+        for decode sizes, calls run without one.  Outputs do not depend on it."""
+        if n_rows <= PLAN_MIN_ROWS:
+            return None
+        if self._plan is None:
+            if not self.int8_row_ptr.is_cuda or torch.cuda.is_current_stream_capturing():
+                return None
+            self._plan = (prefill_plan(int8_tile_ids=self.int8_tile_ids, int8_row_ptr=self.int8_row_ptr,
+                                       fp16_row_ptr=self.fp16_row_ptr, n_tr=self.n_tr, n_tc=self.n_tc),)
+        return self._plan[0]
+
     def _gemm_bias(self, x_fp: torch.Tensor, x_int8: torch.Tensor, sx: torch.Tensor,
                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
         out_dtype = self._out_dtype()
@@ -277,6 +298,7 @@ class MixedLinear(nn.Module):
             int8_row_ptr=self.int8_row_ptr, fp16_tiles=self.fp16_tiles, fp16_tile_ids=self.fp16_tile_ids,
             fp16_row_ptr=self.fp16_row_ptr, M=self.M_orig, K=self.K_orig, n_tr=self.n_tr, n_tc=self.n_tc,
             out_dtype=out_dtype, bias=self._out_bias(out_dtype), out=out, tile_layout=self.tile_layout,
+            prefill_plan=self._prefill_plan(int(x_fp.shape[0])),
         )
 
     def _fused_limit(self) -> int:
