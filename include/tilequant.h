@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-enum { TQ_DTYPE_BF16 = 0, TQ_DTYPE_FP16 = 1 };
+enum { TQ_DTYPE_BF16 = 0, TQ_DTYPE_FP16 = 1, TQ_DTYPE_FP32 = 2 /* tq_quant_tensor_absmax only */ };
 
 /* Storage order of the 64x64 elements inside one packed tile.
  * ROW_MAJOR: tile[j][k] at j*64+k (the reference packer's order, pack.py:115-175).
@@ -91,6 +91,23 @@ int tq_act_quant_with_scales(const void* x, int64_t x_stride_n, int64_t x_stride
 int tq_act_quant_two_level(const void* x, int64_t x_stride_n, int x_dtype, int n, int k, int8_t* q,
                            int64_t q_stride_n, float* sx, float* workspace, int64_t workspace_elems,
                            void* stream);
+
+/* One scale for a whole tensor: replaces quantize_activation_absmax /
+ * quantize_activation_per_tensor_absmax (src/kernels/quant_utils.py:17-37) and
+ * quantize_weight_tile_absmax (:138-148), torch expressions there:
+ *   a = max |x|;  scale = a == 0 ? 1 : f32(x_dtype(f32(a) / 127));
+ *   q = clamp(rint(x_dtype(f32(x) / scale)), -127, 127)
+ * -- the quotient is rounded to x's dtype before rint (a 16-bit tensor divided
+ * by a 0-dim fp32 tensor stays 16-bit in torch); fp32 inputs skip both
+ * roundings.  x: numel contiguous elements of x_dtype (BF16, FP16 or FP32);
+ * q: numel int8; scale: one float written on the device.  numel == 0 writes
+ * nothing (the reference returns scale 1).  workspace:
+ * tq_quant_tensor_workspace_elems(numel) floats (0: none needed).  A tensor
+ * whose scale underflows to 0 (max |x| < 127 * 2^-134 in bf16) gets codes
+ * 127 for x == 0, where the reference's int8 cast of NaN is undefined. */
+int64_t tq_quant_tensor_workspace_elems(int64_t numel);
+int tq_quant_tensor_absmax(const void* x, int64_t numel, int x_dtype, int8_t* q, float* scale,
+                           float* workspace, int64_t workspace_elems, void* stream);
 
 /* ---- mixed INT8/BF16 tile GEMM -----------------------------------------
  * out[n, m] = sum over the INT8 tiles t of output row tile r = m / 64:

@@ -16,13 +16,18 @@ Contents:
 * ``oracle.masks`` -- the Decision/ tile-map archive format and the top-k
   mask rule.
 * ``oracle.torch_ref`` -- the reference's CPU quantization branch as torch
-  ops (quant_utils.py:61-74, 103-115): checker, and the quantization leg of
-  the CPU baseline.
+  ops (quant_utils.py:61-74, 103-115) and its whole-tensor helpers
+  (:17-37, 138-148): checker, and the quantization leg of the CPU baseline.
 * ``oracle.native`` -- ctypes wrapper of ``tq_oracle.c`` (same closed forms in
   C, OpenMP over row tiles) for the larger cases and the CPU baseline.
 
 Parity pinning (what checks each function):
 
+* whole-tensor quantization (``numerics.tensor_quant``): exhaustive sweeps of
+  every bf16 / fp16 value of a range against the reference's torch expressions
+  on CPU tensors (``torch_ref.tensor_quant``), with exact half-integer
+  quotients; a planted mistake (the quotient not rounded to the input dtype)
+  must fail.
 * activation/weight closed forms: exhaustive sweeps over bf16 values against
   torch-CPU ops (the reference's own CPU branch, quant_utils.py:61-74,
   103-115), numpy-vs-C agreement, and the invariant that a tile's absmax

@@ -105,6 +105,36 @@ def act_quant(x: np.ndarray, is_bf16: bool = True):
 
 
 # ---------------------------------------------------------------------------
+# one scale per tensor (quant_utils.py:17-37 quantize_activation_absmax /
+# quantize_activation_per_tensor_absmax, :138-148 quantize_weight_tile_absmax)
+# ---------------------------------------------------------------------------
+
+def tensor_quant(x: np.ndarray, dtype: str = "bf16"):
+    """(codes int8 like x, scale f32) for x holding values of `dtype`
+    ("bf16", "fp16" or "fp32").
+
+    The reference's torch expressions: max_abs = x.abs().max() (exact);
+    sx = (max_abs / 127.0).to(float32) -- the quotient stays in x's dtype, so
+    it is f32(a) / 127 rounded to that dtype; scale 1 when max_abs == 0 (or x is
+    empty).  x_fp / sx divides a 16-bit tensor by a 0-dim fp32 tensor, which
+    torch computes in fp32 and rounds to x's dtype; torch.round is half-even;
+    clamp to [-127, 127]; cast to int8.  (quant_utils.py:17-32, 138-148)
+    """
+    x = np.asarray(x, dtype=np.float32)
+    rnd = (lambda v: np.asarray(v, dtype=np.float32)) if dtype == "fp32" else (
+        lambda v: round_to_dtype(v, dtype == "bf16"))
+    if x.size == 0:
+        return np.zeros(x.shape, np.int8), np.float32(1.0)
+    a = np.float32(np.max(np.abs(x)))
+    if a == 0:
+        return np.zeros(x.shape, np.int8), np.float32(1.0)
+    s = np.float32(rnd(np.float32(a) / np.float32(127.0)))
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        q = np.rint(rnd(x / s))
+    return np.clip(q, -127, 127).astype(np.int8), s
+
+
+# ---------------------------------------------------------------------------
 # weight tiles (pack.py:119-130, 163-167)
 # ---------------------------------------------------------------------------
 

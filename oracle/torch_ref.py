@@ -49,3 +49,16 @@ def act_codes_with_scales(x: torch.Tensor, sx: torch.Tensor) -> torch.Tensor:
 def act_quant(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     sx = act_tile_scales(x)
     return act_codes_with_scales(x, sx), sx
+
+
+def tensor_quant(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quant_utils.py:17-32 (quantize_activation_absmax; also the body of
+    quantize_weight_tile_absmax, :138-148): one scale for the whole tensor,
+    the reference's torch expressions op for op on a CPU tensor."""
+    if x.numel() == 0:
+        return torch.zeros_like(x, dtype=torch.int8), torch.tensor(1.0, dtype=torch.float32)
+    max_abs = x.abs().max()
+    if float(max_abs.item()) == 0.0:
+        return torch.zeros_like(x, dtype=torch.int8), torch.tensor(1.0, dtype=torch.float32)
+    sx = (max_abs / INT8_MAX).to(torch.float32)
+    return torch.clamp(torch.round(x / sx), -127, 127).to(torch.int8), sx

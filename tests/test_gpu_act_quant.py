@@ -173,3 +173,56 @@ def test_two_level_argument_errors():
                                       ws.data_ptr(), 1, stream) == TQ_ERR_WORKSPACE
     assert lib.tq_act_quant_two_level(x.data_ptr(), 128, 0, 500, 128, q.data_ptr(), 128, sx.data_ptr(),
                                       ws.data_ptr(), ws.numel(), stream) == nat.TQ_ERR_ARG
+
+
+def _tensor_case(shape, dtype, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("shape,dtype", [
+    ((64, 64), torch.bfloat16),        # quantize_weight_tile_absmax's tile
+    ((4, 3072), torch.bfloat16),
+    ((1,), torch.bfloat16),
+    ((2, 3, 64), torch.float16),       # any rank
+    ((1000, 1000), torch.float16),     # two-pass form (above one workgroup's 65536 elements)
+    ((3000, 4096), torch.bfloat16),    # 12.3 M elements
+    ((70000,), torch.float32),
+])
+def test_tensor_absmax_quant_matches_oracle(shape, dtype):
+    """quantize_activation_absmax / _per_tensor_absmax / quantize_weight_tile_absmax
+    (tq_quant_tensor_absmax) vs the oracle: codes and scale bitwise."""
+    x = _tensor_case(shape, dtype, seed=sum(shape))
+    name = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    q_ref, s_ref = nm.tensor_quant(x.float().numpy(), name)
+    for fn in (quant_utils.quantize_activation_absmax, quant_utils.quantize_activation_per_tensor_absmax,
+               quant_utils.quantize_weight_tile_absmax):
+        q, s = fn(x.cuda())
+        assert q.shape == x.shape and q.dtype == torch.int8 and s.dim() == 0 and s.dtype == torch.float32
+        assert np.float32(s.item()).view(np.uint32) == np.float32(s_ref).view(np.uint32)
+        assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("dtype,amax", [(torch.bfloat16, 100.0), (torch.bfloat16, 127.0), (torch.float16, 1000.0)])
+def test_tensor_absmax_quant_every_value_of_a_range(dtype, amax):
+    """Every bf16 / fp16 value in [-amax, amax] in one tensor (exact half-integer
+    quotients included), contiguous and as a transposed view."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = (nm.bf16_bits_to_f32(bits) if dtype == torch.bfloat16 else bits.view(np.float16).astype(np.float32))
+    v = np.unique(v[np.isfinite(v) & (np.abs(v) <= amax)])
+    v = v[: (v.size // 8) * 8]
+    x = torch.from_numpy(v).to(dtype)
+    q_ref, s_ref = nm.tensor_quant(x.float().numpy(), "bf16" if dtype == torch.bfloat16 else "fp16")
+    q, s = quant_utils.quantize_activation_absmax(x.cuda())
+    assert s.item() == s_ref and np.array_equal(q.cpu().numpy(), q_ref)
+    xt = x.view(8, -1).cuda().t()   # non-contiguous
+    qt, st = quant_utils.quantize_activation_absmax(xt)
+    assert st.item() == s_ref and np.array_equal(qt.cpu().numpy(), q_ref.reshape(8, -1).T)
+
+
+def test_tensor_absmax_quant_zero_and_empty():
+    for x in (torch.zeros((5, 64), dtype=torch.bfloat16), torch.zeros((0, 64), dtype=torch.bfloat16)):
+        q, s = quant_utils.quantize_weight_tile_absmax(x.cuda())
+        assert s.item() == 1.0 and q.shape == x.shape and int(q.abs().sum()) == 0
+    with pytest.raises(ValueError):
+        quant_utils.quantize_activation_absmax(torch.zeros(4, dtype=torch.int32, device="cuda"))

@@ -26,6 +26,10 @@ def test_quant_ops_refuse_cpu_tensors():
         quant_utils.quantize_activation_tile_absmax(x)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         quant_utils.activation_tile_absmax_scales(x)
+    for fn in (quant_utils.quantize_activation_absmax, quant_utils.quantize_activation_per_tensor_absmax,
+               quant_utils.quantize_weight_tile_absmax):
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            fn(x)
     with pytest.raises(ValueError):
         quant_utils.quantize_activation_tile_absmax(x.view(2, 2, 128))
     with pytest.raises(ValueError):

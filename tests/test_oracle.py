@@ -333,3 +333,51 @@ def test_released_archive_format():
     for stem, ((n_tr, n_tc), ids) in arch.items():
         assert ids.dtype == np.uint16 and np.all(np.diff(ids.astype(np.int64)) > 0)
         assert ids.size == om.keep_count(n_tr * n_tc, 0.01)
+
+
+def _all_bf16_in(lo, hi):
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = nm.bf16_bits_to_f32(bits)
+    return np.unique(v[np.isfinite(v) & (v >= lo) & (v <= hi)])
+
+
+@pytest.mark.parametrize("dtype,amax", [("bf16", 127.0), ("bf16", 100.0), ("bf16", 3.0e-3), ("fp16", 1000.0),
+                                        ("fp16", 0.37), ("fp32", 5.0)])
+def test_tensor_quant_matches_reference_torch_expressions(dtype, amax):
+    """oracle.numerics.tensor_quant against the reference's own torch
+    expressions (quant_utils.py:17-32, on CPU tensors) over every value of the
+    dtype in [-amax, amax] (fp32: a dense grid with exact half-integer
+    quotients), plus all-zero and empty tensors."""
+    from oracle import torch_ref
+
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    if dtype == "bf16":
+        v = _all_bf16_in(-amax, amax)
+    elif dtype == "fp16":
+        h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+        v = np.unique(h[np.isfinite(h) & (np.abs(h) <= amax)])
+    else:
+        s = np.float32(amax) / np.float32(127.0)
+        v = np.concatenate([np.arange(-1270, 1271, dtype=np.float32) / np.float32(10) * s,
+                            (np.arange(-127, 127, dtype=np.float32) + np.float32(0.5)) * s, [np.float32(amax)]])
+    x = torch.from_numpy(np.asarray(v, np.float32)).to(tdt)
+    q_t, s_t = torch_ref.tensor_quant(x)
+    q, s = nm.tensor_quant(x.float().numpy(), dtype)
+    assert np.float32(s) == np.float32(s_t.item())
+    assert np.array_equal(q, q_t.numpy())
+    assert q.min() >= -127 and q.max() <= 127 and np.abs(q).max() >= 126
+    for special in (torch.zeros((3, 5), dtype=tdt), torch.zeros((0, 64), dtype=tdt)):
+        q0, s0 = nm.tensor_quant(special.float().numpy(), dtype)
+        q0t, s0t = torch_ref.tensor_quant(special)
+        assert q0.shape == tuple(special.shape) and np.array_equal(q0, q0t.numpy()) and s0 == s0t.item() == 1.0
+
+
+def test_tensor_quant_planted_mistake_is_caught():
+    """Dropping the rounding of the quotient to bf16 (rint of the fp32 quotient,
+    as the tile kernels do) disagrees with the reference's expressions."""
+    from oracle import torch_ref
+
+    x = torch.from_numpy(_all_bf16_in(-100.0, 100.0)).to(torch.bfloat16)
+    q_t, s_t = torch_ref.tensor_quant(x)
+    wrong = nm.quant_codes(x.float().numpy(), np.float32(s_t.item()))
+    assert not np.array_equal(wrong, q_t.numpy())

@@ -35,6 +35,8 @@ _SIGNATURES = {
     "tq_act_absmax_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
     "tq_act_quant_with_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
     "tq_act_quant_two_level": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _p, _p, _i64, _p]),
+    "tq_quant_tensor_workspace_elems": (_i64, [_i64]),
+    "tq_quant_tensor_absmax": (_i, [_p, _i64, _i, _p, _p, _p, _i64, _p]),
     "tq_gemm_workspace_elems": (_i64, [_i, _i, _i, _i, _i]),
     "tq_gemm_mixed_rows": (_i, [_p, _i64, _p,
                                 _p, _p, _p, _p,

@@ -23,6 +23,8 @@
 //                        per thread on the aligned path.
 // Every kernel has a vector path (unit column stride, 16-byte aligned rows,
 // full tiles) and a scalar path for everything else.
+#include <algorithm>
+
 #include "tq_common.h"
 
 namespace tq {
@@ -202,6 +204,61 @@ act_quant_scaled_kernel(XView v, const float* __restrict__ sx, int8_t* __restric
   }
 }
 
+// ---- one scale for a whole tensor ------------------------------------------
+//
+// quantize_activation_absmax / quantize_weight_tile_absmax
+// (src/kernels/quant_utils.py:17-37, 138-148), which are torch expressions:
+//   a = max |x|                      (exact in x's dtype)
+//   s = a == 0 ? 1 : f32(x_dtype(f32(a) / 127))      (max_abs / 127.0 stays in x's dtype)
+//   q = clamp(rint(x_dtype(f32(x) / s)), -127, 127)  (a 16-bit tensor divided by a 0-dim
+//       fp32 tensor stays 16-bit in torch, so the quotient is rounded to x's dtype
+//       before torch.round -- unlike the tile kernels above, which round fl32(x / s))
+// IEEE divides, half-even rint.  fp32 inputs skip both dtype roundings.
+// Small tensors take one workgroup (absmax then codes); larger ones a
+// partial-max pass and a codes pass that reduces the partials itself.
+struct F32 {
+  __device__ static inline float to_f32(uint32_t b) { return __uint_as_float(b); }
+  __device__ static inline float round(float f) { return f; }
+};
+
+template <class T>
+__device__ inline int8_t tensor_code(float v, float s) {
+  const float t = __builtin_rintf(T::round(v / s));
+  return (int8_t)(int)fmaxf(fminf(t, 127.0f), -127.0f);
+}
+
+constexpr int64_t kTensorOneGroupMax = 1 << 16;   // elements quantized by a single workgroup
+constexpr int kTensorPartials = 1024;              // partial maxima of the two-pass form
+
+template <class T, class S>
+__global__ void __launch_bounds__(kQuantThreads)
+tensor_absmax_partial_kernel(const S* __restrict__ x, int64_t n, float* __restrict__ partial) {
+  __shared__ float red[kQuantThreads / kWave];
+  float m = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQuantThreads)
+    m = fmaxf(m, fabsf(T::to_f32(x[i])));
+  m = block_max(m, red, kQuantThreads / kWave);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+// partial == nullptr: this (single) workgroup takes the absmax itself.
+template <class T, class S>
+__global__ void __launch_bounds__(kQuantThreads)
+tensor_quant_kernel(const S* __restrict__ x, int64_t n, const float* __restrict__ partial, int n_partial,
+                    int8_t* __restrict__ q, float* __restrict__ s_out) {
+  __shared__ float red[kQuantThreads / kWave];
+  float m = 0.0f;
+  if (partial == nullptr) {
+    for (int64_t i = threadIdx.x; i < n; i += kQuantThreads) m = fmaxf(m, fabsf(T::to_f32(x[i])));
+  } else {
+    for (int i = threadIdx.x; i < n_partial; i += kQuantThreads) m = fmaxf(m, partial[i]);
+  }
+  const float s = act_scale_from_absmax<T>(block_max(m, red, kQuantThreads / kWave));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *s_out = s;
+  for (int64_t i = (int64_t)blockIdx.x * kQuantThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQuantThreads)
+    q[i] = tensor_code<T>(T::to_f32(x[i]), s);
+}
+
 static int n_tiles_of(int k) { return (k + kTile - 1) / kTile; }
 
 static int check_x(const void* x, int64_t sn, int64_t sk, int dtype, int n, int k) {
@@ -326,5 +383,37 @@ extern "C" int tq_act_quant_two_level(const void* x, int64_t x_stride_n, int x_d
     hipLaunchKernelGGL(act_absmax_partial_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, workspace, kPartialRows, 0);
     hipLaunchKernelGGL(act_quant_block_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, workspace, n_rb, q, q_stride_n, sx);
   }
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t tq_quant_tensor_workspace_elems(int64_t numel) {
+  return numel > kTensorOneGroupMax ? kTensorPartials : 0;
+}
+
+template <class T, class S>
+static void launch_tensor_quant(const void* x, int64_t numel, int8_t* q, float* s_out, float* ws, hipStream_t s) {
+  const S* xs = static_cast<const S*>(x);
+  if (numel <= kTensorOneGroupMax) {
+    hipLaunchKernelGGL((tensor_quant_kernel<T, S>), dim3(1), dim3(kQuantThreads), 0, s, xs, numel, nullptr, 0, q, s_out);
+    return;
+  }
+  hipLaunchKernelGGL((tensor_absmax_partial_kernel<T, S>), dim3(kTensorPartials), dim3(kQuantThreads), 0, s, xs, numel,
+                     ws);
+  const int64_t blocks = std::min<int64_t>((numel + 8 * kQuantThreads - 1) / (8 * kQuantThreads), 4096);
+  hipLaunchKernelGGL((tensor_quant_kernel<T, S>), dim3((unsigned)blocks), dim3(kQuantThreads), 0, s, xs, numel, ws,
+                     kTensorPartials, q, s_out);
+}
+
+extern "C" int tq_quant_tensor_absmax(const void* x, int64_t numel, int x_dtype, int8_t* q, float* scale,
+                                      float* workspace, int64_t workspace_elems, void* stream) {
+  if (numel < 0 || scale == nullptr || (numel > 0 && (x == nullptr || q == nullptr))) return TQ_ERR_ARG;
+  if (x_dtype != TQ_DTYPE_BF16 && x_dtype != TQ_DTYPE_FP16 && x_dtype != TQ_DTYPE_FP32) return TQ_ERR_DTYPE;
+  if (numel == 0) return TQ_OK;   // the caller's scale is 1 (no launch)
+  const int64_t need = tq_quant_tensor_workspace_elems(numel);
+  if (need > 0 && (workspace == nullptr || workspace_elems < need)) return TQ_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == TQ_DTYPE_BF16) launch_tensor_quant<Bf16, uint16_t>(x, numel, q, scale, workspace, s);
+  else if (x_dtype == TQ_DTYPE_FP16) launch_tensor_quant<Fp16, uint16_t>(x, numel, q, scale, workspace, s);
+  else launch_tensor_quant<F32, uint32_t>(x, numel, q, scale, workspace, s);
   return (int)hipGetLastError();
 }

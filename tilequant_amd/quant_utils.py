@@ -13,6 +13,7 @@ from typing import Tuple
 
 import torch
 
+from . import _native as nat
 from .quantize_activation import (
     activation_tile_absmax_scales_64_fused,
     quantize_activation_tile_absmax_fused,
@@ -25,6 +26,50 @@ INT8_MAX = 127.0
 # The reference quantizes up to this many rows in one fused launch
 # (quant_utils.py:127-133); larger inputs take scales + codes.
 FUSED_MAX_ROWS = 128
+
+_TENSOR_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}   # TQ_DTYPE_*
+
+
+def _quantize_tensor_absmax(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One absmax scale for the whole tensor (tq_quant_tensor_absmax): codes
+    shaped like x_fp and a 0-dim float32 scale, both on x_fp's device."""
+    nat.require_device(x_fp)
+    code = _TENSOR_DTYPES.get(x_fp.dtype)
+    if code is None:
+        raise ValueError(f"expected a bfloat16, float16 or float32 tensor, got {x_fp.dtype}")
+    q = torch.empty(x_fp.shape, device=x_fp.device, dtype=torch.int8)
+    sx = torch.ones((), device=x_fp.device, dtype=torch.float32)
+    n = x_fp.numel()
+    if n == 0:
+        return q, sx
+    x = x_fp.contiguous()
+    need = int(nat.lib().tq_quant_tensor_workspace_elems(n))
+    ws = torch.empty(need, device=x.device, dtype=torch.float32) if need else None
+    rc = nat.lib().tq_quant_tensor_absmax(nat.ptr(x), n, code, nat.ptr(q), nat.ptr(sx), nat.ptr(ws), need,
+                                          nat.stream_handle(x.device))
+    nat.check(rc, "tq_quant_tensor_absmax")
+    return q, sx
+
+
+def quantize_activation_absmax(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(codes, scale) with ONE scale for the whole tensor (quant_utils.py:17-32):
+    scale = (max|x| / 127) in x's dtype, widened to float32 (1 for an empty or
+    all-zero tensor); codes = clamp(round(x / scale), -127, 127), the quotient
+    rounded to x's dtype as torch does for a 16-bit tensor."""
+    return _quantize_tensor_absmax(x_fp)
+
+
+def quantize_activation_per_tensor_absmax(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Alias of quantize_activation_absmax (quant_utils.py:35-38)."""
+    return quantize_activation_absmax(x_fp)
+
+
+def quantize_weight_tile_absmax(w_fp_tile_64x64: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(codes, scale) of one weight tile with one absmax scale
+    (quant_utils.py:138-148): the same closed form as quantize_activation_absmax.
+    (The load-time packer's per-tile scales are f32(a) / 127 unrounded,
+    pack.py:125-130; this helper keeps the reference helper's own form.)"""
+    return _quantize_tensor_absmax(w_fp_tile_64x64)
 
 
 def _check_tile(x_fp: torch.Tensor, tile_n: int) -> None:
