@@ -3,7 +3,8 @@
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
 Follows src/kernels/pack.py:38-62 (id order, CSR row pointers), 65-203
-(tile gather and per-tile INT8 quantization, "gi" style), 246-321 (row
+(tile gather and per-tile INT8 quantization, "gi" style; the "iaa" scale
+search of :132-159 in ``iaa_scales``), 246-321 (row
 stacking of packs that share one input) and src/quantization/api.py:112-117
 (INT8 ids are the complement of the BF16 ids).
 """
@@ -103,6 +104,47 @@ def concat_rows(packs):
         int8_tile_ids=out["int8"][1], int8_row_ptr=out["int8"][2],
         fp16_tiles=out["fp16"][0], fp16_tile_ids=out["fp16"][1], fp16_row_ptr=out["fp16"][2],
     )
+
+
+# ---------------------------------------------------------------------------
+# IAA scale search (pack.py:132-159)
+# ---------------------------------------------------------------------------
+
+IAA_MULTS = (0.75, 1.00, 1.25)
+
+
+def iaa_scales(tiles: np.ndarray, col_imp: np.ndarray):
+    """IAA per-tile scale choice for INT8 tiles [T, 64, 64] (float values) whose
+    64 columns have importances col_imp [T, 64] (the tile's slice of the input-
+    column importance vector).
+
+    pack.py:132-159: base = 1 if a == 0 else f32(a) / 127; candidates
+    s = max(base * m, 1e-12) for m in (0.75, 1, 1.25); the fp32 terms
+    ((clamp(rint(w / s), -127, 127) * s - w)^2 * max(imp, 1e-8)) are formed op
+    by op in fp32 as the reference's torch expressions do; their mean over the
+    tile decides, the first candidate with a strictly lower error winning.
+    The reference's fp32 mean has its own summation order; here the terms are
+    summed in float64 (relative error ~2^-40), so the selection is the exact
+    one.  Returns (scales f32 [T], errors f64 [3, T]) -- the errors let a
+    caller see which tiles are near-ties within an fp32 summation bound.
+    """
+    t = np.asarray(tiles, dtype=np.float32)
+    wm = np.maximum(np.asarray(col_imp, dtype=np.float32), np.float32(1e-8))[:, None, :]
+    base = nm.weight_tile_scales(t)
+    errs, cands = [], []
+    for m in IAA_MULTS:
+        sc = np.maximum(base * np.float32(m), np.float32(1e-12)).astype(np.float32)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            q = np.clip(np.rint(t / sc[:, None, None]), -127, 127).astype(np.float32)
+        d = (q * sc[:, None, None] - t).astype(np.float32)
+        terms = ((d * d).astype(np.float32) * wm).astype(np.float32)
+        errs.append(terms.astype(np.float64).sum(axis=(1, 2)) / 4096.0)
+        cands.append(sc)
+    errs = np.stack(errs)
+    best = np.zeros(t.shape[0], dtype=np.int64)
+    for i in (1, 2):
+        best = np.where(errs[i] < errs[best, np.arange(t.shape[0])], i, best)
+    return np.stack(cands)[best, np.arange(t.shape[0])].astype(np.float32), errs
 
 
 # ---------------------------------------------------------------------------

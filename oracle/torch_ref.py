@@ -62,3 +62,28 @@ def tensor_quant(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         return torch.zeros_like(x, dtype=torch.int8), torch.tensor(1.0, dtype=torch.float32)
     sx = (max_abs / INT8_MAX).to(torch.float32)
     return torch.clamp(torch.round(x / sx), -127, 127).to(torch.int8), sx
+
+
+def iaa_scales(src: torch.Tensor, col_imp_tiles: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """pack.py:132-159 op for op on CPU tensors: src [T, 64, 64] 16-bit INT8
+    tiles, col_imp_tiles [T, 64] their columns' importances.  Returns the
+    chosen scales [T] and the candidates' fp32 mean errors [3, T]."""
+    max_abs = src.abs().amax(dim=(1, 2)).to(torch.float32)
+    base = torch.where(max_abs == 0, torch.ones_like(max_abs, dtype=torch.float32),
+                       (max_abs / 127.0).to(torch.float32))
+    wm = col_imp_tiles.to(torch.float32).clamp_min(1e-8)[:, None, :]
+    src_f = src.to(torch.float32)
+    best_err = best_scales = None
+    errs = []
+    for m in torch.tensor([0.75, 1.00, 1.25], dtype=torch.float32):
+        s = (base * m).clamp_min(1e-12)
+        dq = torch.clamp(torch.round(src_f / s[:, None, None]), -127, 127) * s[:, None, None]
+        err = ((dq - src_f) ** 2 * wm).mean(dim=(1, 2))
+        errs.append(err)
+        if best_err is None:
+            best_err, best_scales = err, s
+        else:
+            better = err < best_err
+            best_err = torch.where(better, err, best_err)
+            best_scales = torch.where(better, s, best_scales)
+    return best_scales.to(torch.float32), torch.stack(errs)

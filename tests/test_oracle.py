@@ -381,3 +381,41 @@ def test_tensor_quant_planted_mistake_is_caught():
     q_t, s_t = torch_ref.tensor_quant(x)
     wrong = nm.quant_codes(x.float().numpy(), np.float32(s_t.item()))
     assert not np.array_equal(wrong, q_t.numpy())
+
+
+def _iaa_case(m, k, seed, dtype=torch.bfloat16):
+    from oracle import packing as opk
+
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn((m, k), generator=g) * 0.02).to(dtype)
+    W[:64, :64] = 0                       # an all-zero tile: the three candidates tie exactly
+    imp = torch.rand(k, generator=g) * 3
+    imp[64:128] = 0                       # importance clamped to 1e-8
+    n_tr, n_tc = m // 64, k // 64
+    src = W.view(n_tr, 64, n_tc, 64).permute(0, 2, 1, 3).reshape(-1, 64, 64)
+    cols = torch.arange(n_tr * n_tc) % n_tc
+    return src, imp.view(n_tc, 64)[cols], opk
+
+
+def test_iaa_oracle_matches_reference_torch_expressions():
+    """oracle.packing.iaa_scales (float64 error sums) against the reference's
+    torch expressions (pack.py:132-159 on CPU tensors, fp32 means): the same
+    choice on every tile whose two best errors differ by more than an fp32
+    summation bound, and few tiles inside it; the all-zero tile takes the
+    first candidate (0.75 x 1)."""
+    from oracle import torch_ref
+
+    src, col_imp, opk = _iaa_case(512, 2048, seed=5)
+    s_ref, e_ref = torch_ref.iaa_scales(src, col_imp)
+    s_or, e_or = opk.iaa_scales(src.float().numpy(), col_imp.numpy())
+    srt = np.sort(e_or, axis=0)
+    near = (srt[1] - srt[0]) <= 1e-4 * srt[1]
+    assert np.array_equal(s_or[~near], s_ref.numpy()[~near])
+    assert near.sum() <= 3 and s_or[0] == np.float32(0.75)
+    # the fp32 means agree with the float64 ones to fp32 summation accuracy
+    assert np.allclose(e_ref.double().numpy(), e_or, rtol=1e-4, atol=0)
+    # planted: a last-wins tie rule (<=) changes the zero tile's choice
+    best = np.zeros(e_or.shape[1], dtype=np.int64)
+    for i in (1, 2):
+        best = np.where(e_or[i] <= e_or[best, np.arange(e_or.shape[1])], i, best)
+    assert best[0] == 2
