@@ -359,17 +359,7 @@ def qwen_measure(args, device):
             for name, _, k in groups:
                 x = torch.randn((args.prefill_tokens, k), generator=gx).to(torch.bfloat16).to(device)
                 lin = mods[name]
-                lin(x)
-                torch.cuda.synchronize()
-                times = []
-                for _ in range(3):
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    lin(x)
-                    e1.record()
-                    torch.cuda.synchronize()
-                    times.append(e0.elapsed_time(e1))
-                pre[name] = st.median(times)
+                pre[name] = steady_ms(lambda: lin(x))
                 pops += 2 * args.prefill_tokens * lin.M_orig * lin.K_orig
                 del x
             pms = sum(pre.values())
@@ -383,6 +373,35 @@ def qwen_measure(args, device):
     out["data"] = ("random-init weights with 3% of input-column and output-row 64-blocks scaled (x4, x3) and the "
                    "top-k per-tile sum|W| mask; decode activations N(0,1) at 4 tokens")
     return out
+
+
+PREFILL_REPS = 10
+PREFILL_WARM_MS = 50.0
+
+
+def steady_ms(fn):
+    """Median of PREFILL_REPS timed calls of fn (HIP events, synchronised each
+    call) after at least PREFILL_WARM_MS of untimed calls: the compute clock
+    has ramped up by then, whatever ran before (host-side packing leaves the
+    GPU idle, decode work is memory-bound)."""
+    import time
+    import torch
+
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= PREFILL_WARM_MS:
+            break
+    times = []
+    for _ in range(PREFILL_REPS):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return statistics.median(times)
 
 
 def prefill_measure(args, device, keep_dir=None):
@@ -416,20 +435,7 @@ def prefill_measure(args, device, keep_dir=None):
     xs = {name: torch.randn((args.prefill_tokens, k), generator=g).to(torch.bfloat16).to(device)
           for name, _, k in GROUPS}
     mods = layers[0]
-    for name, _, _ in GROUPS:
-        mods[name](xs[name])
-    torch.cuda.synchronize()
-    per = {}
-    for name, _, _ in GROUPS:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        times = []
-        for _ in range(5):
-            e0.record()
-            mods[name](xs[name])
-            e1.record()
-            torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1))
-        per[name] = statistics.median(times)
+    per = {name: steady_ms(lambda name=name: mods[name](xs[name])) for name, _, _ in GROUPS}
     total_ms = sum(per.values())
     return {"tokens": args.prefill_tokens, "keep": args.prefill_keep if keep_dir is None else f"released {keep_dir.name}",
             "max_bf16_tiles_per_row_tile": info["max_bf16_per_row"], "layer_ms": total_ms,
@@ -437,7 +443,7 @@ def prefill_measure(args, device, keep_dir=None):
             "frac_int8_peak": info["ops"] / (total_ms / 1e3) / 1e12 / INT8_PEAK_TOPS,
             "group_ms": per, "ops_per_layer": info["ops"], "bf16_tiles": info["t16"],
             "note": "MixedLinear forward per group (scales over all rows, then one quantize + one "
-                    "GEMM), HIP events, median of 5"}
+                    f"GEMM), HIP events, median of {PREFILL_REPS} after {PREFILL_WARM_MS:.0f} ms of warm-up calls"}
 
 
 LLAMA32_3B = dict(vocab_size=128256, hidden_size=HIDDEN, intermediate_size=MLP, num_hidden_layers=LAYERS,

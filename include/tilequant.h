@@ -163,12 +163,12 @@ int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_stride_n, co
 
 /* Host function: the prefill work plan of one packed weight, from HOST copies
  * of its row pointers and INT8 tile ids (fp16_row_ptr may be NULL).  Writes
- * units (row tile | 1 << 30 for a single row tile, else a row-tile pair) into
- * units[0 .. max_units), max_units >= n_tr, and the count of units to
- * dispatch first into *n_first.  Returns the unit count, 0 when the plain pair
- * order is balanced (no plan needed), or TQ_ERR_ARG.  Pairs whose 16-bit tiles
- * make them cost well above the median pair are split into their two row
- * tiles; units costing more than the median go first, heaviest first. */
+ * units (row tile | 1 << 30 for a single row tile, else a row-tile pair), in
+ * row order, into units[0 .. max_units), max_units >= n_tr, and 0 into
+ * *n_first.  Returns the unit count, 0 when no pair needs splitting (the plain
+ * pair order is the plan), or TQ_ERR_ARG.  A pair whose 16-bit tiles make it
+ * cost well above the median pair is split into its two row tiles when that
+ * shortens it (its workgroups would otherwise finish long after the rest). */
 int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* int8_tile_ids,
                          const int32_t* fp16_row_ptr, int n_tr, int n_tc, int32_t* units, int max_units,
                          int* n_first);

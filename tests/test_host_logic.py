@@ -302,21 +302,22 @@ def _covered_rows(units, n_tr):
     return sorted(rows)
 
 
-def test_prefill_plan_splits_and_front_loads_the_released_heavy_row():
+def test_prefill_plan_splits_the_released_heavy_row():
     """Released keep05 map, layer 7 down_proj: row tile 47 holds 127 of its
     128 tiles in 16 bits.  The plan (host code in the library) splits its pair
-    into single row tiles and dispatches row 47 among the first units, which
-    are ordered heaviest first; every row tile is covered exactly once; uniform
-    maps need no plan."""
+    into single row tiles and leaves the balanced pairs alone, in row order;
+    every row tile is covered exactly once; uniform maps need no plan."""
     ids, (n_tr, n_tc) = mask_io.load_fp16_keep_ids_for_layer(GOLDEN / "llama32_3b_gi_keep05",
                                                               "model.layers.7.mlp.down_proj")
     plan = _plan_from_ids16(ids.numpy(), n_tr, n_tc)
     units = plan.units.tolist()
-    assert 47 | 1 << 30 in units[:plan.n_first] and 46 | 1 << 30 in units
-    assert 1 <= plan.n_first < len(units)
+    i = units.index(46 | 1 << 30)
+    assert units[i + 1] == 47 | 1 << 30 and plan.n_first == 0
+    rows = [u & ((1 << 30) - 1) for u in units]
+    assert rows == sorted(rows)
     counts = np.bincount(ids.numpy() // n_tc, minlength=n_tr)
-    first = [u & ((1 << 30) - 1) for u in units[:plan.n_first]]
-    assert all(counts[r] + (0 if units[i] >> 30 else counts[r + 1]) >= 20 for i, r in enumerate(first))
+    split = [u & ((1 << 30) - 1) for u in units if u >> 30]
+    assert all(max(counts[r], counts[r ^ 1]) >= 20 for r in split)   # only 16-bit-heavy pairs split
     assert _covered_rows(units, n_tr) == list(range(n_tr))
     assert _plan_from_ids16(uniform_fp16_ids(48, 128, 0.05, seed=3), 48, 128) is None
 

@@ -2272,16 +2272,18 @@ extern "C" int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_s
 }
 
 // Prefill work plan (host code).  Cost of a unit in ring steps of a pair's
-// INT8 step: a fixed part for set-up and epilogue, an INT8 step per column
-// where a row of the unit has an INT8 tile (cheaper with one row: half the
-// MFMAs and epilogue), and two half steps per 16-bit tile.  Weights measured
-// on MI355X at 8192 tokens, K = 8192: single-row INT8 step 0.68, 16-bit half
-// step 0.63 of a pair's INT8 step.
+// INT8 step: a fixed part for set-up and epilogue, one step per column where
+// a row of the unit has an INT8 tile (a step that multiplies only one row
+// costs 0.68: half the MFMAs and epilogue), and two half steps of 0.63 per
+// 16-bit tile (weights measured on MI355X at 8192 tokens, K = 8192).  A pair
+// far above the median pair (a row tile mostly in 16 bits) is split into its
+// two row tiles when that shortens it: its workgroups would otherwise finish
+// long after the rest.  Units stay in row order: dispatching the heavy units
+// first measured no faster than splitting alone.
 namespace {
-constexpr double kCostFixed = 8.0, kCostInt8Pair = 1.0, kCostInt8Single = 0.7, kCost16Half = 0.65;
+constexpr double kCostFixed = 8.0, kCostInt8Pair = 1.0, kCostInt8Single = 0.68, kCost16Half = 0.63;
 constexpr double kSplitAbove = 1.5;   // split pairs costing more than this x the median pair ...
 constexpr double kSplitGain = 0.9;    // ... when each single row costs less than this x the pair
-constexpr double kFirstAbove = 1.15;  // units costing more than this x the median pair go first
 }
 
 extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* int8_tile_ids,
@@ -2291,13 +2293,12 @@ extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* 
       max_units < n_tr || n_tr >= kUnitSingle)
     return TQ_ERR_ARG;
   if (int8_row_ptr[n_tr] > 0 && int8_tile_ids == nullptr) return TQ_ERR_ARG;
-  std::vector<uint8_t> has8((size_t)n_tc);
-  struct Unit { int w; double cost; };
-  std::vector<Unit> pairs, singles;
+  std::vector<uint8_t> rows8((size_t)n_tc);   // bit j: row r + j has an INT8 tile in this column
+  std::vector<double> pair_cost, single_cost;
   for (int r = 0; r < n_tr; r += 2) {
     const int rows = r + 1 < n_tr ? 2 : 1;
-    int n8[2] = {0, 0}, n16[2] = {0, 0}, n8u = 0;
-    std::fill(has8.begin(), has8.end(), 0);
+    int n8[2] = {0, 0}, n16[2] = {0, 0};
+    std::fill(rows8.begin(), rows8.end(), 0);
     for (int j = 0; j < rows; ++j) {
       const int rr = r + j;
       const int lo = int8_row_ptr[rr], hi = int8_row_ptr[rr + 1];
@@ -2305,8 +2306,7 @@ extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* 
       for (int q = lo; q < hi; ++q) {
         const int64_t c = (int64_t)int8_tile_ids[q] - (int64_t)rr * n_tc;
         if (c < 0 || c >= n_tc) return TQ_ERR_ARG;
-        n8u += has8[c] == 0;
-        has8[c] = 1;
+        rows8[c] |= (uint8_t)(1 << j);
       }
       n8[j] = hi - lo;
       if (fp16_row_ptr != nullptr) {
@@ -2314,44 +2314,35 @@ extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* 
         if (n16[j] < 0) return TQ_ERR_ARG;
       }
     }
-    pairs.push_back({r, kCostFixed + kCostInt8Pair * n8u + 2 * kCost16Half * (n16[0] + n16[1])});
-    singles.push_back({r | kUnitSingle, kCostFixed + kCostInt8Single * n8[0] + 2 * kCost16Half * n16[0]});
-    singles.push_back({(r + 1) | kUnitSingle,
-                       rows == 2 ? kCostFixed + kCostInt8Single * n8[1] + 2 * kCost16Half * n16[1] : 0.0});
+    int both = 0, one = 0;
+    for (int c = 0; c < n_tc; ++c) {
+      both += rows8[c] == 3;
+      one += rows8[c] == 1 || rows8[c] == 2;
+    }
+    pair_cost.push_back(kCostFixed + kCostInt8Pair * both + kCostInt8Single * one +
+                        2 * kCost16Half * (n16[0] + n16[1]));
+    for (int j = 0; j < 2; ++j)
+      single_cost.push_back(kCostFixed + kCostInt8Single * n8[j] + 2 * kCost16Half * n16[j]);
   }
-  std::vector<double> sorted;
-  for (const Unit& u : pairs) sorted.push_back(u.cost);
+  std::vector<double> sorted(pair_cost);
   std::sort(sorted.begin(), sorted.end());
   const double median = sorted[sorted.size() / 2];
-  std::vector<Unit> plan;
-  bool any = false;
-  for (size_t i = 0; i < pairs.size(); ++i) {
-    const Unit& pu = pairs[i];
-    const Unit& a0 = singles[2 * i];
-    const Unit& a1 = singles[2 * i + 1];
-    const bool two = (pu.w + 1) < n_tr;
-    if (two && pu.cost > kSplitAbove * median && std::max(a0.cost, a1.cost) < kSplitGain * pu.cost) {
-      plan.push_back(a0);
-      plan.push_back(a1);
-      any = true;
+  int n = 0;
+  bool split_any = false;
+  for (size_t i = 0; i < pair_cost.size(); ++i) {
+    const int r = (int)(2 * i);
+    const bool two = r + 1 < n_tr;
+    if (two && pair_cost[i] > kSplitAbove * median &&
+        std::max(single_cost[2 * i], single_cost[2 * i + 1]) < kSplitGain * pair_cost[i]) {
+      units[n++] = r | kUnitSingle;
+      units[n++] = (r + 1) | kUnitSingle;
+      split_any = true;
     } else {
-      plan.push_back(pu);
-      any |= pu.cost > kFirstAbove * median;
+      units[n++] = r;
     }
   }
-  if (!any) return 0;   // balanced: the plain pair order is the plan
-  std::stable_sort(plan.begin(), plan.end(), [&](const Unit& x, const Unit& y) {
-    const bool fx = x.cost > kFirstAbove * median, fy = y.cost > kFirstAbove * median;
-    if (fx != fy) return fx;
-    return fx && x.cost > y.cost;   // heavy units by cost, the rest in row order
-  });
-  int nf = 0;
-  for (size_t i = 0; i < plan.size(); ++i) {
-    units[i] = plan[i].w;
-    nf += plan[i].cost > kFirstAbove * median;
-  }
-  *n_first = nf;
-  return (int)plan.size();
+  *n_first = 0;
+  return split_any ? n : 0;   // 0: the plain pair order is the plan
 }
 
 extern "C" int tq_linear_mixed_fused_max_tokens(int k) {

@@ -70,9 +70,10 @@ def _workspace(device, n, M, n_tr, n_tc, split_k):
 
 class PrefillPlan:
     """Work plan for the prefill GEMM over one packed weight: ``units`` (a
-    device int32 tensor) lists row-tile pairs and single row tiles, the
-    ``n_first`` units carrying the most 16-bit tiles first.  Built on the host
-    from the row pointers (``prefill_plan``); the outputs do not depend on it."""
+    device int32 tensor) lists row-tile pairs and single row tiles (value
+    row | 1 << 30), in dispatch order; the first ``n_first`` units take all
+    their token blocks before the others start.  ``prefill_plan`` builds one
+    from the row pointers; the outputs do not depend on it."""
 
     __slots__ = ("units", "n_first")
 
@@ -84,8 +85,8 @@ def prefill_plan(*, int8_tile_ids: torch.Tensor, int8_row_ptr: torch.Tensor, fp1
                  n_tr: int, n_tc: int, device=None) -> Optional[PrefillPlan]:
     """Plan the prefill GEMM's work units from the pack's tile bookkeeping:
     row-tile pairs whose many 16-bit tiles would make them finish long after
-    the others are split into single row tiles, and the heaviest units are
-    dispatched first.  Returns None when the plain pair order is balanced.
+    the others are split into single row tiles (row order kept).  Returns
+    None when no pair needs splitting.
     Copies the row pointers and INT8 ids to the host (a synchronisation):
     call it once per weight, outside graph capture."""
     n_tr, n_tc = int(n_tr), int(n_tc)

@@ -51,7 +51,7 @@ from .quant_utils import (
 
 DEFAULT_ACTIVATION_ROW_CHUNK_SIZE = 16384
 # Above this many rows the GEMM runs its prefill kernel, which takes a work
-# plan (row-tile units ordered by their 16-bit load; see _prefill_plan).
+# plan (16-bit-heavy row-tile pairs split into single row tiles; _prefill_plan).
 PLAN_MIN_ROWS = 64
 # Rows up to which cfg.fused_decode = "auto" fuses quantization into the GEMM
 # (measured on MI355X: 1 row saves ~2 us per projection, 4 rows break even).
