@@ -646,3 +646,37 @@ def test_mixed_linear_builds_and_uses_the_prefill_plan():
     xq, sx = quantize_activation_tile_absmax(x)
     assert torch.equal(y, _gemm(pack, x, xq, sx))
     assert lin(x[:4]).shape == (4, 640)   # decode sizes run without it
+
+
+def test_prefill_plan_fp16_bias_and_ragged_rows():
+    """A planned prefill launch on fp16 weights with a bias and M = 1000 (a
+    ragged last row tile, odd row-tile count) through MixedLinear: bitwise
+    equal to the plain launch, and within tolerance of the oracle."""
+    from tilequant_amd.mixed_linear import MixedLinear
+
+    m, k, n = 1000, 2048, 700
+    n_tr, n_tc = -(-m // 64), k // 64
+    rng = np.random.default_rng(5)
+    mask = rng.random((n_tr, n_tc)) < 0.03
+    mask[6] = True                        # one row tile entirely 16-bit
+    mask[15, : n_tc // 2] = True          # the last (ragged, unpaired) row tile half 16-bit
+    ids16 = np.flatnonzero(mask.ravel()).astype(np.int64)
+    W = make_w(m, k, seed=9, dtype=torch.float16)
+    pack = pack_weight_from_tile_ids(W, n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(complement(ids16, n_tr * n_tc)),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=SimpleNamespace(quant_style="gi", dtype_out="fp16"),
+                                     tile_layout="mfma")
+    bias = (torch.randn(m, generator=torch.Generator().manual_seed(10)) * 0.1).to(torch.float16)
+    lin = MixedLinear(pack, bias.cuda(), SimpleNamespace(quant_style="gi", dtype_out="fp16"))
+    x = make_x(n, k, seed=11, dtype=torch.float16)
+    xd = x.cuda()
+    y = lin(xd)
+    plan = lin._plan[0]
+    assert plan is not None and any(u >> 30 for u in plan.units.cpu().tolist())
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y_plain = _gemm(pack, xd, xq, sx, bias=bias.cuda(), out_dtype=torch.float16)
+    assert torch.equal(y.view(torch.int16), y_plain.view(torch.int16))
+    op = _oracle_pack_any(W, ids16)
+    xq_ref, sx_ref = nm.act_quant(values(x), False)
+    rows = np.unique(np.r_[0:3, n - 3:n])
+    acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
+    assert_gemm_close(y[rows], acc, sab, pack.n_tc, bias=bias.float().numpy())
