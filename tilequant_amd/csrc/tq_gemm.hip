@@ -1775,33 +1775,40 @@ gemm_prefill_v5_kernel(GemmArgs a) {
         const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc0)));
         const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));
         v4i ax[4], bw[8];
+        // operand reads in the order the MFMAs use them -- row 0's weights, the
+        // four token blocks, row 1's weights -- each MFMA group waiting only
+        // for its own reads (LDS reads complete in order)
         asm volatile(
-            "ds_read_b128 %0, %4\n\t"
-            "ds_read_b128 %1, %4 offset:1024\n\t"
-            "ds_read_b128 %2, %4 offset:2048\n\t"
-            "ds_read_b128 %3, %4 offset:3072\n\t"
-            : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
-            : "v"(x_rd + so)
-            : "memory");
-        asm volatile(
-            "ds_read_b128 %0, %8\n\t"
-            "ds_read_b128 %1, %8 offset:1024\n\t"
-            "ds_read_b128 %2, %8 offset:2048\n\t"
-            "ds_read_b128 %3, %8 offset:3072\n\t"
-            "ds_read_b128 %4, %8 offset:4096\n\t"
-            "ds_read_b128 %5, %8 offset:5120\n\t"
-            "ds_read_b128 %6, %8 offset:6144\n\t"
-            "ds_read_b128 %7, %8 offset:7168\n\t"
-            "s_waitcnt lgkmcnt(0)"
+            "ds_read_b128 %0, %12\n\t"
+            "ds_read_b128 %1, %12 offset:1024\n\t"
+            "ds_read_b128 %2, %12 offset:2048\n\t"
+            "ds_read_b128 %3, %12 offset:3072\n\t"
+            "ds_read_b128 %4, %13\n\t"
+            "ds_read_b128 %5, %13 offset:1024\n\t"
+            "ds_read_b128 %6, %13 offset:2048\n\t"
+            "ds_read_b128 %7, %13 offset:3072\n\t"
+            "ds_read_b128 %8, %12 offset:4096\n\t"
+            "ds_read_b128 %9, %12 offset:5120\n\t"
+            "ds_read_b128 %10, %12 offset:6144\n\t"
+            "ds_read_b128 %11, %12 offset:7168\n\t"
             : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+              "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3]),
               "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
-            : "v"(w_rd + so)
+            : "v"(w_rd + so), "v"(x_rd + so)
             : "memory");
+        // wait for the reads up to token block tb (row 0) -- outstanding <= 7 - tb
+        auto wait_tb = [&](int tb) {
+          if (tb == 0) asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]), "+v"(ax[0]) :: "memory");
+          else if (tb == 1) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ax[1]) :: "memory");
+          else if (tb == 2) asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(ax[2]) :: "memory");
+          else asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ax[3]) :: "memory");
+        };
         // one row tile's 16 MFMAs (+ epilogue), with a load part issued after the first 8
-        auto row_mfma = [&](auto j_tag, float sc, int part) {
+        auto row_mfma = [&](auto j_tag, float sc, int part, bool first) {
           constexpr int J = decltype(j_tag)::value;
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
+            if (first) wait_tb(tb);
             if (tb == 2) {
               __builtin_amdgcn_sched_barrier(0);
               issue_part(sn, dst, dmeta, part);
@@ -1815,9 +1822,13 @@ gemm_prefill_v5_kernel(GemmArgs a) {
             }
           }
         };
-        if (h0) row_mfma(std::integral_constant<int, 0>{}, s0, 1);
+        if (h0) row_mfma(std::integral_constant<int, 0>{}, s0, 1, true);
         else issue_part(sn, dst, dmeta, 1);
-        if (h1) row_mfma(std::integral_constant<int, 4>{}, s1, 2);
+        // everything else (row 1's weights; row 0's operands when row 0 took no MFMAs)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(bw[4]), "+v"(bw[5]), "+v"(bw[6]), "+v"(bw[7]), "+v"(ax[0]), "+v"(ax[1]), "+v"(ax[2]),
+                       "+v"(ax[3]) :: "memory");
+        if (h1) row_mfma(std::integral_constant<int, 4>{}, s1, 2, false);
         else issue_part(sn, dst, dmeta, 2);
       } else {
         v4i ax[4], bw[4];
@@ -1830,18 +1841,22 @@ gemm_prefill_v5_kernel(GemmArgs a) {
             "ds_read_b128 %5, %9 offset:1024\n\t"
             "ds_read_b128 %6, %9 offset:2048\n\t"
             "ds_read_b128 %7, %9 offset:3072\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3]),
-              "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3])
-            : "v"(x_rd + so), "v"(w_rd + so)
+            : "=&v"(bw[0]), "=&v"(bw[1]), "=&v"(bw[2]), "=&v"(bw[3]),
+              "=&v"(ax[0]), "=&v"(ax[1]), "=&v"(ax[2]), "=&v"(ax[3])
+            : "v"(w_rd + so), "v"(x_rd + so)
             : "memory");
         constexpr int J = MODE == 2 ? 4 : 0;   // the row's accumulators
         issue_part(sn, dst, dmeta, 1);
         issue_part(sn, dst, dmeta, 2);
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
+        for (int tb = 0; tb < 4; ++tb) {
+          if (tb == 0) asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]), "+v"(ax[0]) :: "memory");
+          else if (tb == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ax[1]) :: "memory");
+          else if (tb == 2) asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(ax[2]) :: "memory");
+          else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ax[3]) :: "memory");
 #pragma unroll
           for (int jb = 0; jb < 4; ++jb) acc[tb][J + jb] = mfma16<XT>(ax[tb], bw[jb], acc[tb][J + jb]);
+        }
       }
     };
     // list16 holds row r0's 16-bit tiles before row r0 + 1's: three loops, one accumulator set each
