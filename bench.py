@@ -76,6 +76,8 @@ def parse():
     ap.add_argument("--released-maps", type=int, default=1,
                     help="also measure decode and prefill with the released Llama-3.2-3B gi tile maps; 0 = skip")
     ap.add_argument("--released-only", action="store_true", help="run only the released-maps section")
+    ap.add_argument("--m-sweep", type=int, default=1,
+                    help="also time the decode linear set at 1, 16 and 64 tokens (BASELINE configs[1]); 0 = skip")
     ap.add_argument("--e2e-batch", type=int, default=4)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-output", type=int, default=256)
@@ -402,6 +404,72 @@ def steady_ms(fn):
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1))
     return statistics.median(times)
+
+
+def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
+    """BASELINE configs[1] at the other token counts it names (M in {1, 4, 16,
+    64}; 4 is the headline): the same 28-layer linear set, quantize + GEMM per
+    projection in one HIP graph per step, and the GEMM launches alone in a
+    graph for the per-launch average (HBM fraction on packed weight bytes)."""
+    import torch
+    from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    s = torch.cuda.Stream()
+
+    def graph_ms(fn, reps):
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    n_launch = len(layers) * len(GROUPS)
+    for m in token_counts:
+        a2 = argparse.Namespace(**vars(args))
+        a2.tokens = m
+        xs = make_inputs(a2, device)
+        step_ms = graph_ms(lambda: [mods[name](xs[name]) for mods in layers for name, _, _ in GROUPS], 10)
+        quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in GROUPS}
+        outs = [torch.empty((m, mods[name].M_orig), device=device, dtype=torch.bfloat16)
+                for mods in layers for name, _, _ in GROUPS]
+
+        def gemms():
+            i = 0
+            for mods in layers:
+                for name, _, _ in GROUPS:
+                    lin, (xq, sx) = mods[name], quant[name]
+                    gemm_mixed_rows_splitk(x_fp=xs[name], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                           int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                           int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                           fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
+                                           M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
+                                           out_dtype=torch.bfloat16, out=outs[i], tile_layout=lin.tile_layout)
+                    i += 1
+
+        gemm_ms = graph_ms(gemms, 10)
+        launch_us = gemm_ms * 1e3 / n_launch
+        ops = info["ops"] / args.tokens * m   # 2 M K per token over the set
+        out[str(m)] = {"ms_per_step": step_ms, "tops": ops / (step_ms / 1e3) / 1e12,
+                       "gbps_packed_weights": info["packed_bytes"] / (step_ms / 1e3) / 1e9,
+                       "hbm_frac_step": info["packed_bytes"] / (step_ms / 1e3) / 1e9 / HBM_PEAK_GBPS,
+                       "gemm_avg_launch_us": launch_us,
+                       "gemm_hbm_frac": info["packed_bytes"] / n_launch / (launch_us / 1e6) / 1e9 / HBM_PEAK_GBPS}
+        del quant, outs, xs
+    return out
 
 
 def prefill_measure(args, device, keep_dir=None):
@@ -1029,6 +1097,7 @@ def main():
         del ws
 
     cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
+    m_sweep = decode_m_sweep(args, device, layers, info) if args.m_sweep else None
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
     torch.cuda.empty_cache()
@@ -1069,6 +1138,7 @@ def main():
                                "step's 112 GEMM launches back to back (activations quantized beforehand); "
                                "per-launch average includes the inter-kernel gaps"},
         "dense_bf16": dense,
+        "decode_m_sweep": m_sweep,
         "prefill": prefill,
         "qwen": qwen,
         "released_maps": released,
