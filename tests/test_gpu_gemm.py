@@ -587,8 +587,8 @@ def _banded_case(m, k, heavy_rows, seed):
     return W, pack, ids16
 
 
-def _plan_of(units, n_first=0):
-    return PrefillPlan(torch.tensor(units, dtype=torch.int32, device="cuda"), n_first)
+def _plan_of(units, n_tr, n_first=0):
+    return PrefillPlan(torch.tensor(units, dtype=torch.int32, device="cuda"), n_first, n_tr)
 
 
 @pytest.mark.parametrize("n,m,k,heavy", [
@@ -616,9 +616,9 @@ def test_prefill_plans_change_nothing_but_the_order(n, m, k, heavy):
         first_rows = {r} if units[0] >> 30 or r + 1 >= n_tr else {r, r + 1}
         assert first_rows & set(heavy)   # a heavy row's unit goes first
     plans = [plan,
-             _plan_of([r | 1 << 30 for r in range(n_tr)]),                          # all single rows
-             _plan_of([r | 1 << 30 for r in reversed(range(n_tr))], n_first=3),      # reversed, three first
-             _plan_of(list(range(0, n_tr, 2))[::-1], n_first=1)]                     # pairs, reversed
+             _plan_of([r | 1 << 30 for r in range(n_tr)], n_tr),                          # all single rows
+             _plan_of([r | 1 << 30 for r in reversed(range(n_tr))], n_tr, n_first=3),      # reversed, three first
+             _plan_of(list(range(0, n_tr, 2))[::-1], n_tr, n_first=1)]                     # pairs, reversed
     for p in plans:
         out = torch.full_like(y, float("nan"))
         gemm_mixed_rows_splitk(
@@ -628,6 +628,13 @@ def test_prefill_plans_change_nothing_but_the_order(n, m, k, heavy):
             n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=torch.bfloat16, out=out, tile_layout=pack.tile_layout,
             prefill_plan=p)
         assert torch.equal(out.view(torch.int16), y.view(torch.int16))
+    with pytest.raises(ValueError, match="row tiles"):   # a plan for a smaller matrix would skip row tiles
+        gemm_mixed_rows_splitk(
+            x_fp=xd, x_int8=xq, sx=sx, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales,
+            int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles,
+            fp16_tile_ids=pack.fp16_tile_ids, fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig,
+            n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=torch.bfloat16, tile_layout=pack.tile_layout,
+            prefill_plan=_plan_of(list(range(0, n_tr - 2, 2)), n_tr - 2))
     op = oracle_pack(W, ids16)
     xq_ref, sx_ref = nm.act_quant(values(x))
     rows = np.unique(np.r_[0:3, n // 2, n - 3:n])

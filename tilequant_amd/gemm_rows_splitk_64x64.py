@@ -72,13 +72,15 @@ class PrefillPlan:
     """Work plan for the prefill GEMM over one packed weight: ``units`` (a
     device int32 tensor) lists row-tile pairs and single row tiles (value
     row | 1 << 30), in dispatch order; the first ``n_first`` units take all
-    their token blocks before the others start.  ``prefill_plan`` builds one
-    from the row pointers; the outputs do not depend on it."""
+    their token blocks before the others start; ``n_tr`` is the row-tile
+    count of the weight it covers (every row tile exactly once).
+    ``prefill_plan`` builds one from the row pointers; the outputs do not
+    depend on it, as long as it covers the weight's row tiles."""
 
-    __slots__ = ("units", "n_first")
+    __slots__ = ("units", "n_first", "n_tr")
 
-    def __init__(self, units: torch.Tensor, n_first: int):
-        self.units, self.n_first = units, int(n_first)
+    def __init__(self, units: torch.Tensor, n_first: int, n_tr: int):
+        self.units, self.n_first, self.n_tr = units, int(n_first), int(n_tr)
 
 
 def prefill_plan(*, int8_tile_ids: torch.Tensor, int8_row_ptr: torch.Tensor, fp16_row_ptr: torch.Tensor,
@@ -106,7 +108,7 @@ def prefill_plan(*, int8_tile_ids: torch.Tensor, int8_row_ptr: torch.Tensor, fp1
     if rc == 0:
         return None
     dev = device if device is not None else int8_row_ptr.device
-    return PrefillPlan(units[:rc].to(dev), n_first.value)
+    return PrefillPlan(units[:rc].to(dev), n_first.value, n_tr)
 
 
 def _check_tiles(name: str, t: torch.Tensor, dtype) -> None:
@@ -191,8 +193,9 @@ def gemm_mixed_rows_splitk(
         units = prefill_plan.units
         if units.device != x_fp.device or units.dtype != torch.int32 or not units.is_contiguous():
             raise ValueError("prefill_plan.units must be a contiguous int32 tensor on the input's device")
-        if not 0 < units.numel() <= n_tr or not 0 <= prefill_plan.n_first <= units.numel():
-            raise ValueError("prefill_plan does not fit this weight")
+        if (prefill_plan.n_tr != n_tr or not 0 < units.numel() <= n_tr
+                or not 0 <= prefill_plan.n_first <= units.numel()):
+            raise ValueError(f"prefill_plan covers {prefill_plan.n_tr} row tiles, the weight has {n_tr}")
         rc = nat.lib().tq_gemm_mixed_rows_planned(*args, nat.ptr(units), units.numel(), prefill_plan.n_first,
                                                   nat.stream_handle(x_fp.device))
         nat.check(rc, "tq_gemm_mixed_rows_planned")
