@@ -774,6 +774,25 @@ def cpu_baseline(args, layers, xs):
         torch.set_num_threads(torch_threads_before)
     t = statistics.median(times)
     reps = len(times)
+    # context: the same sample as dense bf16 torch.nn.functional.linear on the same CPU threads
+    dense_ms = None
+    try:
+        torch.set_num_threads(threads)
+        g = torch.Generator().manual_seed(args.seed + 21)
+        dense_w = [(w["x"], (torch.randn((w["M"], w["K"]), generator=g) * 0.02).to(torch.bfloat16)) for w in work]
+        for x, wd in dense_w:
+            torch.nn.functional.linear(x, wd)
+        dts = []
+        d_start = time.perf_counter()
+        while len(dts) < 3 or (time.perf_counter() - d_start < 3.0 and len(dts) < 20):
+            t0 = time.perf_counter()
+            for x, wd in dense_w:
+                torch.nn.functional.linear(x, wd)
+            dts.append(time.perf_counter() - t0)
+        dense_ms = statistics.median(dts) * 1e3
+        del dense_w
+    finally:
+        torch.set_num_threads(torch_threads_before)
     return {"value": ops / t / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": f"{min(args.cpu_layers, len(layers))} of {len(layers)} layers of the same linear set at "
                       f"{args.tokens} tokens: activation quantization with the reference's torch CPU ops "
@@ -782,7 +801,10 @@ def cpu_baseline(args, layers, xs):
             "ms_per_sample": t * 1e3,
             "quant_ms_per_sample": legs["quant_s"] / reps * 1e3, "gemm_ms_per_sample": legs["gemm_s"] / reps * 1e3,
             "host": {"cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch_threads,
-                     "omp_threads": onat.num_threads()}}
+                     "omp_threads": onat.num_threads()},
+            "dense_bf16_cpu": None if dense_ms is None else {
+                "ms_per_sample": dense_ms, "tops": ops / (dense_ms / 1e3) / 1e12,
+                "note": "context: torch.nn.functional.linear in bf16 on the same sample and threads"}}
 
 
 def released_maps_measure(args, device):
