@@ -595,7 +595,6 @@ def e2e_measure(args, device):
 
     def graph_request(dec):
         torch.cuda.synchronize()
-        e_start = energy_uj()
         t0 = time.perf_counter()
         dec.prefill(prompt)
         torch.cuda.synchronize()
@@ -603,15 +602,13 @@ def e2e_measure(args, device):
         dec.decode(O - 1)
         torch.cuda.synchronize()
         t2 = time.perf_counter()
-        e_end = energy_uj()
-        return t0, t1, t2, (None if e_start is None or e_end is None else e_end - e_start)
+        return t0, t1, t2
 
     @torch.inference_mode()
     def eager_request(model):
         # the reference's dense loop (benchmark_generation.py:74-88), fused SDPA backends only
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             torch.cuda.synchronize()
-            e_start = energy_uj()
             t0 = time.perf_counter()
             out = model(input_ids=prompt.to(device), use_cache=True, logits_to_keep=1)
             cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
@@ -622,23 +619,27 @@ def e2e_measure(args, device):
                 cur, cache = out.logits[:, -1:].argmax(-1), out.past_key_values
             torch.cuda.synchronize()
             t2 = time.perf_counter()
-            e_end = energy_uj()
-            return t0, t1, t2, (None if e_start is None or e_end is None else e_end - e_start)
+            return t0, t1, t2
 
-    def summarize(rows):
-        ttft = statistics.median((t1 - t0) * 1e3 for t0, t1, _, _ in rows)
-        tpot = statistics.median((t2 - t1) * 1e3 / max(O - 1, 1) for _, t1, t2, _ in rows)
-        tps = statistics.median(B * O / (t2 - t0) for t0, _, t2, _ in rows)
+    def summarize(rows, energy_total_uj):
+        ttft = statistics.median((t1 - t0) * 1e3 for t0, t1, _ in rows)
+        tpot = statistics.median((t2 - t1) * 1e3 / max(O - 1, 1) for _, t1, t2 in rows)
+        tps = statistics.median(B * O / (t2 - t0) for t0, _, t2 in rows)
         res = {"ttft_ms": ttft, "tpot_ms": tpot, "output_tok_s": tps, "requests": len(rows)}
-        if all(r[3] is not None for r in rows):
-            # J per 1K tokens = mJ per token (the reference's figure, benchmark_generation.py:148-155)
-            res["energy_j_per_1k_tokens"] = statistics.median(r[3] / 1e3 / (B * O) for r in rows)
+        if energy_total_uj is not None and energy_total_uj > 0:
+            # J per 1K tokens = mJ per token (the reference's figure, benchmark_generation.py:148-155),
+            # over all timed requests together: the counter updates too coarsely for one 0.5 s request
+            res["energy_j_per_1k_tokens"] = energy_total_uj / 1e3 / (B * O * len(rows))
         return res
 
     def run(fn, target):
         for _ in range(args.e2e_warmup):
             fn(target)
-        return summarize([fn(target) for _ in range(args.e2e_repeats)])
+        torch.cuda.synchronize()
+        e0 = energy_uj()
+        rows = [fn(target) for _ in range(args.e2e_repeats)]
+        e1 = energy_uj()
+        return summarize(rows, None if e0 is None or e1 is None else e1 - e0)
 
     res = {"batch": B, "prompt": P, "output": O, "keep": args.keep, "data": "random-init weights, seeded uniform "
            "prompt ids, seeded uniform tile maps"}
@@ -651,6 +652,7 @@ def e2e_measure(args, device):
     res["tilequant_graph"] = run(graph_request, dec)
     res["tilequant_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
     res["tilequant_graph"]["decode_step"] = "fused (9 launches per layer)" if dec._fused else "model forward"
+    res["tilequant_graph"]["prefill"] = "fused glue" if dec._fused_prefill else "model forward"
     dec.close()
     del dec
     if args.released_maps:
@@ -664,9 +666,9 @@ def e2e_measure(args, device):
         gc.collect()
         torch.cuda.empty_cache()
     if args.e2e_module_path:
-        # the reference's structure: the model's own modules replayed in the decode graph
+        # the reference's structure: the model's own modules replayed in the prefill and decode graphs
         dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device,
-                                             fused_decode=False)
+                                             fused_decode=False, fused_prefill=False)
         res["tilequant_graph_module_step"] = run(graph_request, dec)
         dec.close()
         del dec
@@ -682,11 +684,13 @@ def e2e_measure(args, device):
     res["dense_bf16_graph"]["peak_allocated_gib"] = torch.cuda.max_memory_allocated() / 2 ** 30
     res["dense_bf16_graph"]["decode_step"] = "fused glue, hipBLASLt GEMMs on stacked weights" if dec._fused \
         else "model forward"
+    res["dense_bf16_graph"]["prefill"] = "fused glue, hipBLASLt GEMMs on stacked weights" if dec._fused_prefill \
+        else "model forward"
     dec.close()
     del dec
     if args.e2e_module_path:
         dec = CudaGraphGreedyDecoder.prepare(dense, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=device,
-                                             fused_decode=False)
+                                             fused_decode=False, fused_prefill=False)
         res["dense_bf16_graph_module_step"] = run(graph_request, dec)
         dec.close()
         del dec

@@ -346,6 +346,30 @@ int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* cos, const vo
                   int64_t cache_stride_b, int64_t cache_stride_h, int64_t cache_stride_l, int dtype, int n,
                   int q_heads, int kv_heads, int head_dim, int max_len, void* stream);
 
+/* Prefill forms of the glue above, for the B x P rows of a prompt (one wave
+ * per row for the norm, elementwise grids otherwise; same element arithmetic
+ * as the decode forms).  They replace the modules' RMSNorm (input and
+ * post-attention), act_fn(gate) * up, apply_rotary_pos_emb and the static
+ * cache update inside the decoder's captured prefill
+ * (src/runtime/graph_decode.py:238-268 runs the model's forward there).
+ * tq_add_rmsnorm_rows: as tq_add_rmsnorm_quant without the codes, any n,
+ * k <= 8192 a multiple of 8, 16-byte aligned rows.
+ * tq_silu_mul_rows: as tq_silu_mul_quant without the codes, any n, inter a
+ * multiple of 8, 16-byte aligned rows.
+ * tq_rope_prefill: row b * prompt_len + p of qkv is token p of sequence b,
+ * rotated with row p of the cos / sin tables (row stride table_stride); q to
+ * q_out[b, h, p, :] (strides q_stride_b, q_stride_h, q_stride_p), k and v into
+ * the caches at index p (prompt_len <= max_len). */
+int tq_add_rmsnorm_rows(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                        const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out, int64_t y_stride,
+                        int dtype, int n, int k, void* stream);
+int tq_silu_mul_rows(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride, int dtype, int n,
+                     int inter, void* stream);
+int tq_rope_prefill(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin, int64_t table_stride,
+                    void* q_out, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_p, void* k_cache,
+                    void* v_cache, int64_t cache_stride_b, int64_t cache_stride_h, int64_t cache_stride_l, int dtype,
+                    int batch, int prompt_len, int q_heads, int kv_heads, int head_dim, int max_len, void* stream);
+
 /* Greedy decoding step on the device: next_token[b] = token[b] = argmax_v
  * logits[b, v] (torch.argmax order: NaN first, lowest index among equals),
  * generated[b, *position - prompt_len + 1] = that token (no write outside

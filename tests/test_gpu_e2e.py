@@ -289,6 +289,91 @@ def test_silu_mul_quant_matches_module_and_quantizer(n, inter):
     assert torch.equal(q, q_ref) and torch.equal(sx, sx_ref)
 
 
+@pytest.mark.parametrize("n,k,with_delta,dtype", [(1000, 3072, True, torch.bfloat16), (37, 3072, False, torch.bfloat16),
+                                                   (513, 5120, True, torch.bfloat16), (64, 8192, True, torch.float16),
+                                                   (8, 200, True, torch.bfloat16)])
+def test_add_rmsnorm_rows_matches_module(n, k, with_delta, dtype):
+    """Prefill form: h bitwise torch's add, y within 1 ulp of LlamaRMSNorm (sum-of-squares order only)."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    g = torch.Generator().manual_seed(n * 3 + k)
+    x = (torch.randn((n, k), generator=g) * 3).to(dtype).to(DEV)
+    d = (torch.randn((n, k), generator=g) * 2).to(dtype).to(DEV)
+    norm = LlamaRMSNorm(k, eps=1e-6).to(DEV).to(dtype)
+    norm.weight.data = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype).to(DEV)
+    h_ref = (x + d) if with_delta else x
+    with torch.inference_mode():
+        y_ref = norm(h_ref)
+    h = torch.full_like(x, 7.0)
+    y = torch.empty_like(x)
+    rc = nat.lib().tq_add_rmsnorm_rows(x.data_ptr(), k, d.data_ptr() if with_delta else None, k, norm.weight.data_ptr(),
+                                       1e-6, h.data_ptr() if with_delta else None, k, y.data_ptr(), k,
+                                       nat.dtype_code(dtype), n, k, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    if with_delta:
+        assert torch.equal(h, h_ref)
+    else:
+        assert bool((h == 7.0).all())                       # no h without a delta
+    # the fp32 sum of squares is ordered differently from torch's mean: where
+    # that moves h * rsqrt across a rounding boundary, round(h * r) moves one
+    # ulp and weight * it up to two; such elements are rare
+    assert _ulp_close(y, y_ref, 2.0)
+    assert float((y != y_ref).float().mean()) < 1e-3
+
+
+@pytest.mark.parametrize("n,inter,dtype", [(4096, 8192, torch.bfloat16), (333, 1024, torch.bfloat16),
+                                           (17, 136, torch.float16), (9, 192, torch.float16)])
+def test_silu_mul_rows_matches_module(n, inter, dtype):
+    g = torch.Generator().manual_seed(n + inter)
+    gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(dtype).to(DEV)
+    with torch.inference_mode():
+        y_ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+    y = torch.empty((n, inter), dtype=dtype, device=DEV)
+    rc = nat.lib().tq_silu_mul_rows(gu.data_ptr(), 2 * inter, y.data_ptr(), inter, nat.dtype_code(dtype), n, inter,
+                                    torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert _ulp_close(y, y_ref, 1.0)
+    # the decode form on the same rows gives the same values
+    if n <= 64 and inter % 64 == 0:
+        y2 = torch.empty_like(y)
+        rc = nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y2.data_ptr(), inter, None, inter, None,
+                                         nat.dtype_code(dtype), n, inter, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("B,P,hq,hkv,L", [(2, 37, 24, 8, 64), (1, 300, 8, 2, 300), (3, 5, 28, 4, 9)])
+def test_rope_prefill_matches_module_ops(B, P, hq, hkv, L):
+    """Every prompt position rotated with its own table row, bitwise the modules' RoPE;
+    k / v land at cache index p, nothing past P is written."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    D = 128
+    g = torch.Generator().manual_seed(B * 100 + P)
+    qkv = torch.randn((B * P, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(DEV)
+    ang = torch.randn((L, D), generator=g)
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    kc = torch.zeros((B, hkv, L, D), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty((B, hq, P, D), dtype=torch.bfloat16, device=DEV)
+    rc = nat.lib().tq_rope_prefill(qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                                   q_out.data_ptr(), q_out.stride(0), q_out.stride(1), q_out.stride(2), kc.data_ptr(),
+                                   vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), 0, B, P, hq, hkv, D, L,
+                                   torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    q = qkv[:, :hq * D].view(B, P, hq, D).transpose(1, 2)
+    k = qkv[:, hq * D:(hq + hkv) * D].view(B, P, hkv, D).transpose(1, 2)
+    v = qkv[:, (hq + hkv) * D:].view(B, P, hkv, D).transpose(1, 2)
+    q_ref, k_ref = apply_rotary_pos_emb(q, k, cos[:P].view(1, P, D), sin[:P].view(1, P, D))
+    torch.cuda.synchronize()
+    assert torch.equal(q_out, q_ref)
+    assert torch.equal(kc[:, :, :P], k_ref) and torch.equal(vc[:, :, :P], v)
+    assert int(kc[:, :, P:].abs().sum()) == 0 and int(vc[:, :, P:].abs().sum()) == 0
+
+
 def test_rope_cache_matches_module_ops():
     from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
@@ -512,3 +597,41 @@ def test_fused_decode_step_matches_module_forward(family):
         clear = (top2[:, 0] - top2[:, 1]) > 3e-2 * scale
         assert torch.equal(f.argmax(-1)[clear], r.argmax(-1)[clear]), t
     ref.close()
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen"])
+def test_fused_prefill_matches_module_prefill(family):
+    """The decoder's fused prompt forward against the model's own forward
+    (fused_prefill=False): last-token logits within bf16 rounding noise,
+    argmax equal where the margin is clear, the caches' prompt k/v close, and
+    the tokens decoded after either prefill agree where the margins are clear."""
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+
+    config = tiny_llama_config(layers=2) if family == "llama" else tiny_qwen2_config(layers=2)
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out="bf16"), DEV,
+                                               keep_frac=0.05, seed=41)
+    B, P, O = 3, 100, 6
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(42))
+    runs = {}
+    for fused in (True, False):
+        dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV,
+                                             fused_prefill=fused)
+        assert (dec._fused_prefill is not None) == fused
+        dec.prefill(prompt)
+        logits = dec.last_logits[:, -1].float().clone()
+        kv = [(l.keys[:, :, :P].float().clone(), l.values[:, :, :P].float().clone()) for l in dec.cache.layers]
+        assert all(int(l.cumulative_length) == P for l in dec.cache.layers)
+        replay = dec.prefill(prompt).clone()                 # the captured prefill replays the same
+        ids = dec.decode(O - 1).clone()
+        dec.close()
+        runs[fused] = (logits, kv, ids, replay)
+    (lf, kvf, idf, rf), (lm, kvm, idm, rm) = runs[True], runs[False]
+    scale = float(lm.abs().max())
+    assert float((lf - lm).abs().max()) <= 3e-2 * scale
+    top2 = lm.topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 3e-2 * scale
+    assert torch.equal(lf.argmax(-1)[clear], lm.argmax(-1)[clear])
+    for (kf, vf), (km, vm) in zip(kvf, kvm):
+        for a, b in ((kf, km), (vf, vm)):
+            assert float((a - b).abs().max()) <= 3e-2 * float(b.abs().max())
+    assert torch.equal(rf, idf[:, :1]) and torch.equal(rm, idm[:, :1])

@@ -77,6 +77,10 @@ _SIGNATURES = {
     "tq_add_rmsnorm_quant": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _p, _i64, _p,
                                   _i, _i, _i, _p]),
     "tq_silu_mul_quant": (_i, [_p, _i64, _p, _i64, _p, _i64, _p, _i, _i, _i, _p]),
+    "tq_add_rmsnorm_rows": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _i, _i, _i, _p]),
+    "tq_silu_mul_rows": (_i, [_p, _i64, _p, _i64, _i, _i, _i, _p]),
+    "tq_rope_prefill": (_i, [_p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i, _i, _i,
+                             _i, _i, _i, _i, _p]),
     "tq_rope_cache": (_i, [_p, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i, _i, _i, _i, _i,
                            _i, _p]),
     "tq_pack_int8_tiles": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),

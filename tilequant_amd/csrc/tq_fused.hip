@@ -394,6 +394,144 @@ greedy_finish_kernel(const float* __restrict__ pv, const int* __restrict__ pi, i
   if (t == 0) position[0] = pos + 1;
 }
 
+// ---- prefill glue: the same arithmetic on thousands of rows ---------------
+//
+// At prefill (B x P rows) these are bandwidth-bound: one wave per row for the
+// norm (the row's sum of squares stays in the wave), elementwise grids for
+// SiLU * up and RoPE.
+
+// One wave per row: h = x + delta (rounded; h = x without delta), y = w *
+// round(h * rsqrt(mean(h^2) + eps)) -- add_rmsnorm_quant's element arithmetic
+// (only the fp32 order of the sum of squares differs).  CPL 16-byte chunks per
+// lane hold the row between the two passes (k <= 512 * CPL).
+template <class XT, int CPL>
+__global__ void __launch_bounds__(256)
+add_rmsnorm_rows_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6), nw = gridDim.x * 4;
+  const int cpr = a.k >> 3;   // 8-element chunks per row
+  const bool has_delta = a.delta != nullptr;
+  u32x4 wv[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = min(lane + 64 * i, cpr - 1);
+    wv[i] = *reinterpret_cast<const u32x4*>(a.w + ch * 8);
+  }
+  for (int row = gw; row < a.n; row += nw) {
+    const uint16_t* xr = a.x + (int64_t)row * a.ldx;
+    const uint16_t* dr = has_delta ? a.delta + (int64_t)row * a.ldd : xr;
+    u32x4 hv[CPL], dv[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = min(lane + 64 * i, cpr - 1);
+      hv[i] = *reinterpret_cast<const u32x4*>(xr + ch * 8);
+      dv[i] = *reinterpret_cast<const u32x4*>(dr + ch * 8);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const bool live = lane + 64 * i < cpr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t xw = hv[i][e], dw = dv[i][e];
+        if (has_delta)
+          hv[i][e] = XT::pack2(XT::to_f32((uint16_t)xw) + XT::to_f32((uint16_t)dw),
+                               XT::to_f32((uint16_t)(xw >> 16)) + XT::to_f32((uint16_t)(dw >> 16)));
+        if (live) ss = dot2sq<XT>(hv[i][e], ss);
+      }
+    }
+    ss = wave_sum(ss);
+    const float rinv = rsqrtf(ss / (float)a.k + a.eps);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = lane + 64 * i;
+      if (ch >= cpr) continue;
+      u32x4 yv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t h2 = hv[i][e], w2 = wv[i][e];
+        const float n0 = XT::round(XT::to_f32((uint16_t)h2) * rinv);           // hidden_states.to(input_dtype)
+        const float n1 = XT::round(XT::to_f32((uint16_t)(h2 >> 16)) * rinv);
+        yv[e] = XT::pack2(XT::to_f32((uint16_t)w2) * n0, XT::to_f32((uint16_t)(w2 >> 16)) * n1);   // weight * hidden
+      }
+      *reinterpret_cast<u32x4*>(a.y + (int64_t)row * a.ldy + ch * 8) = yv;
+      if (has_delta) *reinterpret_cast<u32x4*>(a.h + (int64_t)row * a.ldh + ch * 8) = hv[i];
+    }
+  }
+}
+
+// y = round(round(silu(gate)) * up) over [n, inter] from [n, 2 inter]: one
+// thread per 8 columns of one row.
+template <class XT>
+__global__ void __launch_bounds__(256)
+silu_mul_rows_kernel(SiluArgs a) {
+  const int cpr = a.inter >> 3;
+  const int64_t total = (int64_t)a.n * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int row = (int)(i / cpr), ch = (int)(i - (int64_t)row * cpr);
+    const uint16_t* g = a.gu + (int64_t)row * a.ldg + ch * 8;
+    const u32x4 gv = *reinterpret_cast<const u32x4*>(g);
+    const u32x4 uv = *reinterpret_cast<const u32x4*>(g + a.inter);
+    u32x4 yv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float y2[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float gf = XT::to_f32((uint16_t)(gv[e] >> (16 * hh)));
+        const float uf = XT::to_f32((uint16_t)(uv[e] >> (16 * hh)));
+        const float sg = XT::round(gf / (1.0f + expf(-gf)));
+        y2[hh] = sg * uf;
+      }
+      yv[e] = XT::pack2(y2[0], y2[1]);
+    }
+    *reinterpret_cast<u32x4*>(a.y + (int64_t)row * a.ldy + ch * 8) = yv;
+  }
+}
+
+// RoPE of a prompt: rows n = b * P + p of the stacked q/k/v output, position
+// p; rotated q to q_out[b, j, p, :] (strides q_sb, q_sh, q_sp), rotated k and
+// v into the caches at index p.  cos / sin: [>= P, 128] tables.  Workgroup
+// (row, group of 4 heads), lane d of wave w rotates the pair (d, d + 64) of
+// head 4 * blockIdx.y + w, with rope_cache_kernel's roundings.
+struct RopePrefillArgs {
+  const uint16_t* qkv;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t ldqkv, ldcs, q_sb, q_sh, q_sp, c_sb, c_sh, c_sl;
+  int P, hq, hkv;
+};
+
+template <class XT>
+__global__ void __launch_bounds__(256)
+rope_prefill_kernel(RopePrefillArgs a) {
+  const int row = blockIdx.x, j = blockIdx.y * 4 + (threadIdx.x >> 6), d = threadIdx.x & 63;
+  if (j >= a.hq + 2 * a.hkv) return;
+  const int b = row / a.P, p = row - b * a.P;
+  const uint16_t* src = a.qkv + (int64_t)row * a.ldqkv + (int64_t)j * 128;
+  const uint16_t rlo = src[d], rhi = src[d + 64];
+  if (j >= a.hq + a.hkv) {   // v head: copy into the cache
+    uint16_t* dst = a.v_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq - a.hkv) * a.c_sh + (int64_t)p * a.c_sl;
+    dst[d] = rlo;
+    dst[d + 64] = rhi;
+    return;
+  }
+  const uint16_t* cr = a.cos + (int64_t)p * a.ldcs;
+  const uint16_t* sr = a.sin + (int64_t)p * a.ldcs;
+  const float lo = XT::to_f32(rlo), hi = XT::to_f32(rhi);
+  const float c0 = XT::to_f32(cr[d]), c1 = XT::to_f32(cr[d + 64]);
+  const float s0 = XT::to_f32(sr[d]), s1 = XT::to_f32(sr[d + 64]);
+  const float o0 = XT::round(XT::round(lo * c0) + XT::round(-hi * s0));
+  const float o1 = XT::round(XT::round(hi * c1) + XT::round(lo * s1));
+  uint16_t* dst = (j < a.hq) ? a.q_out + (int64_t)b * a.q_sb + (int64_t)j * a.q_sh + (int64_t)p * a.q_sp
+                             : a.k_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq) * a.c_sh + (int64_t)p * a.c_sl;
+  dst[d] = XT::from_f32(o0);
+  dst[d + 64] = XT::from_f32(o1);
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace tq
@@ -470,6 +608,80 @@ extern "C" int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* co
   const dim3 grid(n, q_heads + 2 * kv_heads);
   if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(rope_cache_kernel<Bf16>, grid, dim3(64), 0, s, a);
   else hipLaunchKernelGGL(rope_cache_kernel<Fp16>, grid, dim3(64), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_add_rmsnorm_rows(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                                   const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out,
+                                   int64_t y_stride, int dtype, int n, int k, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (n < 0 || k < 0 || (k % 8) != 0 || k > 8192) return TQ_ERR_ARG;
+  if (n == 0 || k == 0) return TQ_OK;
+  if (!x || !weight || !y_out || (delta && !h_out)) return TQ_ERR_ARG;
+  if (x_stride < k || y_stride < k || (delta && (delta_stride < k || h_stride < k))) return TQ_ERR_ARG;
+  if (!al16(x) || !al16(weight) || !al16(y_out) || (x_stride % 8) || (y_stride % 8) ||
+      (delta && (!al16(delta) || !al16(h_out) || (delta_stride % 8) || (h_stride % 8))))
+    return TQ_ERR_ALIGN;
+  NormArgs a{};
+  a.x = static_cast<const uint16_t*>(x); a.delta = static_cast<const uint16_t*>(delta);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.h = static_cast<uint16_t*>(h_out); a.y = static_cast<uint16_t*>(y_out);
+  a.ldx = x_stride; a.ldd = delta_stride; a.ldh = h_stride; a.ldy = y_stride;
+  a.n = n; a.k = k; a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(std::min((n + 3) / 4, 2048)), block(256);
+  const bool wide = k > 4096;
+  if (dtype == TQ_DTYPE_BF16) {
+    if (wide) hipLaunchKernelGGL((add_rmsnorm_rows_kernel<Bf16, 16>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((add_rmsnorm_rows_kernel<Bf16, 8>), grid, block, 0, s, a);
+  } else {
+    if (wide) hipLaunchKernelGGL((add_rmsnorm_rows_kernel<Fp16, 16>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((add_rmsnorm_rows_kernel<Fp16, 8>), grid, block, 0, s, a);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_silu_mul_rows(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride, int dtype,
+                                int n, int inter, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (n < 0 || inter < 0 || (inter % 8) != 0) return TQ_ERR_ARG;
+  if (n == 0 || inter == 0) return TQ_OK;
+  if (!gate_up || !y_out || gu_stride < 2 * (int64_t)inter || y_stride < inter) return TQ_ERR_ARG;
+  if (!al16(gate_up) || !al16(y_out) || (gu_stride % 8) || (y_stride % 8)) return TQ_ERR_ALIGN;
+  SiluArgs a{};
+  a.gu = static_cast<const uint16_t*>(gate_up); a.y = static_cast<uint16_t*>(y_out);
+  a.ldg = gu_stride; a.ldy = y_stride; a.n = n; a.inter = inter;
+  const int64_t total = (int64_t)n * (inter / 8);
+  const dim3 grid((unsigned)std::min<int64_t>((total + 255) / 256, 8192)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(silu_mul_rows_kernel<Bf16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(silu_mul_rows_kernel<Fp16>, grid, block, 0, s, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_rope_prefill(const void* qkv, int64_t qkv_stride, const void* cos, const void* sin,
+                               int64_t table_stride, void* q_out, int64_t q_stride_b, int64_t q_stride_h,
+                               int64_t q_stride_p, void* k_cache, void* v_cache, int64_t cache_stride_b,
+                               int64_t cache_stride_h, int64_t cache_stride_l, int dtype, int batch, int prompt_len,
+                               int q_heads, int kv_heads, int head_dim, int max_len, void* stream) {
+  if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
+  if (head_dim != 128 || batch < 0 || prompt_len < 0 || q_heads <= 0 || kv_heads <= 0 || prompt_len > max_len ||
+      table_stride < 128)
+    return TQ_ERR_ARG;
+  if (batch == 0 || prompt_len == 0) return TQ_OK;
+  if ((int64_t)batch * prompt_len >= (1LL << 31) || qkv_stride < (int64_t)(q_heads + 2 * kv_heads) * 128) return TQ_ERR_ARG;
+  if (!qkv || !cos || !sin || !q_out || !k_cache || !v_cache) return TQ_ERR_ARG;
+  RopePrefillArgs a{};
+  a.qkv = static_cast<const uint16_t*>(qkv); a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin); a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_cache = static_cast<uint16_t*>(k_cache); a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.ldqkv = qkv_stride; a.ldcs = table_stride; a.q_sb = q_stride_b; a.q_sh = q_stride_h; a.q_sp = q_stride_p;
+  a.c_sb = cache_stride_b; a.c_sh = cache_stride_h; a.c_sl = cache_stride_l;
+  a.P = prompt_len; a.hq = q_heads; a.hkv = kv_heads;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(batch * prompt_len, (q_heads + 2 * kv_heads + 3) / 4);
+  if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(rope_prefill_kernel<Bf16>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(rope_prefill_kernel<Fp16>, grid, dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
 

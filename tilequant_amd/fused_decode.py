@@ -227,3 +227,109 @@ class FusedDecodeStep:
         self._norm(cur, delta, norm, self.h[k], self.final, None, None)
         logits = self.model.lm_head(self.final.view(B, 1, self.hidden))
         return logits
+
+
+class FusedPrefillStep:
+    """Prompt forward (``batch`` sequences of ``prompt_len`` tokens, positions
+    0 .. prompt_len - 1) for a bound model and static cache: what the model's
+    own forward computes at prefill, with the row-parallel forms of the glue
+    kernels -- ``tq_add_rmsnorm_rows`` for the residual adds and both
+    RMSNorms, ``tq_rope_prefill`` for RoPE and the cache writes,
+    ``tq_silu_mul_rows`` for SiLU(gate) * up -- around the model's own
+    projections (MixedLinear or stacked dense) and the decoder's causal SDPA.
+    The modules spend ~7 elementwise launches per RMSNorm and several more per
+    RoPE, SiLU and cache update over the 8192 x 3072 activations.  Returns the
+    logits of each sequence's last token [B, 1, V] (the ``logits_to_keep=1``
+    forward).  Element arithmetic follows the modules op by op; the fp32 sum
+    of squares of each RMSNorm is the only reordered reduction."""
+
+    def __init__(self, model: nn.Module, cache, batch: int, prompt_len: int, max_cache_len: int,
+                 device: torch.device, attention, layers: Optional[List["_Layer"]] = None,
+                 cos_table: Optional[torch.Tensor] = None, sin_table: Optional[torch.Tensor] = None) -> None:
+        cfg = model.config.get_text_config(decoder=True)
+        check_fused_architecture(cfg, model.model.layers[0].self_attn)
+        self.model, self.text, self.cache = model, model.model, cache
+        self.B, self.P, self.L = int(batch), int(prompt_len), int(max_cache_len)
+        if self.P > self.L:
+            raise ValueError("prompt longer than the cache")
+        self.device = device
+        self.attention = attention
+        self.hidden = int(cfg.hidden_size)
+        self.hq, self.hkv = int(cfg.num_attention_heads), int(cfg.num_key_value_heads)
+        self.head_dim = int(getattr(cfg, "head_dim", None) or self.hidden // self.hq)
+        if self.head_dim != 128:
+            raise ValueError("fused prefill serves head_dim 128")
+        if self.hidden % 8 or self.hidden > 8192:
+            raise ValueError("fused prefill serves hidden sizes <= 8192, multiples of 8")
+        self.inter = int(cfg.intermediate_size)
+        self.layers: List[_Layer] = layers if layers is not None else [_Layer(l) for l in self.text.layers]
+        self.dtype = self.text.embed_tokens.weight.dtype
+        self.code = nat.dtype_code(self.dtype)
+        self.scale = float(self.text.layers[0].self_attn.scaling)
+        N, H, dt, dev = self.B * self.P, self.hidden, self.dtype, device
+        e = lambda *s: torch.empty(s, device=dev, dtype=dt)   # noqa: E731
+        self.h = [e(N, H), e(N, H)]                          # residual stream, ping-pong
+        self.y = e(N, H)                                     # normed activations
+        self.q = e(self.B, self.hq, self.P, self.head_dim)   # rotated queries, SDPA layout
+        self.m = e(N, self.inter)                            # silu(gate) * up
+        self.h_last = e(self.B, H)
+        self.final = e(self.B, H)
+        if cos_table is None or sin_table is None:
+            with torch.inference_mode():
+                pos = torch.arange(self.P, device=dev).view(1, -1)
+                cos, sin = self.text.rotary_emb(torch.empty((1, 1, 1), device=dev, dtype=dt), pos)
+            cos_table = cos.reshape(self.P, self.head_dim).contiguous()
+            sin_table = sin.reshape(self.P, self.head_dim).contiguous()
+        self.cos_table, self.sin_table = cos_table, sin_table
+
+    def _norm(self, x, delta, ln, h_out, y_out, n) -> None:
+        rc = nat.lib().tq_add_rmsnorm_rows(
+            nat.ptr(x), x.stride(0), nat.ptr(delta), delta.stride(0) if delta is not None else 0,
+            nat.ptr(ln.weight), float(ln.variance_epsilon), nat.ptr(h_out), h_out.stride(0) if h_out is not None else 0,
+            nat.ptr(y_out), y_out.stride(0), self.code, n, self.hidden, nat.stream_handle(self.device))
+        nat.check(rc, "tq_add_rmsnorm_rows")
+
+    @staticmethod
+    def _project(lin: nn.Module, x: torch.Tensor) -> torch.Tensor:
+        return lin(x)
+
+    @torch.inference_mode()
+    def __call__(self, prompt: torch.Tensor) -> torch.Tensor:
+        """prompt [B, P] int64 -> logits [B, 1, V]; the cache holds the prompt's k/v afterwards."""
+        B, P, N, H = self.B, self.P, self.B * self.P, self.hidden
+        stream = nat.stream_handle(self.device)
+        layers = self.cache.layers
+        if not layers[0].is_initialized:
+            self.cache.early_initialization(B, self.hkv, self.head_dim, self.dtype, self.device)
+        x = self.text.embed_tokens(prompt).view(N, H)
+        cur, delta = x, None
+        k = 0
+        for li, ly in enumerate(self.layers):
+            h_new = self.h[k]
+            self._norm(cur, delta, ly.ln1, h_new if delta is not None else None, self.y, N)
+            resid = h_new if delta is not None else cur
+            qkv = self._project(ly.qkv, self.y)
+            kc, vc = layers[li].keys, layers[li].values
+            rc = nat.lib().tq_rope_prefill(
+                nat.ptr(qkv), qkv.stride(0), nat.ptr(self.cos_table), nat.ptr(self.sin_table),
+                self.cos_table.stride(0), nat.ptr(self.q), self.q.stride(0), self.q.stride(1), self.q.stride(2),
+                nat.ptr(kc), nat.ptr(vc), kc.stride(0), kc.stride(1), kc.stride(2), self.code, B, P, self.hq,
+                self.hkv, self.head_dim, kc.shape[2], stream)
+            nat.check(rc, "tq_rope_prefill")
+            layers[li].cumulative_length.add_(P)   # the cache's own bookkeeping, as its update() keeps it
+            attn = self.attention(self.q, kc[:, :, :P], vc[:, :, :P], self.scale)   # [B, P, Hq, D]
+            o = self._project(ly.o, attn.reshape(N, self.hq * self.head_dim))
+            k ^= 1
+            h2 = self.h[k]
+            self._norm(resid, o, ly.ln2, h2, self.y, N)
+            gu = self._project(ly.gate_up, self.y)
+            rc = nat.lib().tq_silu_mul_rows(nat.ptr(gu), gu.stride(0), nat.ptr(self.m), self.m.stride(0), self.code,
+                                            N, self.inter, stream)
+            nat.check(rc, "tq_silu_mul_rows")
+            d = self._project(ly.down, self.m)
+            cur, delta = h2, d
+            k ^= 1
+        # final norm on each sequence's last token only (the norm is per row)
+        last = lambda t: t.view(B, P, H)[:, P - 1]   # noqa: E731  [B, H], row stride P * H
+        self._norm(last(cur), last(delta), self.text.norm, self.h_last, self.final, B)
+        return self.model.lm_head(self.final.view(B, 1, H))

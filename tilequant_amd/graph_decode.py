@@ -24,6 +24,11 @@ ROCm specifics (this build's own design):
   Qwen2 layouts with head_dim 128 and up to 16 sequences; ``fused_decode=False``
   (or any other architecture) replays the model's own forward as the reference
   does.
+* The prompt forward of the same architectures runs ``FusedPrefillStep``: the
+  model's projections and this module's SDPA, with the residual adds,
+  RMSNorms, RoPE + cache writes and SiLU * up in row-parallel HIP kernels
+  instead of the modules' elementwise chains; ``fused_prefill=False`` runs the
+  model's forward.
 * Argmax, token feedback and the position counter stay on the device, as in
   the reference (graph_decode.py:347-385): no scalar leaves the GPU between
   replays.
@@ -123,7 +128,8 @@ class CudaGraphGreedyDecoder:
     prefill graph; ``decode`` replays the one-token graph."""
 
     def __init__(self, model: torch.nn.Module, *, prompt_tokens: int, max_new_tokens: int, batch_size: int = 1,
-                 device="cuda", prefill_only: bool = False, fused_decode: bool = True) -> None:
+                 device="cuda", prefill_only: bool = False, fused_decode: bool = True,
+                 fused_prefill: bool = True) -> None:
         if prompt_tokens < 1:
             raise ValueError("prompt_tokens must be positive")
         if batch_size < 1:
@@ -188,6 +194,24 @@ class CudaGraphGreedyDecoder:
                 self._fused = FusedDecodeStep(model, self.cache, self.batch_size, self.max_cache_len, self.device)
             except (ValueError, AttributeError):
                 self._fused = None
+        # The prompt forward from the row-parallel glue kernels where the
+        # architecture allows (tilequant_amd.fused_decode.FusedPrefillStep);
+        # otherwise the model's own forward.  It shares the decode step's
+        # stacked projections and RoPE tables.
+        self._fused_prefill = None
+        if fused_prefill:
+            from .fused_decode import FusedPrefillStep
+
+            try:
+                fd = self._fused
+                self._fused_prefill = FusedPrefillStep(
+                    model, self.cache, self.batch_size, self.prompt_tokens, self.max_cache_len, self.device,
+                    attention=lambda q, k, v, scale: _prefill_attention(self, q, k, v, 0.0, scale),
+                    layers=fd.layers if fd is not None else None,
+                    cos_table=fd.cos_table if fd is not None else None,
+                    sin_table=fd.sin_table if fd is not None else None)
+            except (ValueError, AttributeError):
+                self._fused_prefill = None
         self._prefill_graph: Optional[torch.cuda.CUDAGraph] = None
         self._graph: Optional[torch.cuda.CUDAGraph] = None
         self._prefill_logits: Optional[torch.Tensor] = None
@@ -229,10 +253,10 @@ class CudaGraphGreedyDecoder:
     @torch.inference_mode()
     def prepare(cls, model: torch.nn.Module, *, prompt_tokens: int = 128, max_new_tokens: int = 512,
                 batch_size: int = 1, device="cuda", prefill_only: bool = False,
-                fused_decode: bool = True) -> "CudaGraphGreedyDecoder":
+                fused_decode: bool = True, fused_prefill: bool = True) -> "CudaGraphGreedyDecoder":
         """Allocate, warm up and capture the prefill and decode graphs."""
         dec = cls(model, prompt_tokens=prompt_tokens, max_new_tokens=max_new_tokens, batch_size=batch_size,
-                  device=device, prefill_only=prefill_only, fused_decode=fused_decode)
+                  device=device, prefill_only=prefill_only, fused_decode=fused_decode, fused_prefill=fused_prefill)
         try:
             dec._capture()
         except BaseException:
@@ -277,12 +301,15 @@ class CudaGraphGreedyDecoder:
             self._generated.zero_()
             self._position.fill_(self.prompt_tokens)
             self._decode_seq_used.fill_(self.prompt_tokens + 1)   # valid length of the first decode step
-        out = self.model(input_ids=self._prompt, attention_mask=None, position_ids=self._prefill_positions.view(1, -1),
-                         past_key_values=self.cache, cache_position=self._prefill_positions, use_cache=True,
-                         logits_to_keep=1)
-        self._prefill_logits = out.logits
+        if self._fused_prefill is not None:
+            logits = self._fused_prefill(self._prompt)
+        else:
+            logits = self.model(input_ids=self._prompt, attention_mask=None,
+                                position_ids=self._prefill_positions.view(1, -1), past_key_values=self.cache,
+                                cache_position=self._prefill_positions, use_cache=True, logits_to_keep=1).logits
+        self._prefill_logits = logits
         if not self._prefill_only:
-            self._token.copy_(out.logits.argmax(dim=-1))
+            self._token.copy_(logits.argmax(dim=-1))
             self._generated[:, :1].copy_(self._token)
 
     @torch.inference_mode()
