@@ -359,7 +359,8 @@ int tq_rope_cache(const void* qkv, int64_t qkv_stride, const void* cos, const vo
  * tq_rope_prefill: row b * prompt_len + p of qkv is token p of sequence b,
  * rotated with row p of the cos / sin tables (row stride table_stride); q to
  * q_out[b, h, p, :] (strides q_stride_b, q_stride_h, q_stride_p), k and v into
- * the caches at index p (prompt_len <= max_len). */
+ * the caches at index p (prompt_len <= max_len); 16-byte aligned base pointers,
+ * every stride a multiple of 8 elements. */
 int tq_add_rmsnorm_rows(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
                         const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out, int64_t y_stride,
                         int dtype, int n, int k, void* stream);

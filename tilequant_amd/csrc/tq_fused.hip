@@ -491,9 +491,10 @@ silu_mul_rows_kernel(SiluArgs a) {
 
 // RoPE of a prompt: rows n = b * P + p of the stacked q/k/v output, position
 // p; rotated q to q_out[b, j, p, :] (strides q_sb, q_sh, q_sp), rotated k and
-// v into the caches at index p.  cos / sin: [>= P, 128] tables.  Workgroup
-// (row, group of 4 heads), lane d of wave w rotates the pair (d, d + 64) of
-// head 4 * blockIdx.y + w, with rope_cache_kernel's roundings.
+// v into the caches at index p.  cos / sin: [>= P, 128] tables.  One thread
+// per (row, head, 8-element chunk t of the low half): it rotates elements
+// 8t .. 8t + 7 with their partners 64 + 8t .. (16-byte loads and stores) with
+// rope_cache_kernel's roundings.
 struct RopePrefillArgs {
   const uint16_t* qkv;
   const uint16_t* cos;
@@ -502,34 +503,54 @@ struct RopePrefillArgs {
   uint16_t* k_cache;
   uint16_t* v_cache;
   int64_t ldqkv, ldcs, q_sb, q_sh, q_sp, c_sb, c_sh, c_sl;
-  int P, hq, hkv;
+  int P, hq, hkv, n;
 };
 
 template <class XT>
 __global__ void __launch_bounds__(256)
 rope_prefill_kernel(RopePrefillArgs a) {
-  const int row = blockIdx.x, j = blockIdx.y * 4 + (threadIdx.x >> 6), d = threadIdx.x & 63;
-  if (j >= a.hq + 2 * a.hkv) return;
-  const int b = row / a.P, p = row - b * a.P;
-  const uint16_t* src = a.qkv + (int64_t)row * a.ldqkv + (int64_t)j * 128;
-  const uint16_t rlo = src[d], rhi = src[d + 64];
-  if (j >= a.hq + a.hkv) {   // v head: copy into the cache
-    uint16_t* dst = a.v_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq - a.hkv) * a.c_sh + (int64_t)p * a.c_sl;
-    dst[d] = rlo;
-    dst[d + 64] = rhi;
-    return;
+  const int nh = a.hq + 2 * a.hkv;
+  const int64_t total = (int64_t)a.n * nh * 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int t = (int)(i & 7);
+    const int64_t rh = i >> 3;
+    const int row = (int)(rh / nh), j = (int)(rh - (int64_t)row * nh);
+    const int b = row / a.P, p = row - b * a.P;
+    const uint16_t* src = a.qkv + (int64_t)row * a.ldqkv + (int64_t)j * 128 + 8 * t;
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + 64);
+    uint16_t* dst;
+    if (j >= a.hq + a.hkv) {   // v head: copy into the cache
+      dst = a.v_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq - a.hkv) * a.c_sh + (int64_t)p * a.c_sl + 8 * t;
+      *reinterpret_cast<u32x4*>(dst) = lo;
+      *reinterpret_cast<u32x4*>(dst + 64) = hi;
+      continue;
+    }
+    const uint16_t* cr = a.cos + (int64_t)p * a.ldcs + 8 * t;
+    const uint16_t* sr = a.sin + (int64_t)p * a.ldcs + 8 * t;
+    const u32x4 c0 = *reinterpret_cast<const u32x4*>(cr), c1 = *reinterpret_cast<const u32x4*>(cr + 64);
+    const u32x4 s0 = *reinterpret_cast<const u32x4*>(sr), s1 = *reinterpret_cast<const u32x4*>(sr + 64);
+    u32x4 o0, o1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r0[2], r1[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int sh = 16 * hh;
+        const float l = XT::to_f32((uint16_t)(lo[e] >> sh)), h = XT::to_f32((uint16_t)(hi[e] >> sh));
+        const float cl = XT::to_f32((uint16_t)(c0[e] >> sh)), ch = XT::to_f32((uint16_t)(c1[e] >> sh));
+        const float sl = XT::to_f32((uint16_t)(s0[e] >> sh)), shi = XT::to_f32((uint16_t)(s1[e] >> sh));
+        r0[hh] = XT::round(l * cl) - XT::round(h * sl);   // round(-x) == -round(x) (half-even)
+        r1[hh] = XT::round(h * ch) + XT::round(l * shi);
+      }
+      o0[e] = (uint32_t)XT::from_f32(r0[0]) | ((uint32_t)XT::from_f32(r0[1]) << 16);
+      o1[e] = (uint32_t)XT::from_f32(r1[0]) | ((uint32_t)XT::from_f32(r1[1]) << 16);
+    }
+    dst = (j < a.hq) ? a.q_out + (int64_t)b * a.q_sb + (int64_t)j * a.q_sh + (int64_t)p * a.q_sp + 8 * t
+                     : a.k_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq) * a.c_sh + (int64_t)p * a.c_sl + 8 * t;
+    *reinterpret_cast<u32x4*>(dst) = o0;
+    *reinterpret_cast<u32x4*>(dst + 64) = o1;
   }
-  const uint16_t* cr = a.cos + (int64_t)p * a.ldcs;
-  const uint16_t* sr = a.sin + (int64_t)p * a.ldcs;
-  const float lo = XT::to_f32(rlo), hi = XT::to_f32(rhi);
-  const float c0 = XT::to_f32(cr[d]), c1 = XT::to_f32(cr[d + 64]);
-  const float s0 = XT::to_f32(sr[d]), s1 = XT::to_f32(sr[d + 64]);
-  const float o0 = XT::round(XT::round(lo * c0) + XT::round(-hi * s0));
-  const float o1 = XT::round(XT::round(hi * c1) + XT::round(lo * s1));
-  uint16_t* dst = (j < a.hq) ? a.q_out + (int64_t)b * a.q_sb + (int64_t)j * a.q_sh + (int64_t)p * a.q_sp
-                             : a.k_cache + (int64_t)b * a.c_sb + (int64_t)(j - a.hq) * a.c_sh + (int64_t)p * a.c_sl;
-  dst[d] = XT::from_f32(o0);
-  dst[d + 64] = XT::from_f32(o1);
 }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -671,15 +692,21 @@ extern "C" int tq_rope_prefill(const void* qkv, int64_t qkv_stride, const void* 
   if (batch == 0 || prompt_len == 0) return TQ_OK;
   if ((int64_t)batch * prompt_len >= (1LL << 31) || qkv_stride < (int64_t)(q_heads + 2 * kv_heads) * 128) return TQ_ERR_ARG;
   if (!qkv || !cos || !sin || !q_out || !k_cache || !v_cache) return TQ_ERR_ARG;
+  // 16-byte accesses: every row, head, table row and cache slot starts 16-byte aligned
+  if (!al16(qkv) || !al16(cos) || !al16(sin) || !al16(q_out) || !al16(k_cache) || !al16(v_cache) || (qkv_stride % 8) ||
+      (table_stride % 8) || (q_stride_b % 8) || (q_stride_h % 8) || (q_stride_p % 8) || (cache_stride_b % 8) ||
+      (cache_stride_h % 8) || (cache_stride_l % 8))
+    return TQ_ERR_ALIGN;
   RopePrefillArgs a{};
   a.qkv = static_cast<const uint16_t*>(qkv); a.cos = static_cast<const uint16_t*>(cos);
   a.sin = static_cast<const uint16_t*>(sin); a.q_out = static_cast<uint16_t*>(q_out);
   a.k_cache = static_cast<uint16_t*>(k_cache); a.v_cache = static_cast<uint16_t*>(v_cache);
   a.ldqkv = qkv_stride; a.ldcs = table_stride; a.q_sb = q_stride_b; a.q_sh = q_stride_h; a.q_sp = q_stride_p;
   a.c_sb = cache_stride_b; a.c_sh = cache_stride_h; a.c_sl = cache_stride_l;
-  a.P = prompt_len; a.hq = q_heads; a.hkv = kv_heads;
+  a.P = prompt_len; a.hq = q_heads; a.hkv = kv_heads; a.n = batch * prompt_len;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(batch * prompt_len, (q_heads + 2 * kv_heads + 3) / 4);
+  const int64_t total = (int64_t)a.n * (q_heads + 2 * kv_heads) * 8;
+  const dim3 grid((unsigned)std::min<int64_t>((total + 255) / 256, 16384));
   if (dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(rope_prefill_kernel<Bf16>, grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(rope_prefill_kernel<Fp16>, grid, dim3(256), 0, s, a);
   return (int)hipGetLastError();
