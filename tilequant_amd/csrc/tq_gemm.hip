@@ -451,21 +451,43 @@ gemm_splitk_kernel(GemmArgs a) {
   // Batches of U tiles: ids and weights of a batch are all in flight before
   // the first wait; the load phases are branch-free (positions past the
   // batch re-read the last valid tile, an L2 hit, and are never used).
+  // The ids and scales of up to 64 of the wave's tiles come with one vector
+  // load each (lane i: the wave's tile win + i; past the end the last tile
+  // again), so a batch's activation loads need no id round trip of their own.
   int cs[U];
   float sw[U];
   v4i bw[U][JBW];
-  auto load_batch = [&](int p0) {
+  const int first_p = lo8 + wave;
+  int idl = 0, win = 0;
+  float swl = 0.0f;
+  auto load_window = [&](int k0) {   // k0: the wave's tile index of lane 0
+    const int pc = min(first_p + (k0 + lane) * W, hi8 - 1);
+    idl = a.ids8[pc];
+    swl = a.sw8[pc];
+    win = k0;
+  };
+  auto load_weights = [&](int p0, v4i (&dst)[U][JBW]) {   // need no id
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int pu = min(p0 + u * W, hi8 - 1);
-      cs[u] = col_of(a.ids8[pu], rbase, a.n_tc);
-      sw[u] = a.sw8[pu];
 #pragma unroll
-      for (int j = 0; j < JBW; ++j) bw[u][j] = load_w8(a, pu, jb0 + j, lane);
+      for (int j = 0; j < JBW; ++j) dst[u][j] = load_w8(a, pu, jb0 + j, lane);
     }
   };
-  const int first_p = lo8 + wave;
-  if (first_p < hi8) load_batch(first_p);        // the first batch streams during the prologue
+  auto load_meta = [&](int p0) {
+    const int k0 = (p0 - first_p) / W;
+    if (k0 - win + U > 64) load_window(k0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cs[u] = col_of(__builtin_amdgcn_readlane(idl, k0 - win + u), rbase, a.n_tc);
+      sw[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), k0 - win + u));
+    }
+  };
+  if (first_p < hi8) load_window(0);
+  if (first_p < hi8) {                             // the first batch streams during the prologue
+    load_weights(first_p, bw);
+    load_meta(first_p);
+  }
 
   const int ldc = a.n_tc * 64;                    // FUSED: LDS code row stride
   int8_t* codes = reinterpret_cast<int8_t*>(red);
@@ -491,8 +513,25 @@ gemm_splitk_kernel(GemmArgs a) {
     __syncthreads();
   }
 
+  // Whole-tile (JBW 4) waves issue the next batch's weights after this
+  // batch's activation loads and before its MFMAs, so one batch's compute and
+  // the next one's HBM round trip overlap (vmcnt returns in order: the MFMAs
+  // wait for the activation only).  One-j-block waves have no registers to
+  // spare for it at 16 waves per workgroup.
+  constexpr bool PREFETCH = JBW == 4;
+  v4i bwn[U][JBW];
   for (int p0 = first_p; p0 < hi8; p0 += U * W) {
-    if (p0 != first_p) load_batch(p0);
+    if (p0 != first_p) {
+      load_meta(p0);
+      if constexpr (PREFETCH) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int j = 0; j < JBW; ++j) bw[u][j] = bwn[u][j];
+      } else {
+        load_weights(p0, bw);
+      }
+    }
     const int nu = min(U, (hi8 - p0 + W - 1) / W);   // valid tiles in this batch (uniform)
     v4i ax[U][TB];
     float sxs[U];
@@ -509,6 +548,7 @@ gemm_splitk_kernel(GemmArgs a) {
           ax[u][tb] = load_xq<XVEC ? 1 : 0>(a, tb * 16 + arow, cs[u] * 64 + akq * 16);
       }
     }
+    if (PREFETCH && p0 + U * W < hi8) load_weights(p0 + U * W, bwn);
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (u < nu) {
@@ -1961,11 +2001,13 @@ struct SplitPlan {
   int S, W, tb, jbw;
 };
 
-static int plan_u(int jbw, int tb) { return jbw == 1 ? (tb == 1 ? 8 : (tb == 2 ? 4 : 2)) : (tb == 1 ? 4 : (tb == 2 ? 2 : 1)); }
+static int plan_u(int jbw, int tb) { return jbw == 1 ? (tb == 1 ? 8 : 4) : (tb == 1 ? 4 : 2); }
 
 static int plan_max_waves(int jbw, int tb) {
-  // LDS for the reduction: W * jbw * tb * 1 KiB <= 64 KiB; launch bound 16 / 8 waves
-  int w = 64 / (jbw * tb);
+  // LDS for the reduction: W * jbw * tb * 1 KiB <= 64 KiB (128 KiB for four
+  // token blocks, whose waves otherwise take a dozen tiles each one batch at a
+  // time); launch bound 16 / 8 waves
+  int w = (tb == 4 ? 128 : 64) / (jbw * tb);
   const int bound = jbw == 4 ? 8 : 16;
   return w < bound ? w : bound;
 }
@@ -2051,7 +2093,7 @@ static hipError_t launch_split_kernel(dim3 grid, dim3 block, size_t lds, hipStre
 template <class XT, bool FUSED, bool XVEC, int JBW>
 static hipError_t launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 grid, dim3 block, size_t lds,
                                  hipStream_t s) {
-  constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 2 : 1;
+  constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 4 : 2;
   if constexpr (FUSED) {
     const int n = a.n;
     if (n <= 1) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>>(grid, block, lds, s, a);
