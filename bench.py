@@ -413,7 +413,9 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
     graph for the per-launch average (HBM fraction on packed weight bytes)."""
     import torch
     from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+    from tilequant_amd.mixed_linear import TOKEN_BLOCKED_ROWS
     from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+    from tilequant_amd.quantize_activation import quantize_activation_token_blocked
 
     s = torch.cuda.Stream()
 
@@ -443,7 +445,10 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
         a2.tokens = m
         xs = make_inputs(a2, device)
         step_ms = graph_ms(lambda: [mods[name](xs[name]) for mods in layers for name, _, _ in GROUPS], 10)
-        quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in GROUPS}
+        # the codes in the layout MixedLinear gives the GEMM at this row count
+        blocked = TOKEN_BLOCKED_ROWS[0] <= m <= TOKEN_BLOCKED_ROWS[1]
+        quantize = quantize_activation_token_blocked if blocked else quantize_activation_tile_absmax
+        quant = {name: quantize(xs[name]) for name, _, _ in GROUPS}
         outs = [torch.empty((m, mods[name].M_orig), device=device, dtype=torch.bfloat16)
                 for mods in layers for name, _, _ in GROUPS]
 
@@ -457,7 +462,8 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
                                            int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
                                            fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
                                            M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
-                                           out_dtype=torch.bfloat16, out=outs[i], tile_layout=lin.tile_layout)
+                                           out_dtype=torch.bfloat16, out=outs[i], tile_layout=lin.tile_layout,
+                                           x_int8_layout="token_blocked" if blocked else "row_major")
                     i += 1
 
         gemm_ms = graph_ms(gemms, 10)
@@ -467,7 +473,8 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
                        "gbps_packed_weights": info["packed_bytes"] / (step_ms / 1e3) / 1e9,
                        "hbm_frac_step": info["packed_bytes"] / (step_ms / 1e3) / 1e9 / HBM_PEAK_GBPS,
                        "gemm_avg_launch_us": launch_us,
-                       "gemm_hbm_frac": info["packed_bytes"] / n_launch / (launch_us / 1e6) / 1e9 / HBM_PEAK_GBPS}
+                       "gemm_hbm_frac": info["packed_bytes"] / n_launch / (launch_us / 1e6) / 1e9 / HBM_PEAK_GBPS,
+                       "activation_codes": "token_blocked" if blocked else "row_major"}
         del quant, outs, xs
     return out
 

@@ -37,6 +37,20 @@ enum { TQ_DTYPE_BF16 = 0, TQ_DTYPE_FP16 = 1, TQ_DTYPE_FP32 = 2 /* tq_quant_tenso
  *   W[16 jb + j][32 h + 8 kq .. + 7]. */
 enum { TQ_LAYOUT_ROW_MAJOR = 0, TQ_LAYOUT_MFMA = 1 };
 
+/* Flag OR'ed into the tile_layout argument of the GEMM entries (and the
+ * descriptor's tile_layout): the INT8 activation codes x_int8 are TOKEN-BLOCKED
+ * instead of row-major.  Token-blocked codes of n rows, k = 64 * n_tc columns
+ * are n_tc * ceil(n / 16) blocks of 1 KiB, block (c, b) at offset
+ * (c * ceil(n / 16) + b) * 1024, in the MFMA A-operand order: 16-byte run l
+ * (kq = l / 16, j = l % 16) holds the codes of row 16 b + j, columns
+ * 64 c + 16 kq .. + 15; rows n .. 16 ceil(n / 16) - 1 hold zeros.  Each
+ * operand load of the GEMM is then one contiguous 1 KiB (8 whole cache
+ * lines) instead of 16 row pieces of 64 bytes.  Accepted for 1 <= n <= 64
+ * with k = 64 * n_tc (x_int8_stride_n is ignored); the result is bitwise that
+ * of the same codes row-major.  tq_act_quant_token_blocked writes them.  No
+ * reference counterpart (the reference keeps codes row-major). */
+enum { TQ_XQ_TOKEN_BLOCKED = 0x100 };
+
 enum {
   TQ_OK = 0,
   TQ_ERR_ARG = -1,       /* bad size / null pointer / inconsistent shape */
@@ -60,6 +74,15 @@ int tq_abi_version(void);
  * One launch; any n (the reference routes n <= 128 here, quant_utils.py:119-134). */
 int tq_act_quant_fused(const void* x, int64_t x_stride_n, int64_t x_stride_k, int x_dtype,
                        int n, int k, int8_t* q, int64_t q_stride_n, float* sx, void* stream);
+
+/* tq_act_quant_fused writing the codes TOKEN-BLOCKED (see TQ_XQ_TOKEN_BLOCKED):
+ * q has 16 * ceil(n / 16) * k bytes, padding rows zero; same scales and code
+ * values.  1 <= n <= 64, k a multiple of 64, unit column stride, 16-byte
+ * aligned rows (x_stride_n % 8 == 0).  Counterpart of the reference's
+ * quantize_activation_tile_absmax_fused (quantize_activation.py:118-155) for
+ * the token-blocked operand format the 17..64-token GEMM reads. */
+int tq_act_quant_token_blocked(const void* x, int64_t x_stride_n, int x_dtype, int n, int k, int8_t* q,
+                               float* sx, void* stream);
 
 /* Elements of fp32 workspace tq_act_absmax_scales needs for (n, k); 0 when
  * the scales are produced in a single pass. */
@@ -212,7 +235,8 @@ typedef struct tq_linear_desc {
   int64_t x_stride, out_stride;
   int n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout;
   int fused;              /* 1: one-launch quantize + GEMM (n <= tq_linear_mixed_fused_max_tokens(k)) */
-  int8_t* x_int8;         /* [n, k] scratch codes (unused when fused) */
+  int8_t* x_int8;         /* [n, k] scratch codes (unused when fused); with TQ_XQ_TOKEN_BLOCKED in
+                             tile_layout: [16 ceil(n / 16), k], token-blocked */
   float* sx;              /* [ceil(k/64)] scratch scales (unused when fused) */
   const int8_t* int8_tiles;
   const float* int8_scales;

@@ -52,6 +52,18 @@ def test_argument_errors_return_before_any_launch(lib):
     assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
                                   None, 0, 0, None, 1, 64, 64, 1, 1, 0, 5, None, 0, None) == -2
     assert lib.tq_tiles_relayout(None, None, 1, 3, 0, 1, None) == -1
+    # token-blocked codes: 1..64 rows, k a multiple of 64 (no device memory touched)
+    assert lib.tq_act_quant_token_blocked(None, 64, 0, 0, 64, None, None, None) == -1
+    assert lib.tq_act_quant_token_blocked(None, 64, 0, 65, 64, None, None, None) == -1
+    assert lib.tq_act_quant_token_blocked(None, 100, 0, 4, 100, None, None, None) == -1
+    assert lib.tq_act_quant_token_blocked(None, 64, 3, 4, 64, None, None, None) == -2
+    blocked = nat.TQ_LAYOUT["mfma"] | nat.TQ_XQ_TOKEN_BLOCKED
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, 65, 64, 64, 1, 1, 0, blocked, None, 0, None) == -1
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, 4, 64, 100, 1, 2, 0, blocked, None, 0, None) == -1
+    assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
+                                  None, 0, 0, None, 0, 64, 64, 1, 1, 0, blocked, None, 0, None) == 0
     # empty problems are a no-op success
     assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
                                   None, 0, 0, None, 0, 64, 64, 1, 1, 0, 1, None, 0, None) == 0

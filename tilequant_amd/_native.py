@@ -17,6 +17,8 @@ ABI_VERSION = 1
 
 TQ_DTYPE = {torch.bfloat16: 0, torch.float16: 1}
 TQ_LAYOUT = {"row_major": 0, "mfma": 1}
+# flag OR'ed into the GEMM's tile_layout argument: the INT8 codes are token-blocked
+TQ_XQ_TOKEN_BLOCKED = 0x100
 
 TQ_ERR_ARG = -1
 
@@ -31,6 +33,7 @@ _SIGNATURES = {
     "tq_error_string": (ctypes.c_char_p, [_i]),
     "tq_abi_version": (_i, []),
     "tq_act_quant_fused": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _i64, _p, _p]),
+    "tq_act_quant_token_blocked": (_i, [_p, _i64, _i, _i, _i, _p, _p, _p]),
     "tq_act_absmax_workspace_elems": (_i64, [_i, _i]),
     "tq_act_absmax_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
     "tq_act_quant_with_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),

@@ -68,15 +68,34 @@ __device__ float tile_absmax(const XView& v, int c, int row0, int row1) {
   return m;
 }
 
+// Byte offset of the 8 codes of row `row`, columns col .. col + 7 (col % 8 == 0)
+// in token-blocked codes with nb 16-row blocks per column tile (TQ_XQ_TOKEN_BLOCKED):
+// block (c, row / 16) is the MFMA A operand of that 16 x 64 slice, 16-byte run
+// l = 16 kq + row % 16 holding columns 64 c + 16 kq .. + 15.
+__device__ inline int64_t blocked_offset(int row, int col, int nb) {
+  const int c = col >> 6, kq = (col & 63) >> 4;
+  return ((int64_t)(c * nb + (row >> 4)) * 64 + kq * 16 + (row & 15)) * 16 + (col & 15);
+}
+
+// nb > 0: codes token-blocked with nb 16-row blocks per column tile (vector
+// path only; rows n .. 16 nb - 1 are written as zeros), else row-major with
+// row stride ldq.
 template <class T>
 __global__ void __launch_bounds__(kQuantThreads)
-act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
+act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, int nb) {
   __shared__ float red[kQuantThreads / kWave];
   const int c = blockIdx.x, t = threadIdx.x;
   const float a = block_max(tile_absmax<T>(v, c, 0, v.n), red, kQuantThreads / kWave);
   const float s = act_scale_from_absmax<T>(a);
   const CodeScale cs(s);
   if (t == 0) sx[c] = s;
+  if (nb > 0) {
+    const int col = c * kTile + (t % 8) * 8;
+    for (int row = t / 8; row < 16 * nb; row += kRowsPerPass)
+      *reinterpret_cast<u32x2*>(q + blocked_offset(row, col, nb)) =
+          row < v.n ? codes8<T>(load8(v, row, col), cs) : u32x2{0u, 0u};
+    return;
+  }
   const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
   if (tile_vec_ok(v, c) && qvec) {
     const int col = c * kTile + (t % 8) * 8;
@@ -293,9 +312,26 @@ extern "C" int tq_act_quant_fused(const void* x, int64_t x_stride_n, int64_t x_s
   }
   dim3 grid(n_tc);
   if (x_dtype == TQ_DTYPE_BF16)
-    hipLaunchKernelGGL(act_quant_fused_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx);
+    hipLaunchKernelGGL(act_quant_fused_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx, 0);
   else
-    hipLaunchKernelGGL(act_quant_fused_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx);
+    hipLaunchKernelGGL(act_quant_fused_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, q, q_stride_n, sx, 0);
+  return (int)hipGetLastError();
+}
+
+extern "C" int tq_act_quant_token_blocked(const void* x, int64_t x_stride_n, int x_dtype, int n, int k, int8_t* q,
+                                          float* sx, void* stream) {
+  int rc = check_x(x, x_stride_n, 1, x_dtype, n, k);
+  if (rc) return rc;
+  if (n < 1 || n > 64 || k < kTile || (k % kTile) != 0 || q == nullptr || sx == nullptr) return TQ_ERR_ARG;
+  if ((x_stride_n % 8) != 0 || !aligned16(x) || ((uintptr_t)q & 7u) != 0) return TQ_ERR_ALIGN;
+  XView v{static_cast<const uint16_t*>(x), x_stride_n, 1, n, k};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nb = (n + 15) / 16;
+  dim3 grid(n_tiles_of(k));
+  if (x_dtype == TQ_DTYPE_BF16)
+    hipLaunchKernelGGL(act_quant_fused_kernel<Bf16>, grid, dim3(kQuantThreads), 0, s, v, q, (int64_t)0, sx, nb);
+  else
+    hipLaunchKernelGGL(act_quant_fused_kernel<Fp16>, grid, dim3(kQuantThreads), 0, s, v, q, (int64_t)0, sx, nb);
   return (int)hipGetLastError();
 }
 

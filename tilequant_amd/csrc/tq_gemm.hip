@@ -61,6 +61,7 @@ struct GemmArgs {
   int layout;     // TQ_LAYOUT_*
   int xvec;       // activations allow 16-byte loads (aligned rows, k == 64 * n_tc)
   int ovec;       // output rows allow 16-byte stores (16-byte aligned base, ldo % 8 == 0)
+  int xblk;       // > 0: xq is token-blocked (TQ_XQ_TOKEN_BLOCKED) with xblk 16-row blocks per column tile
   int splits;       // split-K decode kernel: splits per row tile
   int32_t* counters;  // [n_tr] arrival counters (zero between launches)
   float* partials;    // [n_tr, splits, n, 64] fp32 split partials
@@ -419,9 +420,12 @@ __device__ inline float quant_col_tile(const GemmArgs& a, const XSlice<NPOW, XVE
 // tiles per wave; 1 = one 1 KiB j-block of each tile (four workgroups share
 // a row tile, so narrow outputs still fill the GPU without any
 // cross-workgroup reduction).  Launch bound: 16 waves at JBW 1, 8 at JBW 4.
-template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW>
+// XBLK: the codes are token-blocked (a.xblk blocks of 16 rows per column
+// tile): each activation operand is one contiguous 1 KiB load.
+template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW, bool XBLK = false>
 __global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
 gemm_splitk_kernel(GemmArgs a) {
+  static_assert(!(XBLK && FUSED), "the fused prologue stages its own codes");
   // dynamic LDS: FUSED codes [n][64*n_tc] + sx[n_tc] during the main loop,
   // the wave partials for the reduction afterwards (the two never overlap in time)
   extern __shared__ float red[];
@@ -448,24 +452,11 @@ gemm_splitk_kernel(GemmArgs a) {
   const int n8 = hi8 - lo8;
 
   // ---------------- INT8 tiles: wave takes positions lo8 + wave + i*W ----------------
-  // Batches of U tiles: ids and weights of a batch are all in flight before
-  // the first wait; the load phases are branch-free (positions past the
-  // batch re-read the last valid tile, an L2 hit, and are never used).
-  // The ids and scales of up to 64 of the wave's tiles come with one vector
-  // load each (lane i: the wave's tile win + i; past the end the last tile
-  // again), so a batch's activation loads need no id round trip of their own.
-  int cs[U];
-  float sw[U];
+  // Batches of U tiles: weights and activation operands of a batch are all in
+  // flight before the first wait; the load phases are branch-free (positions
+  // past the batch re-read the last valid tile, an L2 hit, and are never used).
   v4i bw[U][JBW];
   const int first_p = lo8 + wave;
-  int idl = 0, win = 0;
-  float swl = 0.0f;
-  auto load_window = [&](int k0) {   // k0: the wave's tile index of lane 0
-    const int pc = min(first_p + (k0 + lane) * W, hi8 - 1);
-    idl = a.ids8[pc];
-    swl = a.sw8[pc];
-    win = k0;
-  };
   auto load_weights = [&](int p0, v4i (&dst)[U][JBW]) {   // need no id
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -474,20 +465,7 @@ gemm_splitk_kernel(GemmArgs a) {
       for (int j = 0; j < JBW; ++j) dst[u][j] = load_w8(a, pu, jb0 + j, lane);
     }
   };
-  auto load_meta = [&](int p0) {
-    const int k0 = (p0 - first_p) / W;
-    if (k0 - win + U > 64) load_window(k0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      cs[u] = col_of(__builtin_amdgcn_readlane(idl, k0 - win + u), rbase, a.n_tc);
-      sw[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), k0 - win + u));
-    }
-  };
-  if (first_p < hi8) load_window(0);
-  if (first_p < hi8) {                             // the first batch streams during the prologue
-    load_weights(first_p, bw);
-    load_meta(first_p);
-  }
+  if (first_p < hi8) load_weights(first_p, bw);   // the first batch streams during the prologue
 
   const int ldc = a.n_tc * 64;                    // FUSED: LDS code row stride
   int8_t* codes = reinterpret_cast<int8_t*>(red);
@@ -520,48 +498,75 @@ gemm_splitk_kernel(GemmArgs a) {
   // spare for it at 16 waves per workgroup.
   constexpr bool PREFETCH = JBW == 4;
   v4i bwn[U][JBW];
-  for (int p0 = first_p; p0 < hi8; p0 += U * W) {
-    if (p0 != first_p) {
-      load_meta(p0);
-      if constexpr (PREFETCH) {
+  // The ids, weight scales and activation scales of up to 64 of the wave's
+  // tiles come with one vector load each (lane i: the wave's tile w0 + i W;
+  // past the end the last tile again), once per window of 64 tiles and
+  // outside the batch loop.  The batch loop then issues no conditional loads,
+  // so its waits count exactly: a window reload inside it made every batch
+  // wait for all of its loads (the next batch's prefetched weights included),
+  // and a scalar load of sx[c] per tile put a scalar round trip before each
+  // tile's MFMAs.  Same tiles, same order: outputs are unchanged.
+  for (int w0 = first_p; w0 < hi8; w0 += 64 * W) {
+    const int pc = min(w0 + lane * W, hi8 - 1);
+    const int cl = col_of(a.ids8[pc], rbase, a.n_tc);
+    const float swl = a.sw8[pc];
+    float sxv;
+    if constexpr (FUSED) sxv = sxl[cl];
+    else sxv = a.sx[cl];
+    const int wend = min(hi8, w0 + 64 * W);   // 64 is a multiple of U: batches never straddle windows
+    for (int p0 = w0; p0 < wend; p0 += U * W) {
+      const int k0 = (p0 - w0) / W;
+      const int nu = min(U, (hi8 - p0 + W - 1) / W);   // valid tiles in this batch (uniform)
+      // Activation operands first, then (one-j-block waves) this batch's
+      // weights: both round trips in flight together.  Issued the other way
+      // round, the compiler's wait before the activation addresses (the
+      // previous batch's loads) also waited for the weights just issued.
+      v4i ax[U][TB];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int j = 0; j < JBW; ++j) bw[u][j] = bwn[u][j];
-      } else {
-        load_weights(p0, bw);
-      }
-    }
-    const int nu = min(U, (hi8 - p0 + W - 1) / W);   // valid tiles in this batch (uniform)
-    v4i ax[U][TB];
-    float sxs[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if constexpr (FUSED) {
-        sxs[u] = sxl[cs[u]];
-        ax[u][0] = (arow < a.n) ? *reinterpret_cast<const v4i*>(codes + arow * ldc + cs[u] * 64 + akq * 16)
-                                : v4i{0, 0, 0, 0};
-      } else {
-        sxs[u] = a.sx[cs[u]];
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb)
-          ax[u][tb] = load_xq<XVEC ? 1 : 0>(a, tb * 16 + arow, cs[u] * 64 + akq * 16);
-      }
-    }
-    if (PREFETCH && p0 + U * W < hi8) load_weights(p0 + U * W, bwn);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (u < nu) {
-        const float sc = sxs[u] * sw[u];
-#pragma unroll
-        for (int j = 0; j < JBW; ++j)
+      for (int u = 0; u < U; ++u) {
+        const int c = __builtin_amdgcn_readlane(cl, k0 + u);
+        if constexpr (FUSED) {
+          ax[u][0] = (arow < a.n) ? *reinterpret_cast<const v4i*>(codes + arow * ldc + c * 64 + akq * 16)
+                                  : v4i{0, 0, 0, 0};
+        } else {
 #pragma unroll
           for (int tb = 0; tb < TB; ++tb) {
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[u][tb], bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
+            if constexpr (XBLK) {   // blocks past the last one: zero operand (clamped read stays in the buffer)
+              const v4i v = *reinterpret_cast<const v4i*>(
+                  a.xq + ((int64_t)(c * a.xblk + min(tb, a.xblk - 1)) * 64 + lane) * 16);
+              ax[u][tb] = tb < a.xblk ? v : v4i{0, 0, 0, 0};
+            } else {
+              ax[u][tb] = load_xq<XVEC ? 1 : 0>(a, tb * 16 + arow, c * 64 + akq * 16);
+            }
           }
+        }
       }
+      if (p0 != first_p) {
+        if constexpr (PREFETCH) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int j = 0; j < JBW; ++j) bw[u][j] = bwn[u][j];
+        } else {
+          load_weights(p0, bw);
+        }
+      }
+      if (PREFETCH && p0 + U * W < hi8) load_weights(p0 + U * W, bwn);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u < nu) {
+          const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sxv), k0 + u)) *
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), k0 + u));
+#pragma unroll
+          for (int j = 0; j < JBW; ++j)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+              const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[u][tb], bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
+            }
+        }
+    }
   }
 
   // ---------------- 16-bit tiles: rotation continues after the INT8 ones ----------------
@@ -2102,6 +2107,12 @@ static hipError_t launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 gri
     if (n <= 8) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>>(grid, block, lds, s, a);
     return launch_split_kernel<gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>>(grid, block, lds,
                                                                                                    s, a);
+  } else if (a.xblk > 0) {
+    switch (p.tb) {
+      case 1: return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, true, JBW, true>>(grid, block, lds, s, a);
+      case 2: return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, true, JBW, true>>(grid, block, lds, s, a);
+      default: return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, true, JBW, true>>(grid, block, lds, s, a);
+    }
   } else {
     switch (p.tb) {
       case 1: return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
@@ -2242,14 +2253,17 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
                            int n_tc, int split_k, int tile_layout, float* workspace,
                            int64_t workspace_elems, const int32_t* units, int n_units, int n_first,
                            void* stream) {
+  const bool xblk = (tile_layout & TQ_XQ_TOKEN_BLOCKED) != 0;   // token-blocked codes
+  tile_layout &= ~TQ_XQ_TOKEN_BLOCKED;
   int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
   if (rc) return rc;
   if (units != nullptr && (n_units < 1 || n_units > n_tr || n_first < 0 || n_first > n_units))
     return TQ_ERR_ARG;
+  if (xblk && (n > kDecodeMaxTokens || k != n_tc * 64)) return TQ_ERR_ARG;
   if (n == 0 || m == 0) return TQ_OK;
   if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_int8 == nullptr || sx == nullptr)
     return TQ_ERR_ARG;
-  if (x_int8_stride_n < k) return TQ_ERR_ARG;
+  if (!xblk && x_int8_stride_n < k) return TQ_ERR_ARG;
   const bool has16 = fp16_tiles != nullptr && fp16_tile_ids != nullptr && fp16_row_ptr != nullptr;
   if (has16 && (x_fp == nullptr || x_fp_stride_n < k)) return TQ_ERR_ARG;
   if (!aligned16(int8_tiles) || (has16 && !aligned16(fp16_tiles))) return TQ_ERR_ALIGN;
@@ -2264,11 +2278,16 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
   a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
+  if (xblk) a.ldq = k;   // the stride argument is ignored for token-blocked codes
   a.xvec = xvec_ok(a);
   a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
+  if (xblk) {   // read by gemm_splitk_kernel only, on its vector path
+    if (!a.xvec || !aligned16(x_int8)) return TQ_ERR_ALIGN;
+    a.xblk = (n + 15) / 16;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
-  if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec) {
+  if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec && !xblk) {
     const DecodePlan d = plan_decode(n, k, n_tr, n_tc, false);
     if (d.ok)
       return (int)((x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, false>(a, d, s)
@@ -2472,7 +2491,10 @@ extern "C" int tq_linear_forward(const tq_linear_desc* d) {
                                  d->int8_row_ptr, d->fp16_tiles, d->fp16_tile_ids, d->fp16_row_ptr, d->out,
                                  d->out_stride, d->out_dtype, d->bias, d->n, d->m, d->k, d->n_tr, d->n_tc, 0,
                                  d->tile_layout, d->workspace, d->workspace_elems, d->stream);
-  const int rc = tq_act_quant_fused(d->x, d->x_stride, 1, d->x_dtype, d->n, d->k, d->x_int8, d->k, d->sx, d->stream);
+  const int rc = (d->tile_layout & TQ_XQ_TOKEN_BLOCKED)
+                     ? tq_act_quant_token_blocked(d->x, d->x_stride, d->x_dtype, d->n, d->k, d->x_int8, d->sx, d->stream)
+                     : tq_act_quant_fused(d->x, d->x_stride, 1, d->x_dtype, d->n, d->k, d->x_int8, d->k, d->sx,
+                                          d->stream);
   if (rc != 0) return rc;
   return tq_gemm_mixed_rows(d->x_int8, d->k, d->sx, d->int8_tiles, d->int8_scales, d->int8_tile_ids, d->int8_row_ptr,
                             d->x, d->x_stride, d->x_dtype, d->fp16_tiles, d->fp16_tile_ids, d->fp16_row_ptr, d->out,

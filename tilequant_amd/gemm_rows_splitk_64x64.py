@@ -140,6 +140,7 @@ def gemm_mixed_rows_splitk(
     out: Optional[torch.Tensor] = None,
     tile_layout: str = "row_major",
     prefill_plan: Optional[PrefillPlan] = None,
+    x_int8_layout: str = "row_major",
 ) -> torch.Tensor:
     """Return x @ W^T (+ bias) for a packed mixed INT8/16-bit weight.
 
@@ -149,7 +150,10 @@ def gemm_mixed_rows_splitk(
     tile list are reduced per output tile (in fixed order); ``None`` picks it
     from the shape.  ``prefill_plan`` (optional, from ``prefill_plan()`` for
     this weight) orders the prefill kernel's work; it does not change the
-    result.  Results are bitwise reproducible for fixed arguments.
+    result.  ``x_int8_layout="token_blocked"`` takes codes from
+    ``quantize_activation_token_blocked`` (1..64 rows; the result is bitwise
+    that of the same codes row-major).  Results are bitwise reproducible for
+    fixed arguments.
     """
     nat.require_device(x_fp, x_int8, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
                        fp16_tiles, fp16_tile_ids, fp16_row_ptr, bias, out)
@@ -159,8 +163,19 @@ def gemm_mixed_rows_splitk(
         out = torch.empty((n, M), device=x_fp.device, dtype=out_dtype)
     elif tuple(out.shape) != (n, M) or out.dtype != out_dtype or out.stride(1) != 1:
         raise ValueError("out must be an (N, M) tensor of out_dtype with unit column stride")
-    if x_int8.dim() != 2 or x_int8.shape[0] != n or x_int8.shape[1] < K or x_int8.stride(1) != 1:
-        raise ValueError("x_int8 must be an (N, >=K) int8 tensor with unit column stride")
+    if x_int8_layout == "token_blocked":
+        if not 1 <= n <= 64 or K != 64 * n_tc:
+            raise ValueError("token-blocked codes take 1..64 rows and K == 64 * n_tc")
+        if (x_int8.dtype != torch.int8 or x_int8.dim() != 1 or x_int8.numel() != 16 * ((n + 15) // 16) * K
+                or not x_int8.is_contiguous()):
+            raise ValueError("token-blocked x_int8 must be a flat contiguous int8 tensor of 16 * ceil(N / 16) * K codes")
+        x_int8_stride, layout_flag = K, nat.TQ_XQ_TOKEN_BLOCKED
+    elif x_int8_layout == "row_major":
+        if x_int8.dim() != 2 or x_int8.shape[0] != n or x_int8.shape[1] < K or x_int8.stride(1) != 1:
+            raise ValueError("x_int8 must be an (N, >=K) int8 tensor with unit column stride")
+        x_int8_stride, layout_flag = x_int8.stride(0), 0
+    else:
+        raise ValueError(f"x_int8_layout must be 'row_major' or 'token_blocked', got {x_int8_layout!r}")
     if x_fp.dim() != 2 or x_fp.shape[1] < K or x_fp.stride(1) != 1:
         raise ValueError("x_fp must be an (N, >=K) tensor with unit column stride")
     if sx.dtype != torch.float32 or sx.numel() < n_tc or not sx.is_contiguous():
@@ -182,13 +197,13 @@ def gemm_mixed_rows_splitk(
     if n == 0 or M == 0:
         return out
     ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
-    args = (nat.ptr(x_int8), x_int8.stride(0), nat.ptr(sx),
+    args = (nat.ptr(x_int8), x_int8_stride, nat.ptr(sx),
             nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
             nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
             nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
             nat.ptr(fp16_row_ptr) if has16 else None,
             nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
-            n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems)
+            n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout] | layout_flag, ws_ptr, ws_elems)
     if prefill_plan is not None:
         units = prefill_plan.units
         if units.device != x_fp.device or units.dtype != torch.int32 or not units.is_contiguous():

@@ -43,6 +43,7 @@ from . import _native as nat
 from .gemm_rows_splitk_64x64 import (PrefillPlan, fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused,
                                      prefill_plan)
 from .pack import Pack, concat_packs_along_rows
+from .quantize_activation import quantize_activation_token_blocked
 from .quant_utils import (
     activation_tile_absmax_scales,
     quantize_activation_tile_absmax,
@@ -78,6 +79,12 @@ _CU_COUNT: Dict[int, int] = {}
 # Sibling projections reuse one activation quantization for inputs of at least
 # this many rows (the reference's threshold, mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
+# Inputs of this many rows up to 64 (the GEMM's four-token-block range) are
+# quantized into token-blocked codes: every activation operand load of the
+# GEMM is then one contiguous 1 KiB instead of 16 row pieces of 64 bytes
+# (Llama-3.2-3B decode linear set at 64 tokens on MI355X: 77.6 -> ~57 us of
+# GEMM per layer).  Outputs are bitwise those of row-major codes.
+TOKEN_BLOCKED_ROWS = (33, 64)
 
 
 def _linear_forward():
@@ -165,22 +172,38 @@ class ServeOnce:
 _SHARED_QUANT: Dict[Tuple[int, int], ServeOnce] = {}
 
 
-def _quantize_for(module: nn.Module, x: torch.Tensor, x_work: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Codes and scales of ``x_work`` (the 2-D view of ``x``) for ``module``,
-    shared with its sibling projections under inference mode for inputs of at
-    least ACTIVATION_QUANT_CACHE_MIN_ROWS rows."""
+def _token_blocked(x_work: torch.Tensor, tile_n: int) -> bool:
+    """Whether ``x_work``'s codes go token-blocked (TOKEN_BLOCKED_ROWS, full
+    64-column tiles, 16-byte aligned rows)."""
+    n, k = x_work.shape
+    return (TOKEN_BLOCKED_ROWS[0] <= n <= TOKEN_BLOCKED_ROWS[1] and tile_n == 64 and k % 64 == 0
+            and x_work.stride(1) == 1 and x_work.stride(0) % 8 == 0 and x_work.data_ptr() % 16 == 0)
+
+
+def _quantize(x_work: torch.Tensor, tile_n: int, blocked: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    if blocked:
+        return quantize_activation_token_blocked(x_work)
+    return quantize_activation_tile_absmax(x_work, tile_n=tile_n)
+
+
+def _quantize_for(module: nn.Module, x: torch.Tensor, x_work: torch.Tensor,
+                  blocked: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Codes and scales of ``x_work`` (the 2-D view of ``x``) for ``module``
+    (token-blocked when ``blocked``), shared with its sibling projections
+    under inference mode for inputs of at least ACTIVATION_QUANT_CACHE_MIN_ROWS
+    rows."""
     if x_work.shape[0] < ACTIVATION_QUANT_CACHE_MIN_ROWS or not x_work.is_cuda \
             or not torch.is_inference_mode_enabled():
-        return quantize_activation_tile_absmax(x_work, tile_n=module.tile_n)
+        return _quantize(x_work, module.tile_n, blocked)
     slot = (x_work.device.index or 0, torch.cuda.current_stream(x_work.device).cuda_stream)
     memo = _SHARED_QUANT.get(slot)
     if memo is None:
         memo = _SHARED_QUANT[slot] = ServeOnce()
-    key = (_view_key(x), module.tile_n)
+    key = (_view_key(x), module.tile_n, blocked)
     hit = memo.take(x, key, id(module))
     if hit is not None:
         return hit
-    codes = quantize_activation_tile_absmax(x_work, tile_n=module.tile_n)
+    codes = _quantize(x_work, module.tile_n, blocked)
     memo.put(x, key, id(module), codes)
     return codes
 
@@ -290,7 +313,7 @@ class MixedLinear(nn.Module):
         return self._plan[0]
 
     def _gemm_bias(self, x_fp: torch.Tensor, x_int8: torch.Tensor, sx: torch.Tensor,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, x_int8_layout: str = "row_major") -> torch.Tensor:
         out_dtype = self._out_dtype()
         return gemm_mixed_rows_splitk(
             x_fp=x_fp, x_int8=x_int8, sx=sx,
@@ -298,7 +321,7 @@ class MixedLinear(nn.Module):
             int8_row_ptr=self.int8_row_ptr, fp16_tiles=self.fp16_tiles, fp16_tile_ids=self.fp16_tile_ids,
             fp16_row_ptr=self.fp16_row_ptr, M=self.M_orig, K=self.K_orig, n_tr=self.n_tr, n_tc=self.n_tc,
             out_dtype=out_dtype, bias=self._out_bias(out_dtype), out=out, tile_layout=self.tile_layout,
-            prefill_plan=self._prefill_plan(int(x_fp.shape[0])),
+            prefill_plan=self._prefill_plan(int(x_fp.shape[0])), x_int8_layout=x_int8_layout,
         )
 
     def _fused_limit(self) -> int:
@@ -413,8 +436,10 @@ class MixedLinear(nn.Module):
         if 0 < n_rows <= min(self._fused_rows_for_cfg(), chunk):
             y = self._fused_decode(x_work)
         elif n_rows <= chunk:
-            x_int8, sx = _quantize_for(self, x, x_work)
-            y = self._gemm_bias(x_fp=x_work, x_int8=x_int8, sx=sx)
+            blocked = _token_blocked(x_work, self.tile_n)
+            x_int8, sx = _quantize_for(self, x, x_work, blocked)
+            y = self._gemm_bias(x_fp=x_work, x_int8=x_int8, sx=sx,
+                                x_int8_layout="token_blocked" if blocked else "row_major")
         else:
             sx = activation_tile_absmax_scales(x_work, tile_n=self.tile_n)
             y = torch.empty((n_rows, self.M_orig), device=x_work.device, dtype=self._out_dtype())

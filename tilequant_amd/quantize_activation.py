@@ -52,6 +52,31 @@ def quantize_activation_tile_absmax_fused(x_fp: torch.Tensor) -> Tuple[torch.Ten
     return x_q, sx
 
 
+def token_blocked_elems(n: int, k: int) -> int:
+    """Bytes of token-blocked codes of n rows and k columns: 16-row blocks."""
+    return 16 * ((int(n) + 15) // 16) * int(k)
+
+
+def quantize_activation_token_blocked(x_fp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quantize_activation_tile_absmax_fused with the codes TOKEN-BLOCKED, the
+    operand format of the 17..64-token GEMM: a flat int8 tensor of
+    ``token_blocked_elems(n, k)`` bytes in which block (c, b) -- rows
+    16 b .. 16 b + 15 of column tile c -- is one 1 KiB MFMA A operand (16-byte
+    run 16 kq + j holds row 16 b + j, columns 64 c + 16 kq .. + 15; rows past n
+    are zero).  Same scales and code values.  1 <= n <= 64, k a multiple of 64,
+    rows 16-byte aligned with unit column stride."""
+    _check_x(x_fp)
+    n, k = (int(v) for v in x_fp.shape)
+    if not 1 <= n <= 64 or k == 0 or k % 64:
+        raise ValueError(f"token-blocked codes take 1..64 rows and a multiple of 64 columns, got {(n, k)}")
+    x_q = torch.empty((token_blocked_elems(n, k),), device=x_fp.device, dtype=torch.int8)
+    sx = torch.empty((k // 64,), device=x_fp.device, dtype=torch.float32)
+    rc = nat.lib().tq_act_quant_token_blocked(nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype), n, k,
+                                              nat.ptr(x_q), nat.ptr(sx), nat.stream_handle(x_fp.device))
+    nat.check(rc, "tq_act_quant_token_blocked")
+    return x_q, sx
+
+
 def activation_tile_absmax_scales_64_fused(x_fp: torch.Tensor) -> torch.Tensor:
     """Scales only, over all rows (reference :158-176)."""
     _check_x(x_fp)
