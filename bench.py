@@ -413,7 +413,6 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
     graph for the per-launch average (HBM fraction on packed weight bytes)."""
     import torch
     from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
-    from tilequant_amd.mixed_linear import TOKEN_BLOCKED_ROWS
     from tilequant_amd.quant_utils import quantize_activation_tile_absmax
     from tilequant_amd.quantize_activation import quantize_activation_token_blocked
 
@@ -445,10 +444,10 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
         a2.tokens = m
         xs = make_inputs(a2, device)
         step_ms = graph_ms(lambda: [mods[name](xs[name]) for mods in layers for name, _, _ in GROUPS], 10)
-        # the codes in the layout MixedLinear gives the GEMM at this row count
-        blocked = TOKEN_BLOCKED_ROWS[0] <= m <= TOKEN_BLOCKED_ROWS[1]
-        quantize = quantize_activation_token_blocked if blocked else quantize_activation_tile_absmax
-        quant = {name: quantize(xs[name]) for name, _, _ in GROUPS}
+        # the codes in the layout MixedLinear gives each projection's GEMM at this row count
+        blocked = {name: layers[0][name].token_blocked_codes(m) for name, _, _ in GROUPS}
+        quant = {name: (quantize_activation_token_blocked if blocked[name] else quantize_activation_tile_absmax)(
+            xs[name]) for name, _, _ in GROUPS}
         outs = [torch.empty((m, mods[name].M_orig), device=device, dtype=torch.bfloat16)
                 for mods in layers for name, _, _ in GROUPS]
 
@@ -463,7 +462,7 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
                                            fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
                                            M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
                                            out_dtype=torch.bfloat16, out=outs[i], tile_layout=lin.tile_layout,
-                                           x_int8_layout="token_blocked" if blocked else "row_major")
+                                           x_int8_layout="token_blocked" if blocked[name] else "row_major")
                     i += 1
 
         gemm_ms = graph_ms(gemms, 10)
@@ -474,7 +473,7 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
                        "hbm_frac_step": info["packed_bytes"] / (step_ms / 1e3) / 1e9 / HBM_PEAK_GBPS,
                        "gemm_avg_launch_us": launch_us,
                        "gemm_hbm_frac": info["packed_bytes"] / n_launch / (launch_us / 1e6) / 1e9 / HBM_PEAK_GBPS,
-                       "activation_codes": "token_blocked" if blocked else "row_major"}
+                       "token_blocked_codes": sorted(name for name, b in blocked.items() if b)}
         del quant, outs, xs
     return out
 

@@ -139,20 +139,38 @@ def test_token_blocked_gemm_rejects_wrong_buffers():
         _gemm(pack, x65, q65.reshape(-1), s65, "token_blocked")
 
 
-@pytest.mark.parametrize("n", [32, 33, 48, 64])
-def test_mixed_linear_rows_33_to_64_take_token_blocked_codes_bitwise(n):
-    """MixedLinear quantizes 33..64-row inputs token-blocked; its output is the
-    row-major computation's bit for bit (32 rows stay row-major)."""
-    _, pack, _ = _pack(5120, 3072, 0.01, seed=77)
+@pytest.mark.parametrize("m,k,n,blocked", [
+    (5120, 3072, 16, False), (5120, 3072, 17, True), (5120, 3072, 24, True), (5120, 3072, 32, True),
+    (5120, 3072, 33, True), (5120, 3072, 48, True), (5120, 3072, 64, True),
+    (3072, 8192, 8, False), (3072, 8192, 16, True), (3072, 8192, 24, True)])
+def test_mixed_linear_token_blocked_rows_are_bitwise_row_major(m, k, n, blocked):
+    """MixedLinear quantizes token-blocked where the GEMM prefers it (17..64
+    rows; fewer for wide inputs whose codes do not fit LDS) -- through the
+    cached eager launch below 32 rows, the shared-quantization path from 32 --
+    and its output is the row-major computation's bit for bit."""
+    _, pack, _ = _pack(m, k, 0.01, seed=77)
     lin = MixedLinear(pack, None, CFG)
-    x = make_x(n, 3072, seed=n).cuda()
+    assert lin.token_blocked_codes(n) == blocked
+    x = make_x(n, k, seed=n).cuda()
     xq, sx = quantize_activation_tile_absmax(x)
     ref = _gemm(pack, x, xq, sx, "row_major")
-    with torch.inference_mode():
-        y = lin(x)
-        y3 = lin(x.view(1, n, 3072))
+    y = lin(x)                                    # eager: descriptor path below 32 rows
     assert torch.equal(y, ref)
-    assert torch.equal(y3.view(n, -1), ref)
+    assert torch.equal(lin(x), ref)               # the cached descriptor again
+    with torch.inference_mode():
+        assert torch.equal(lin(x.view(1, n, k)).view(n, -1), ref)
+    # captured in a HIP graph (the quantize + GEMM path), replayed
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        lin(x)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        yg = lin(x)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ref)
 
 
 def test_projection_group_at_64_rows_equals_members():

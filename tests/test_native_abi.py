@@ -70,6 +70,17 @@ def test_argument_errors_return_before_any_launch(lib):
     assert lib.tq_pack_int8_tiles(None, 64, 0, 64, 64, None, 0, 1, 1, None, None, None, None) == 0
 
 
+def test_token_blocked_preference(lib):
+    """Token-blocked codes for 17..64 rows, and below that only where the codes
+    do not fit the LDS-staged decode kernel (k = 8192 from 12 rows on)."""
+    pref = lib.tq_gemm_prefers_token_blocked
+    assert pref(64, 3072, 80, 48) == 1 and pref(33, 3072, 48, 48) == 1 and pref(17, 3072, 256, 48) == 1
+    assert pref(32, 8192, 48, 128) == 1
+    assert pref(16, 3072, 80, 48) == 0 and pref(4, 3072, 256, 48) == 0 and pref(4, 8192, 48, 128) == 0
+    assert pref(16, 8192, 48, 128) == 1
+    assert pref(65, 3072, 48, 48) == 0 and pref(0, 3072, 48, 48) == 0 and pref(16, 3000, 48, 47) == 0
+
+
 def test_workspace_sizing(lib):
     assert lib.tq_act_absmax_workspace_elems(128, 3072) == 0
     assert lib.tq_act_absmax_workspace_elems(8192, 3072) == 32 * 48

@@ -2434,6 +2434,17 @@ extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* 
   return split_any ? n : 0;   // 0: the plain pair order is the plan
 }
 
+extern "C" int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc) {
+  if (n < 1 || n > kDecodeMaxTokens || n_tr < 1 || k != n_tc * 64) return 0;
+  // 17..64 rows: the split-K kernel on token-blocked codes beats the
+  // LDS-staged kernel wherever that one fits (Llama-3.2-3B projections at 32
+  // tokens on MI355X: QKV 13.2 -> 9.7 us, O 8.9 -> 7.7, Gate/Up 17.1 -> 16.7);
+  // up to 16 rows only where the codes do not fit LDS (Down at 16 tokens:
+  // 12.1 -> 10.3 us; the others stay faster staged).
+  if (n > 16) return 1;
+  return plan_decode(n, k, n_tr, n_tc, false).ok ? 0 : 1;
+}
+
 extern "C" int tq_linear_mixed_fused_max_tokens(int k) {
   const int n_tc = (k + 63) / 64;
   int n = kFusedMaxTokens;

@@ -43,7 +43,7 @@ from . import _native as nat
 from .gemm_rows_splitk_64x64 import (PrefillPlan, fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused,
                                      prefill_plan)
 from .pack import Pack, concat_packs_along_rows
-from .quantize_activation import quantize_activation_token_blocked
+from .quantize_activation import quantize_activation_token_blocked, token_blocked_elems
 from .quant_utils import (
     activation_tile_absmax_scales,
     quantize_activation_tile_absmax,
@@ -79,12 +79,6 @@ _CU_COUNT: Dict[int, int] = {}
 # Sibling projections reuse one activation quantization for inputs of at least
 # this many rows (the reference's threshold, mixed_linear.py:20-21).
 ACTIVATION_QUANT_CACHE_MIN_ROWS = 32
-# Inputs of this many rows up to 64 (the GEMM's four-token-block range) are
-# quantized into token-blocked codes: every activation operand load of the
-# GEMM is then one contiguous 1 KiB instead of 16 row pieces of 64 bytes
-# (Llama-3.2-3B decode linear set at 64 tokens on MI355X: 77.6 -> ~57 us of
-# GEMM per layer).  Outputs are bitwise those of row-major codes.
-TOKEN_BLOCKED_ROWS = (33, 64)
 
 
 def _linear_forward():
@@ -172,12 +166,11 @@ class ServeOnce:
 _SHARED_QUANT: Dict[Tuple[int, int], ServeOnce] = {}
 
 
-def _token_blocked(x_work: torch.Tensor, tile_n: int) -> bool:
-    """Whether ``x_work``'s codes go token-blocked (TOKEN_BLOCKED_ROWS, full
-    64-column tiles, 16-byte aligned rows)."""
-    n, k = x_work.shape
-    return (TOKEN_BLOCKED_ROWS[0] <= n <= TOKEN_BLOCKED_ROWS[1] and tile_n == 64 and k % 64 == 0
-            and x_work.stride(1) == 1 and x_work.stride(0) % 8 == 0 and x_work.data_ptr() % 16 == 0)
+def _blockable(x_work: torch.Tensor) -> bool:
+    """Rows the token-blocked quantizer takes: full 64-column tiles, unit
+    column stride, 16-byte aligned rows."""
+    return (x_work.shape[1] % 64 == 0 and x_work.stride(1) == 1 and x_work.stride(0) % 8 == 0
+            and x_work.data_ptr() % 16 == 0)
 
 
 def _quantize(x_work: torch.Tensor, tile_n: int, blocked: bool) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -249,6 +242,7 @@ class MixedLinear(nn.Module):
         else:
             self.register_parameter("bias", None)
         self._launches: Dict[Tuple[Any, ...], _Launch] = {}
+        self._blocked_rows: Dict[int, bool] = {}
         self._plan: Optional[Tuple[Optional[PrefillPlan]]] = None   # (plan,) once built
 
     def _apply(self, fn, recurse=True):
@@ -324,6 +318,19 @@ class MixedLinear(nn.Module):
             prefill_plan=self._prefill_plan(int(x_fp.shape[0])), x_int8_layout=x_int8_layout,
         )
 
+    def token_blocked_codes(self, n_rows: int) -> bool:
+        """Whether this module quantizes ``n_rows``-row inputs into
+        token-blocked codes: where the GEMM's schedule runs faster on them
+        (``tq_gemm_prefers_token_blocked``: 17..64 rows, and fewer where the
+        codes do not fit the LDS-staged kernel).  Outputs are bitwise those of
+        row-major codes; only the operand loads change (each 16-row x 64-column
+        slice one contiguous 1 KiB instead of 16 row pieces of 64 bytes)."""
+        hit = self._blocked_rows.get(n_rows)
+        if hit is None:
+            hit = self._blocked_rows[n_rows] = self.tile_n == 64 and bool(nat.lib().tq_gemm_prefers_token_blocked(
+                int(n_rows), self.K_orig, self.n_tr, self.n_tc))
+        return hit
+
     def _fused_limit(self) -> int:
         limit = getattr(self, "_fused_rows", None)
         if limit is None:
@@ -375,7 +382,13 @@ class MixedLinear(nn.Module):
         d.n, d.m, d.k, d.n_tr, d.n_tc = n, self.M_orig, self.K_orig, self.n_tr, self.n_tc
         d.x_dtype, d.out_dtype = nat.dtype_code(x_work.dtype), nat.dtype_code(out_dtype)
         d.tile_layout, d.fused = nat.TQ_LAYOUT[self.tile_layout], int(fused)
-        if not fused:
+        if not fused and self.token_blocked_codes(n) and _blockable(x_work):
+            d.tile_layout |= nat.TQ_XQ_TOKEN_BLOCKED
+            x_int8 = torch.empty((token_blocked_elems(n, k),), device=dev, dtype=torch.int8)
+            sx = torch.empty((self.n_tc,), device=dev, dtype=torch.float32)
+            keep += [x_int8, sx]
+            d.x_int8, d.sx = x_int8.data_ptr(), sx.data_ptr()
+        elif not fused:
             x_int8 = torch.empty((n, k), device=dev, dtype=torch.int8)
             sx = torch.empty((self.n_tc,), device=dev, dtype=torch.float32)
             keep += [x_int8, sx]
@@ -399,7 +412,7 @@ class MixedLinear(nn.Module):
         bias = self.bias
         fused = 0 < n <= min(self._fused_rows_for_cfg(), self._activation_row_chunk_size())
         key = (n, x_work.stride(0), x_work.dtype, dev.index, stream, self.int8_tiles.data_ptr(),
-               0 if bias is None else bias.data_ptr(), out_dtype, self.tile_layout, fused)
+               0 if bias is None else bias.data_ptr(), out_dtype, self.tile_layout, fused, _blockable(x_work))
         launch = self._launches.get(key)
         if launch is None:
             launch = self._launches[key] = self._build_launch(x_work, stream, out_dtype, fused)
@@ -436,7 +449,7 @@ class MixedLinear(nn.Module):
         if 0 < n_rows <= min(self._fused_rows_for_cfg(), chunk):
             y = self._fused_decode(x_work)
         elif n_rows <= chunk:
-            blocked = _token_blocked(x_work, self.tile_n)
+            blocked = self.token_blocked_codes(n_rows) and _blockable(x_work)
             x_int8, sx = _quantize_for(self, x, x_work, blocked)
             y = self._gemm_bias(x_fp=x_work, x_int8=x_int8, sx=sx,
                                 x_int8_layout="token_blocked" if blocked else "row_major")
