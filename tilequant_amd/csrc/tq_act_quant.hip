@@ -85,18 +85,38 @@ __global__ void __launch_bounds__(kQuantThreads)
 act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, int nb) {
   __shared__ float red[kQuantThreads / kWave];
   const int c = blockIdx.x, t = threadIdx.x;
+  const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
+  if (v.n <= 2 * kRowsPerPass && tile_vec_ok(v, c) && (nb > 0 || qvec)) {
+    // Up to 64 rows a thread's share is two 8-element groups: loaded once and
+    // kept in registers from the absmax to the codes (one global round trip
+    // instead of two; same closed form, same codes).
+    const int col = c * kTile + (t % 8) * 8;
+    u32x4 w[2];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = t / 8 + i * kRowsPerPass;
+      w[i] = row < v.n ? load8(v, row, col) : u32x4{0u, 0u, 0u, 0u};
+      m = max8<T>(w[i], m);
+    }
+    const float s = act_scale_from_absmax<T>(block_max(m, red, kQuantThreads / kWave));
+    const CodeScale cs(s);
+    if (t == 0) sx[c] = s;
+    const int rows = nb > 0 ? 16 * nb : v.n;   // token-blocked: padding rows are written as zeros
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = t / 8 + i * kRowsPerPass;
+      if (row >= rows) continue;
+      const u32x2 code = row < v.n ? codes8<T>(w[i], cs) : u32x2{0u, 0u};
+      if (nb > 0) *reinterpret_cast<u32x2*>(q + blocked_offset(row, col, nb)) = code;
+      else *reinterpret_cast<u32x2*>(q + (int64_t)row * ldq + col) = code;
+    }
+    return;
+  }
   const float a = block_max(tile_absmax<T>(v, c, 0, v.n), red, kQuantThreads / kWave);
   const float s = act_scale_from_absmax<T>(a);
   const CodeScale cs(s);
   if (t == 0) sx[c] = s;
-  if (nb > 0) {
-    const int col = c * kTile + (t % 8) * 8;
-    for (int row = t / 8; row < 16 * nb; row += kRowsPerPass)
-      *reinterpret_cast<u32x2*>(q + blocked_offset(row, col, nb)) =
-          row < v.n ? codes8<T>(load8(v, row, col), cs) : u32x2{0u, 0u};
-    return;
-  }
-  const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
   if (tile_vec_ok(v, c) && qvec) {
     const int col = c * kTile + (t % 8) * 8;
     for (int row = t / 8; row < v.n; row += kRowsPerPass)
