@@ -270,7 +270,9 @@ class FusedPrefillStep:
         e = lambda *s: torch.empty(s, device=dev, dtype=dt)   # noqa: E731
         self.h = [e(N, H), e(N, H)]                          # residual stream, ping-pong
         self.y = e(N, H)                                     # normed activations
-        self.q = e(self.B, self.hq, self.P, self.head_dim)   # rotated queries, SDPA layout
+        # rotated queries, token-major [B, P, Hq, D], handed to SDPA as the [B, Hq, P, D] view: the fused
+        # backends then return token-major output, which the O projection reads without a transpose copy
+        self.q = e(self.B, self.P, self.hq, self.head_dim).transpose(1, 2)
         self.m = e(N, self.inter)                            # silu(gate) * up
         self.h_last = e(self.B, H)
         self.final = e(self.B, H)

@@ -81,7 +81,10 @@ def _graph_attention(module, query, key, value, attention_mask, dropout: float =
 def _prefill_attention(dec, query, key, value, dropout: float, scale: float) -> torch.Tensor:
     """Causal SDPA on the fused backends.  Grouped-query heads go in directly
     where the backend takes them; otherwise (found once, in the eager warm-up
-    before capture) the kv heads are repeated to the query heads first."""
+    before capture) the kv heads are repeated to the query heads first.  The
+    backends return their output in the query's memory layout, so a query
+    that is a [B, H, P, D] view of token-major storage (the fused prefill's)
+    gives token-major output and the final ``contiguous()`` copies nothing."""
     with sdpa_kernel(list(_FUSED_SDPA)):
         if dec._sdpa_gqa is not False:
             try:
