@@ -341,6 +341,30 @@ def test_split_k_counters_reset_over_many_launches_and_graph_replays():
         assert torch.equal(_fused(pack, x, split_k=8), y0)   # eager work between replays
 
 
+@pytest.mark.parametrize("m,k", [(3072, 3072), (1024, 4096), (3072, 8192), (640, 1024), (3584, 3584)])
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_lane_quantization_equals_two_launch_path(m, k, n, dtype):
+    """Fused decode workgroups with one thread per 8-column chunk of a row
+    (3072, 4096, 8192 and 3584 columns on these grids) take the column-tile
+    absmax from registers and DPP instead of LDS atomics from 2 rows on; one
+    row and 1024 columns (4 waves, 128 chunks per row) take the general path.  Both are bitwise the
+    separate quantizer + GEMM, including an all-zero column tile (scale 1), a
+    tile whose absmax sits in the last row and one of signed half-integers."""
+    W, pack, ids16 = _case(m, k, 0.02, seed=970 + n + k, dtype=dtype)
+    x = make_x(n, k, seed=971 + n + k, dtype=dtype)
+    x[:, 64:128] = 0                                  # scale 1, codes 0
+    x[n - 1, 200] = -37.5                             # absmax in the last row, negative
+    if k >= 320:
+        x[:, 256:320] = torch.tensor([(-1) ** i * (i + 0.5) for i in range(64)], dtype=torch.float32).to(dtype)
+    xd = x.cuda()
+    xq, sx = quantize_activation_tile_absmax(xd)
+    y2 = _gemm(pack, xd, xq, sx, out_dtype=dtype)
+    yf = _fused(pack, xd, out_dtype=dtype)
+    assert torch.equal(yf, y2)
+    assert torch.equal(_fused(pack, xd, out_dtype=dtype), yf)
+
+
 def test_fused_rejects_more_than_16_rows():
     W, pack, _ = _case(128, 128, 0.1, seed=960)
     with pytest.raises(ValueError):

@@ -172,8 +172,10 @@ def test_fused_decode_option_is_bitwise_identical():
         assert torch.equal(lin_f(x), y)
         assert torch.equal(lin_a(x), y)   # "auto": fused up to 4 rows here (narrow input, 64 workgroups)
     assert lin_a._fused_rows_for_cfg() == 4
-    wide, _, _, _ = _linear(256, 8192, 0.01, 82, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
-    assert wide._fused_rows_for_cfg() == 2   # 8192 columns: quantization repeated per workgroup is too dear
+    down, _, _, _ = _linear(256, 8192, 0.01, 82, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    assert down._fused_rows_for_cfg() == 4   # 8192 columns, 16 workgroups: fused up to 4 rows
+    wide, _, _, _ = _linear(256, 12288, 0.01, 83, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    assert wide._fused_rows_for_cfg() == 2   # wider: quantization repeated per workgroup is too dear
 
 
 @pytest.mark.parametrize("fused_mode", ["auto", False, True])

@@ -59,12 +59,14 @@ PLAN_MIN_ROWS = 64
 FUSED_AUTO_MAX_ROWS = 2
 # ... and up to this many rows when the repeated quantization is cheap: inputs
 # of at most FUSED_AUTO_NARROW_K columns whose decode grid (four workgroups
-# per 64-row output tile) gives no CU a second workgroup.  At 4 rows on MI355X
-# the O projection (3072 x 3072, 192 workgroups) runs fused in 7.4-7.5 us
-# instead of 7.8-8.1 us for quantize + GEMM; Q/K/V (320 workgroups), Gate/Up
-# (1024) and Down (8192 columns) are slower fused.
+# per 64-row output tile) gives no CU a second workgroup.  Such a workgroup
+# quantizes with one thread per 8-column chunk of a row (register + DPP
+# absmax, one barrier).  At 4 rows on MI355X (28 layers, cold weights): O
+# (3072 x 3072, 192 workgroups) 7.0 us fused vs 7.7 quantize + GEMM, Down
+# (3072 x 8192, 192 workgroups) 10.5 vs 11.2; Q/K/V (320 workgroups, 10.0 vs
+# 9.8) and Gate/Up (1024, 22.1 vs 14.5) stay two launches.
 FUSED_AUTO_NARROW_ROWS = 4
-FUSED_AUTO_NARROW_K = 4096
+FUSED_AUTO_NARROW_K = 8192
 
 
 def _device_cus(device: torch.device) -> int:
