@@ -178,6 +178,40 @@ def test_fused_decode_option_is_bitwise_identical():
     assert wide._fused_rows_for_cfg() == 2   # wider: quantization repeated per workgroup is too dear
 
 
+@pytest.mark.parametrize("n", [2, 3, 4])
+def test_down_width_fused_by_auto_policy_eager_and_graph(n):
+    """Llama-3.2-3B Down width (3072 x 8192, 192 workgroups): the "auto" policy
+    runs quantize + GEMM as one launch up to 4 rows (lane quantization, 16
+    waves); eager calls, the cached descriptor, inference mode and HIP-graph
+    replays are all bitwise the two-launch module's output, and within the
+    oracle's tolerance."""
+    off = SimpleNamespace(quant_style="gi", dtype_out="bf16", fused_decode=False)
+    ref_lin, W, ids16, _ = _linear(3072, 8192, 0.01, 990 + n, off, bias=True)
+    auto = MixedLinear(ref_lin.to_pack(), ref_lin.bias.detach(), SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    assert auto._fused_rows_for_cfg() == 4
+    x_cpu = make_x(n, 8192, seed=991 + n)
+    x = x_cpu.cuda()
+    ref = ref_lin(x)
+    assert torch.equal(auto(x), ref)
+    assert torch.equal(auto(x), ref)                      # cached descriptor
+    with torch.inference_mode():
+        assert torch.equal(auto(x.view(1, n, 8192)).view(n, -1), ref)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        auto(x)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        yg = auto(x)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ref)
+        assert torch.equal(ref_lin(x), ref)               # eager work between replays
+    acc, sab, n_tc = _expected(W, ids16, x_cpu)
+    assert_gemm_close(ref, acc, sab, n_tc, bias=values(ref_lin.bias.detach().cpu()))
+
+
 @pytest.mark.parametrize("fused_mode", ["auto", False, True])
 @pytest.mark.parametrize("bias,dtype_out", [(False, "bf16"), (True, "fp16")])
 def test_cached_launch_path_equals_uncached_calls(fused_mode, bias, dtype_out):
