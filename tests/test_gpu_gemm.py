@@ -347,8 +347,9 @@ def test_split_k_counters_reset_over_many_launches_and_graph_replays():
 def test_fused_lane_quantization_equals_two_launch_path(m, k, n, dtype):
     """Fused decode workgroups with one thread per 8-column chunk of a row
     (3072, 4096, 8192 and 3584 columns on these grids) take the column-tile
-    absmax from registers and DPP instead of LDS atomics from 2 rows on; one
-    row and 1024 columns (4 waves, 128 chunks per row) take the general path.  Both are bitwise the
+    absmax from registers and DPP instead of LDS atomics from 2 rows on (from
+    one row with 16 waves: 8192 columns); one row on fewer waves and 1024
+    columns (4 waves, 128 chunks per row) take the general path.  Both are bitwise the
     separate quantizer + GEMM, including an all-zero column tile (scale 1), a
     tile whose absmax sits in the last row and one of signed half-integers."""
     W, pack, ids16 = _case(m, k, 0.02, seed=970 + n + k, dtype=dtype)

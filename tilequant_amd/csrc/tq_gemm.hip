@@ -830,10 +830,11 @@ gemm_decode_kernel(GemmArgs a) {
   // many-unit batches (UMAX 12 / 16) run 4 waves on more than 32 column
   // tiles, so T < cpr there: not compiled in (it would cost them registers).
   // Measured on MI355X (Llama-3.2-3B projections, cold weights): 0.4-1.8 us
-  // faster per launch at 2-4 rows, 0.1-0.3 us slower at one row, which keeps
-  // the general path.
+  // faster per launch at 2-4 rows; at one row 0.2 us faster with 16 waves
+  // (four barriers cost more there) but 0.1-0.3 us slower with 6, so one-row
+  // launches of fewer than 16 waves keep the general path.
   constexpr bool kQuantByLanes = QUANT && UMAX <= 8;
-  if (kQuantByLanes && T == cpr && a.n >= 2) {
+  if (kQuantByLanes && T == cpr && (a.n >= 2 || T >= 1024)) {
     uint32_t m = 0u;
 #pragma unroll
     for (int j = 0; j < CMAX; ++j)
