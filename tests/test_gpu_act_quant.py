@@ -142,10 +142,13 @@ def test_exact_half_integer_quotients_round_half_even(dtype):
 
 
 @pytest.mark.parametrize("n,k,dtype", [(513, 64, torch.bfloat16), (1000, 3072, torch.float16),
-                                       (8192, 8192, torch.bfloat16), (4353, 1024, torch.float16)])
+                                       (8192, 8192, torch.bfloat16), (4353, 1024, torch.float16),
+                                       (777, 3136, torch.bfloat16), (20000, 192, torch.float16)])
 def test_two_level_launch_equals_scales_then_codes(n, k, dtype):
     """tq_act_quant_two_level (the codes kernel reduces the absmax partials
-    itself) against the oracle and the two-call path, bitwise."""
+    itself, two column tiles per workgroup) against the oracle and the
+    two-call path, bitwise; odd tile counts (1, 3, 49) leave the last
+    workgroup one tile, 20000 rows give 79 partials per column."""
     x = make_x(n, k, seed=3000 + n + k, dtype=dtype)
     xd = x.cuda()
     q, sx = quantize_activation_tile_absmax_two_level(xd)
