@@ -259,14 +259,55 @@ int tq_linear_forward(const tq_linear_desc* d);
  * reference keeps codes row-major); MixedLinear asks it per row count. */
 int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc);
 
-/* TEST-ONLY.  Writes the exact INT32 product of every INT8 tile with every
- * token row, products[t][row][j] (int32 [T8, n, 64]), computed by the same
- * device tile routine the GEMM uses.  No reference counterpart: it exposes
- * the quantity the reference's tl.dot produces at gemm_rows_splitk_64x64.py:134. */
-int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
-                              const int8_t* int8_tiles, const int32_t* int8_tile_ids,
-                              const int32_t* int8_row_ptr, int n, int k, int n_tr, int n_tc,
-                              int tile_layout, int32_t* products, void* stream);
+/* TEST-ONLY.  Kernel families of the automatic GEMM schedule, as reported by
+ * the *_products_i32 entries below. */
+enum {
+  TQ_KERNEL_DECODE = 1,                 /* LDS-staged decode kernel on given codes (n <= 32) */
+  TQ_KERNEL_DECODE_QUANT = 2,           /* the same kernel quantizing the activation itself (n <= 16) */
+  TQ_KERNEL_SPLITK = 3,                 /* split-K decode kernel, row-major codes (n <= 64) */
+  TQ_KERNEL_SPLITK_TOKEN_BLOCKED = 4,   /* split-K decode kernel, token-blocked codes */
+  TQ_KERNEL_SPLITK_QUANT = 5,           /* split-K decode kernel quantizing the activation itself */
+  TQ_KERNEL_PREFILL_V5 = 6,             /* prefill DMA ring, two row tiles, 16-bit tiles in the ring */
+  TQ_KERNEL_PREFILL_V3 = 7,             /* prefill DMA ring for k > 19456 */
+  TQ_KERNEL_PREFILL_ASYNC = 8,          /* prefill DMA ring for k > 32768 */
+  TQ_KERNEL_PREFILL_REGISTER = 9        /* prefill through registers (unaligned rows or k % 64 != 0) */
+};
+
+/* TEST-ONLY.  tq_gemm_mixed_rows_planned (prefill_units may be NULL, then it
+ * is tq_gemm_mixed_rows) launching the DUMP instantiation of the very kernel
+ * the automatic schedule picks for these arguments: besides writing out as
+ * usual, every INT8 tile's exact INT32 product -- the v_mfma_i32_16x16x64_i8
+ * result before its scale FMA -- is written for the token rows row0 ..
+ * row0 + rows - 1 into products, int32 [T8][rows][64]: products[p][i][j] =
+ * sum_k x_int8[row0 + i][64 c + k] * W8_p[j][k] for the INT8 tile at position
+ * p (column tile c).  *kernel (host pointer, nullable) receives the
+ * TQ_KERNEL_* family that ran.  bf16 activations only (TQ_ERR_DTYPE
+ * otherwise); 0 <= row0, 1 <= rows <= n - row0.  No reference counterpart: it
+ * exposes the quantity the reference's tl.dot produces at
+ * src/kernels/triton/gemm_rows_splitk_64x64.py:125-137, for every kernel. */
+int tq_gemm_mixed_rows_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
+                                    const int8_t* int8_tiles, const float* int8_scales,
+                                    const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                                    const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                                    const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                                    const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                                    int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                                    int n_tc, int split_k, int tile_layout, float* workspace,
+                                    int64_t workspace_elems, const int32_t* prefill_units, int n_units,
+                                    int n_first, int32_t* products, int row0, int rows, int* kernel,
+                                    void* stream);
+
+/* TEST-ONLY.  The same for tq_linear_mixed_fused: the products are those of
+ * the codes the kernel computes from x_fp itself. */
+int tq_linear_mixed_fused_products_i32(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
+                                       const int8_t* int8_tiles, const float* int8_scales,
+                                       const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                                       const void* fp16_tiles, const int32_t* fp16_tile_ids,
+                                       const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n,
+                                       int out_dtype, const void* bias, int n, int m, int k, int n_tr,
+                                       int n_tc, int split_k, int tile_layout, float* workspace,
+                                       int64_t workspace_elems, int32_t* products, int row0, int rows,
+                                       int* kernel, void* stream);
 
 /* ---- decode attention ----------------------------------------------------
  * One query token per sequence over a static KV cache read up to a length

@@ -4,8 +4,12 @@
   MixedLinear with the reference's 4096-row chunks (two chunks, whole-input
   scales) and with one chunk -- bitwise equal -- and against the oracle on
   sampled rows.
-* Qwen2.5-7B gate / down and Qwen2.5-14B stacked Q/K/V at their
-  real output widths, clustered keep10 / keep20 masks, 4 and 8192 tokens,
+  The stacked Q/K/V (5120 x 3072) and Gate/Up (16384 x 3072) groups at 8192
+  tokens, with the automatic schedule and with an explicit work plan.
+* every projection of Qwen2.5-7B (stacked Q/K/V 4608 x 3584, O,
+  stacked Gate/Up 37888 x 3584, Down) and Qwen2.5-14B (stacked Q/K/V
+  7168 x 5120, O, stacked Gate/Up 27648 x 5120, Down 5120 x 13824) at its
+  real output width, clustered keep10 / keep20 masks, 4 and 8192 tokens,
   against the oracle on sampled rows (the oracle's cost does not grow with the
   token count).
 * the 28-layer Llama-3.2-3B with a vocabulary of 128256 at batch 4,
@@ -36,7 +40,7 @@ from helpers import assert_gemm_close, bits, clustered_weight, complement, make_
 from oracle import native as onat
 from oracle import numerics as nm
 from oracle import packing as opk
-from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
+from tilequant_amd.gemm_rows_splitk_64x64 import PrefillPlan, gemm_mixed_rows_splitk
 from tilequant_amd.mixed_linear import MixedLinear
 from tilequant_amd.pack import concat_packs_along_rows, pack_weight_from_tile_ids
 from tilequant_amd.quant_utils import quantize_activation_tile_absmax
@@ -79,12 +83,35 @@ def _oracle_rows(op, x_cpu, rows, sx_ref):
     return xq_rows, acc, sab
 
 
-def _gemm(pack, xd, xq, sx):
+def _gemm(pack, xd, xq, sx, plan=None):
     return gemm_mixed_rows_splitk(
         x_fp=xd, x_int8=xq, sx=sx, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales,
         int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles,
         fp16_tile_ids=pack.fp16_tile_ids, fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig,
-        n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=torch.bfloat16, tile_layout=pack.tile_layout)
+        n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=torch.bfloat16, tile_layout=pack.tile_layout,
+        prefill_plan=plan)
+
+
+def _stack(members, frac, seed, clustered):
+    """Device and oracle packs of members stacked along the output rows (as
+    MixedLinearGroup stacks Q/K/V and Gate/Up), packs checked bit-exact; and
+    the most 16-bit tiles any row tile of a member carries."""
+    packs, ops, max16 = [], [], 0
+    for i, (m, kk) in enumerate(members):
+        if clustered:
+            W, ids16 = clustered_weight(m, kk, frac, seed=seed + i)
+        else:
+            W = make_w(m, kk, seed=seed + i)
+            ids16 = uniform_fp16_ids(m // 64, kk // 64, frac, seed=seed + 50 + i)
+        packs.append(_pack(W, ids16))
+        ops.append(oracle_pack(W, ids16))
+        _check_pack(packs[-1], ops[-1])
+        rp = ops[-1].fp16_row_ptr
+        max16 = max(max16, int((rp[1:] - rp[:-1]).max()))
+        del W
+    pack = packs[0] if len(packs) == 1 else concat_packs_along_rows(packs)
+    op = ops[0] if len(ops) == 1 else opk.concat_rows(ops)
+    return pack, op, max16
 
 
 # ---- configs[2]: whole Llama-3.2-3B projections at 8192 tokens ------------------------------------
@@ -117,33 +144,52 @@ def test_llama_prefill_projection_8192_tokens_two_chunks(m, k):
     assert_gemm_close(y1[torch.from_numpy(rows).to(DEV)], acc, sab, n_tc)
 
 
+@pytest.mark.parametrize("group", ["qkv", "gate_up"])
+def test_llama_prefill_stacked_groups_8192_tokens(group):
+    """The stacked Q/K/V (5120 x 3072) and Gate/Up (16384 x 3072) groups at
+    8192 tokens, keep05 uniform, against the oracle on sampled rows: with the
+    automatic schedule and with an explicit work plan of single row tiles
+    (every row tile its own unit), which must give bitwise the same output."""
+    members = {"qkv": [(3072, 3072), (1024, 3072), (1024, 3072)], "gate_up": [(8192, 3072), (8192, 3072)]}[group]
+    pack, op, _ = _stack(members, 0.05, seed=31 + len(members), clustered=False)
+    n, k = 8192, 3072
+    x = make_x(n, k, seed=33)
+    xd = x.to(DEV)
+    xq, sx = quantize_activation_tile_absmax(xd)
+    sx_ref = onat.act_scales(values(x))
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), sx_ref.view(np.uint32))
+    y = _gemm(pack, xd, xq, sx)
+    units = torch.tensor([r | (1 << 30) for r in range(pack.n_tr)], dtype=torch.int32, device=DEV)
+    y_plan = _gemm(pack, xd, xq, sx, plan=PrefillPlan(units, 0, pack.n_tr))
+    assert torch.equal(y_plan, y)
+    rows = _sample_rows(n)
+    _, acc, sab = _oracle_rows(op, x, rows, sx_ref)
+    assert_gemm_close(y[torch.from_numpy(rows).to(DEV)], acc, sab, op.n_tc)
+
+
 # ---- configs[3]: Qwen2.5 widths with clustered masks -------------------------------------------
 
 QWEN_SHAPES = {
-    "qwen7b_gate": [(18944, 3584)],
+    "qwen7b_qkv": [(3584, 3584), (512, 3584), (512, 3584)],        # stacked q/k/v: 4608 x 3584
+    "qwen7b_o": [(3584, 3584)],
+    "qwen7b_gate_up": [(18944, 3584), (18944, 3584)],              # stacked gate/up: 37888 x 3584
     "qwen7b_down": [(3584, 18944)],
-    "qwen14b_qkv": [(5120, 5120), (1024, 5120), (1024, 5120)],   # stacked q/k/v: 7168 x 5120
+    "qwen14b_qkv": [(5120, 5120), (1024, 5120), (1024, 5120)],     # stacked q/k/v: 7168 x 5120
+    "qwen14b_o": [(5120, 5120)],
+    "qwen14b_gate_up": [(13824, 5120), (13824, 5120)],             # stacked gate/up: 27648 x 5120
+    "qwen14b_down": [(5120, 13824)],
 }
 
 
 @pytest.mark.parametrize("frac", [0.10, 0.20])
 @pytest.mark.parametrize("proj", sorted(QWEN_SHAPES))
 def test_qwen_real_widths_clustered_masks(proj, frac):
-    """Qwen2.5-7B gate (18944 x 3584), down (3584 x 18944) and Qwen2.5-14B
-    stacked Q/K/V (7168 x 5120) with top-k clustered BF16 tiles: packs
-    bit-exact; 4-token decode and 8192-token prefill outputs vs the oracle."""
+    """Every Qwen2.5-7B / 14B projection group at its real width with top-k
+    clustered BF16 tiles: packs bit-exact; 4-token decode and 8192-token
+    prefill outputs vs the oracle."""
     members = QWEN_SHAPES[proj]
     k = members[0][1]
-    packs, ops, max16 = [], [], 0
-    for i, (m, kk) in enumerate(members):
-        W, ids16 = clustered_weight(m, kk, frac, seed=m + kk + i + int(frac * 100))
-        packs.append(_pack(W, ids16))
-        ops.append(oracle_pack(W, ids16))
-        _check_pack(packs[-1], ops[-1])
-        rp = ops[-1].fp16_row_ptr
-        max16 = max(max16, int((rp[1:] - rp[:-1]).max()))
-    pack = packs[0] if len(packs) == 1 else concat_packs_along_rows(packs)
-    op = ops[0] if len(ops) == 1 else opk.concat_rows(ops)
+    pack, op, max16 = _stack(members, frac, seed=sum(m for m, _ in members) + k + int(frac * 100), clustered=True)
     assert max16 >= 4 * frac * op.n_tc   # clustered: some row tiles carry several times the mean share
     for n in (4, 8192):
         x = make_x(n, k, seed=k + n)

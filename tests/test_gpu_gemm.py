@@ -16,7 +16,8 @@ from helpers import assert_gemm_close, bits, complement, make_w, make_x, oracle_
 from oracle import native as onat
 from oracle import numerics as nm
 from oracle import packing as opk
-from tilequant_amd.gemm_rows_splitk_64x64 import PrefillPlan, gemm_mixed_rows_splitk, gemm_tile_products_i32, prefill_plan
+from tilequant_amd.gemm_rows_splitk_64x64 import PrefillPlan, gemm_mixed_rows_products_i32, gemm_mixed_rows_splitk, \
+    prefill_plan
 from tilequant_amd.pack import pack_weight_from_tile_ids, relayout_pack
 from tilequant_amd.quant_utils import quantize_activation_tile_absmax
 
@@ -58,13 +59,17 @@ def _oracle_pack_any(W, ids16):
     return p
 
 
-def _gemm(pack, xd, xq, sx, bias=None, out=None, split_k=None, out_dtype=torch.bfloat16):
-    return gemm_mixed_rows_splitk(
+def _kw(pack, xd, xq, sx, bias=None, out=None, split_k=None, out_dtype=torch.bfloat16):
+    return dict(
         x_fp=xd, x_int8=xq, sx=sx, int8_tiles=pack.int8_tiles, int8_scales=pack.int8_scales,
         int8_tile_ids=pack.int8_tile_ids, int8_row_ptr=pack.int8_row_ptr, fp16_tiles=pack.fp16_tiles,
         fp16_tile_ids=pack.fp16_tile_ids, fp16_row_ptr=pack.fp16_row_ptr, M=pack.M_orig, K=pack.K_orig,
         n_tr=pack.n_tr, n_tc=pack.n_tc, out_dtype=out_dtype, bias=bias, split_k=split_k, out=out,
         tile_layout=pack.tile_layout)
+
+
+def _gemm(pack, xd, xq, sx, bias=None, out=None, split_k=None, out_dtype=torch.bfloat16):
+    return gemm_mixed_rows_splitk(**_kw(pack, xd, xq, sx, bias, out, split_k, out_dtype))
 
 
 def test_config1_packer_products_and_output():
@@ -83,13 +88,14 @@ def test_config1_packer_products_and_output():
     xq, sx = quantize_activation_tile_absmax(xd)
     xq_ref, sx_ref = nm.act_quant(values(x))
     assert np.array_equal(xq.cpu().numpy(), xq_ref) and np.array_equal(sx.cpu().numpy(), sx_ref)
-    # INT32 tile products: bit-exact, through the GEMM's own device routine
-    P = gemm_tile_products_i32(x_int8=xq, int8_tiles=pack.int8_tiles, int8_tile_ids=pack.int8_tile_ids,
-                               int8_row_ptr=pack.int8_row_ptr, K=3072, n_tr=48, n_tc=48, tile_layout="mfma")
+    # INT32 tile products: bit-exact, from the DUMP instantiation of the kernel this shape runs
+    y_dump, P, kern = gemm_mixed_rows_products_i32(**_kw(pack, xd, xq, sx))
+    assert kern == "decode"
     P_ref = onat.tile_products_i32(xq_ref, op.int8_tiles, op.int8_tile_ids, 48)
     assert np.array_equal(P.cpu().numpy(), P_ref)
     # output within tolerance of the exact sum
     y = _gemm(pack, xd, xq, sx)
+    assert torch.equal(y_dump, y)
     acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
     worst_ulp = assert_gemm_close(y, acc, sab, 48)
     assert worst_ulp <= 2.0
@@ -100,8 +106,7 @@ def test_config1_packer_products_and_output():
     rm = relayout_pack(pack, "row_major")
     assert np.array_equal(rm.int8_tiles.cpu().numpy(), op.int8_tiles)
     assert torch.equal(_gemm(rm, xd, xq, sx), y)
-    P_rm = gemm_tile_products_i32(x_int8=xq, int8_tiles=rm.int8_tiles, int8_tile_ids=rm.int8_tile_ids,
-                                  int8_row_ptr=rm.int8_row_ptr, K=3072, n_tr=48, n_tc=48, tile_layout="row_major")
+    _, P_rm, _ = gemm_mixed_rows_products_i32(**_kw(rm, xd, xq, sx))
     assert torch.equal(P_rm, P)
     back = relayout_pack(rm, "mfma")
     assert torch.equal(back.int8_tiles, pack.int8_tiles) and torch.equal(back.fp16_tiles, pack.fp16_tiles)
@@ -131,11 +136,12 @@ def test_token_counts_and_ragged_shapes(n):
     xq, sx = quantize_activation_tile_absmax(xd)
     xq_ref, sx_ref = nm.act_quant(values(x))
     assert np.array_equal(xq.cpu().numpy(), xq_ref)
-    P = gemm_tile_products_i32(x_int8=xq, int8_tiles=pack.int8_tiles, int8_tile_ids=pack.int8_tile_ids,
-                               int8_row_ptr=pack.int8_row_ptr, K=300, n_tr=pack.n_tr, n_tc=pack.n_tc,
-                               tile_layout="mfma")
+    # K % 64 != 0: split-K decode kernel (<= 64 rows) or register prefill kernel, on unaligned rows
+    y_dump, P, kern = gemm_mixed_rows_products_i32(**_kw(pack, xd, xq, sx))
+    assert kern == ("splitk" if n <= 64 else "prefill_register")
     assert np.array_equal(P.cpu().numpy(), onat.tile_products_i32(xq_ref, op.int8_tiles, op.int8_tile_ids, 5, K=300))
     y = _gemm(pack, xd, xq, sx)
+    assert torch.equal(y_dump, y)
     acc, sab = _oracle_f64(pack, op, x, xq_ref, sx_ref)
     assert_gemm_close(y, acc, sab, pack.n_tc)
 

@@ -13,7 +13,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtilequant_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TQ_DTYPE = {torch.bfloat16: 0, torch.float16: 1}
 TQ_LAYOUT = {"row_major": 0, "mfma": 1}
@@ -65,7 +65,22 @@ _SIGNATURES = {
                                    _p, _i64, _i, _p,
                                    _i, _i, _i, _i, _i,
                                    _i, _i, _p, _i64, _p]),
-    "tq_gemm_tile_products_i32": (_i, [_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
+    "tq_gemm_mixed_rows_products_i32": (_i, [_p, _i64, _p,
+                                             _p, _p, _p, _p,
+                                             _p, _i64, _i,
+                                             _p, _p, _p,
+                                             _p, _i64, _i, _p,
+                                             _i, _i, _i, _i, _i,
+                                             _i, _i, _p, _i64,
+                                             _p, _i, _i,
+                                             _p, _i, _i, ctypes.POINTER(_i), _p]),
+    "tq_linear_mixed_fused_products_i32": (_i, [_p, _i64, _i,
+                                                _p, _p, _p, _p,
+                                                _p, _p, _p,
+                                                _p, _i64, _i, _p,
+                                                _i, _i, _i, _i, _i,
+                                                _i, _i, _p, _i64,
+                                                _p, _i, _i, ctypes.POINTER(_i), _p]),
     "tq_decode_attention_workspace_elems": (_i64, [_i, _i, _i]),
     "tq_decode_attention_plan": (_i, [_i, _i, _i, _i, _i, _i, _p, _p]),
     "tq_decode_attention": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,

@@ -55,7 +55,10 @@ struct GemmArgs {
   uint16_t* out;
   int64_t ldo;
   const uint16_t* bias;
+  // DUMP instantiations only: int32 [T8, dump_n, 64] products of token rows
+  // dump_r0 .. dump_r0 + dump_n - 1 (see dump_i32)
   int32_t* dump;
+  int dump_r0, dump_n;
   int n, m, k, n_tr, n_tc;
   int out_bf16;   // output dtype: 1 bf16, 0 fp16
   int layout;     // TQ_LAYOUT_*
@@ -74,12 +77,9 @@ struct GemmArgs {
 
 constexpr int32_t kUnitSingle = 1 << 30;
 
-constexpr int kMaxWaves = 16;
 constexpr int kDecodeMaxTokens = 64;  // token counts served by gemm_splitk_kernel
 constexpr int kFusedMaxTokens = 16;   // token counts the fused quantize+GEMM path takes
 constexpr size_t kFusedMaxLds = 64 * 1024;   // the fused path keeps n x k int8 codes in LDS
-constexpr int kUnroll8 = 4;   // INT8 tiles in flight per wave
-constexpr int kUnroll16 = 2;  // 16-bit tiles in flight per wave
 
 // ---- operand loads --------------------------------------------------------
 
@@ -140,168 +140,22 @@ __device__ inline int col_of(int id, int rbase, int n_tc) {
   return (int)min((unsigned)(id - rbase), (unsigned)(n_tc - 1));
 }
 
-// Sum the W waves' partial accumulators through LDS in wave order 0..W-1 (a
-// fixed order: bitwise reproducible), round to the output dtype, add bias
-// with the reference's double rounding, store.  D layout: lane l holds
-// column jb*16 + l%16 and tokens n0 + tb*16 + 4*(l/16) + v.
-template <int TB>
-__device__ inline void reduce_store(const GemmArgs& a, float* red, const v4f* acc, int W, int wave,
-                                    int lane, int r, int jb, int n0) {
-  constexpr int E = TB * 4 * 64;
+// Test instantiations (DUMP = true) of the production kernels: the exact
+// INT32 result d of an INT8 tile's v_mfma_i32_16x16x64_i8, before its scale
+// FMA, is also written to a.dump[p][row - dump_r0][col] for the token rows
+// row0 + v (v = 0..3, the D layout) inside [dump_r0, dump_r0 + dump_n).  p is
+// the tile's INT8 position, col the output feature inside the row tile.
+// Everything else in the kernel is unchanged, so the products come from the
+// very instruction stream that computes the outputs.
+template <bool DUMP>
+__device__ inline void dump_i32(const GemmArgs& a, int p, int row0, int col, const v4i& d) {
+  if constexpr (DUMP) {
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[(wave * TB * 4 + tb * 4 + v) * 64 + lane] = acc[tb][v];
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    float sum = red[e];
-    for (int w = 1; w < W; ++w) sum += red[w * E + e];
-    const int ln = e & 63, tv = e >> 6, tb = tv >> 2, v = tv & 3;
-    const int row = n0 + tb * 16 + 4 * (ln >> 4) + v;
-    const int col = r * 64 + jb * 16 + (ln & 15);
-    if (row < a.n && col < a.m) {
-      uint16_t y;
-      if (a.out_bf16) {
-        y = Bf16::from_f32(sum);
-        if (a.bias) y = Bf16::from_f32(Bf16::to_f32(y) + Bf16::to_f32(a.bias[col]));
-      } else {
-        y = Fp16::from_f32(sum);
-        if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
-      }
-      a.out[(int64_t)row * a.ldo + col] = y;
+    for (int v = 0; v < 4; ++v) {
+      const int rr = row0 + v - a.dump_r0;
+      if ((unsigned)rr < (unsigned)a.dump_n) a.dump[((int64_t)p * a.dump_n + rr) * 64 + col] = d[v];
     }
   }
-}
-
-// ---- the kernel -----------------------------------------------------------
-
-// 64-token blocks hold 4x the accumulators: cap them at 8 waves (256 VGPRs).
-constexpr int max_waves_for(int tb) { return tb == 4 ? 8 : kMaxWaves; }
-
-template <class XT, int TB, bool DUMP>
-__global__ void __launch_bounds__(max_waves_for(TB) * kWave)
-gemm_rows_kernel(GemmArgs a) {
-  extern __shared__ float red[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int W = blockDim.x >> 6;
-  const int r = blockIdx.x >> 2, jb = blockIdx.x & 3;
-  const int n0 = blockIdx.y * 16 * TB;
-  const int arow = lane & 15;       // A operand token row within a 16-block
-  const int akq = lane >> 4;        // A operand k chunk
-  const int rbase = r * a.n_tc;     // tile id = r * n_tc + c for tiles of row r
-
-  v4f acc[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) acc[tb] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // ---------------- INT8 tiles ----------------
-  const int lo8 = a.rp8[r], hi8 = a.rp8[r + 1];
-  int p = lo8 + wave;
-  for (; p + (kUnroll8 - 1) * W < hi8; p += kUnroll8 * W) {
-    int c[kUnroll8];
-    float s[kUnroll8];
-    v4i bw[kUnroll8];
-    v4i ax[kUnroll8][TB];
-#pragma unroll
-    for (int u = 0; u < kUnroll8; ++u) {
-      const int pu = p + u * W;
-      c[u] = col_of(a.ids8[pu], rbase, a.n_tc);
-      bw[u] = load_w8(a, pu, jb, lane);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll8; ++u) {
-      if constexpr (!DUMP) s[u] = a.sx[c[u]] * a.sw8[p + u * W];
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) ax[u][tb] = load_xq(a, n0 + tb * 16 + arow, c[u] * 64 + akq * 16);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll8; ++u) {
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[u][tb], bw[u], v4i{0, 0, 0, 0}, 0, 0, 0);
-        if constexpr (DUMP) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = n0 + tb * 16 + 4 * akq + v;
-            if (row < a.n) a.dump[((int64_t)(p + u * W) * a.n + row) * 64 + jb * 16 + arow] = d[v];
-          }
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[tb][v] = fmaf((float)d[v], s[u], acc[tb][v]);
-        }
-      }
-    }
-  }
-  for (; p < hi8; p += W) {
-    const int c = col_of(a.ids8[p], rbase, a.n_tc);
-    const v4i bw = load_w8(a, p, jb, lane);
-    float s = 0.0f;
-    if constexpr (!DUMP) s = a.sx[c] * a.sw8[p];
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const v4i ax = load_xq(a, n0 + tb * 16 + arow, c * 64 + akq * 16);
-      v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
-      if constexpr (DUMP) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = n0 + tb * 16 + 4 * akq + v;
-          if (row < a.n) a.dump[((int64_t)p * a.n + row) * 64 + jb * 16 + arow] = d[v];
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[tb][v] = fmaf((float)d[v], s, acc[tb][v]);
-      }
-    }
-  }
-  if constexpr (DUMP) return;
-
-  // ---------------- 16-bit tiles ----------------
-  if (a.w16 != nullptr) {
-    const int lo16 = a.rp16[r], hi16 = a.rp16[r + 1];
-    // continue the round-robin where the INT8 tiles stopped
-    const int n8 = hi8 - lo8;
-    const int first = (wave - (n8 % W) + W) % W;
-    int q = lo16 + first;
-    for (; q + (kUnroll16 - 1) * W < hi16; q += kUnroll16 * W) {
-      int c[kUnroll16];
-      v4i bw[kUnroll16][2];
-      v4i ax[kUnroll16][TB][2];
-#pragma unroll
-      for (int u = 0; u < kUnroll16; ++u) {
-        c[u] = col_of(a.ids16[q + u * W], rbase, a.n_tc);
-        bw[u][0] = load_w16(a, q + u * W, jb, 0, lane);
-        bw[u][1] = load_w16(a, q + u * W, jb, 1, lane);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll16; ++u)
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            ax[u][tb][h] = load_xf(a, n0 + tb * 16 + arow, c[u] * 64 + h * 32 + akq * 8);
-#pragma unroll
-      for (int u = 0; u < kUnroll16; ++u)
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          acc[tb] = mfma16<XT>(ax[u][tb][0], bw[u][0], acc[tb]);
-          acc[tb] = mfma16<XT>(ax[u][tb][1], bw[u][1], acc[tb]);
-        }
-    }
-    for (; q < hi16; q += W) {
-      const int c = col_of(a.ids16[q], rbase, a.n_tc);
-      const v4i b0 = load_w16(a, q, jb, 0, lane), b1 = load_w16(a, q, jb, 1, lane);
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        const v4i a0 = load_xf(a, n0 + tb * 16 + arow, c * 64 + akq * 8);
-        const v4i a1 = load_xf(a, n0 + tb * 16 + arow, c * 64 + 32 + akq * 8);
-        acc[tb] = mfma16<XT>(a0, b0, acc[tb]);
-        acc[tb] = mfma16<XT>(a1, b1, acc[tb]);
-      }
-    }
-  }
-
-  reduce_store<TB>(a, red, acc, W, wave, lane, r, jb, n0);
 }
 
 // ---- split-K decode kernel (N <= 64 tokens) ---------------------------------
@@ -422,10 +276,12 @@ __device__ inline float quant_col_tile(const GemmArgs& a, const XSlice<NPOW, XVE
 // cross-workgroup reduction).  Launch bound: 16 waves at JBW 1, 8 at JBW 4.
 // XBLK: the codes are token-blocked (a.xblk blocks of 16 rows per column
 // tile): each activation operand is one contiguous 1 KiB load.
-template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW, bool XBLK = false>
+template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW, bool XBLK = false, bool DUMP = false>
 __global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
 gemm_splitk_kernel(GemmArgs a) {
   static_assert(!(XBLK && FUSED), "the fused prologue stages its own codes");
+  // a batch of U tiles must never straddle two 64-tile metadata windows
+  static_assert(64 % U == 0, "U must divide the 64-tile window");
   // dynamic LDS: FUSED codes [n][64*n_tc] + sx[n_tc] during the main loop,
   // the wave partials for the reduction afterwards (the two never overlap in time)
   extern __shared__ float red[];
@@ -562,6 +418,7 @@ gemm_splitk_kernel(GemmArgs a) {
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
               const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[u][tb], bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
+              dump_i32<DUMP>(a, p0 + u * W, tb * 16 + 4 * akq, (jb0 + j) * 16 + arow, d);
 #pragma unroll
               for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
             }
@@ -718,7 +575,7 @@ __device__ inline int w8_lane_offset(int layout, int lane) {
   return layout == TQ_LAYOUT_MFMA ? lane * 16 : (lane & 15) * 64 + (lane >> 4) * 16;
 }
 
-template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP = false>
 __global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
 gemm_decode_kernel(GemmArgs a) {
   extern __shared__ __align__(16) int8_t dsm[];
@@ -916,6 +773,7 @@ gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
           for (int j = 0; j < JBW; ++j) {
             const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, bw[u][j], v4i{0, 0, 0, 0}, 0, 0, 0);
+            dump_i32<DUMP>(a, lo8 + q0 + u * W, tb * 16 + 4 * akq, (jb0 + j) * 16 + arow, d);
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[j][tb][v] = fmaf((float)d[v], sc, acc[j][tb][v]);
           }
@@ -1031,7 +889,7 @@ constexpr int kPfTokens = 256;                  // tokens per workgroup
 constexpr int kPfThreads = 256;                 // 4 waves
 constexpr int kPfXBytes = kPfTokens * 64;       // activation slice per K step
 
-template <class XT>
+template <class XT, bool DUMP = false>
 __global__ void __launch_bounds__(kPfThreads)
 gemm_prefill_kernel(GemmArgs a) {
   __shared__ __align__(16) int8_t wbuf[2][4096];
@@ -1101,6 +959,7 @@ gemm_prefill_kernel(GemmArgs a) {
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+        dump_i32<DUMP>(a, p, n0 + wave * 64 + tb * 16 + 4 * akq, jb * 16 + arow, d);
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], sc, acc[tb][jb][v]);
       }
@@ -1193,7 +1052,7 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((V & 0xF) | ((V >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <class XT, int P>
+template <class XT, int P, bool DUMP = false>
 __global__ void __launch_bounds__(kPfThreads)
 gemm_prefill_async_kernel(GemmArgs a) {
   __shared__ __align__(16) int8_t smem[P * kPfStage];
@@ -1263,7 +1122,8 @@ gemm_prefill_async_kernel(GemmArgs a) {
     // registers).
     auto step = [&](int p, v4i (&dnew)[4][4], float& snew) {
       const int stage = (p - base) % P;
-      wait_vmcnt<5 * (P - 2)>();
+      if constexpr (DUMP) wait_vmcnt<0>();   // stores count in vmcnt too
+      else wait_vmcnt<5 * (P - 2)>();
       // s_barrier without __syncthreads' release fence: that fence waits for
       // every outstanding load (vmcnt(0)), in-flight DMA included.  The DMA
       // writes are ordered by the vmcnt wait above; the asm LDS reads below
@@ -1301,7 +1161,16 @@ gemm_prefill_async_kernel(GemmArgs a) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
           dnew[tb][jb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+      if constexpr (DUMP) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) dump_i32<DUMP>(a, p, n0 + wave * 64 + tb * 16 + 4 * akq, jb * 16 + arow, dnew[tb][jb]);
+      }
       snew = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc)));
+      // gfx9 counts stores in vmcnt too: drain the dump's stores so the next
+      // step's vmcnt wait counts ring loads only
+      if constexpr (DUMP) wait_vmcnt<0>();
     };
     auto epilogue = [&](const v4i (&d)[4][4], float sc) {
 #pragma unroll
@@ -1399,7 +1268,7 @@ constexpr int kP3Stage = kPfXBytes + 2 * 4096;
 constexpr int kP3Stages = 4;
 constexpr int kP3MaxCols = 512;   // k <= 32768
 
-template <class XT>
+template <class XT, bool DUMP = false>
 __global__ void __launch_bounds__(kP3Threads)
 gemm_prefill_v3_kernel(GemmArgs a) {
   __shared__ __align__(16) int8_t smem[kP3Stages * kP3Stage];
@@ -1475,7 +1344,8 @@ gemm_prefill_v3_kernel(GemmArgs a) {
 
     for (int c = 0; c < n_tc; ++c) {
       const int stage = c % P;
-      wait_vmcnt<3 * (P - 2)>();
+      if constexpr (DUMP) wait_vmcnt<0>();   // stores count in vmcnt too
+      else wait_vmcnt<3 * (P - 2)>();
       asm volatile("s_barrier" ::: "memory");
       const int cn = min(c + P - 1, n_tc - 1);
       int pn, pc;
@@ -1514,9 +1384,11 @@ gemm_prefill_v3_kernel(GemmArgs a) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
           const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+          dump_i32<DUMP>(a, __builtin_amdgcn_readfirstlane(pc), n0 + tq * 64 + tb * 16 + 4 * akq, jb * 16 + arow, d);
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[tb][jb][v] = fmaf((float)d[v], scu, acc[tb][jb][v]);
         }
+      if constexpr (DUMP) wait_vmcnt<0>();   // the dump's stores count in vmcnt: keep the ring's count exact
     }
     wait_vmcnt<0>();   // drain the re-issued tail loads
   }
@@ -1598,8 +1470,10 @@ constexpr int kP5MaxCols = 304;   // k <= 19456 (Qwen2.5-7B down: 296 column til
 constexpr int kP5OutRow = 272;    // LDS bytes per staged output row (256 + 16: no bank conflicts)
 static_assert(4 * 64 * kP5OutRow <= kP5Stages * kP3Stage, "output staging fits the ring");
 
-template <class XT>
-__global__ void __launch_bounds__(kP5Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// DUMP instantiations run one wave per SIMD: the dump's addresses then fit in
+// registers (at two waves per SIMD they spilled to scratch).
+template <class XT, bool DUMP = false>
+__global__ void __launch_bounds__(kP5Threads) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 : 2, DUMP ? 1 : 2)))
 gemm_prefill_v5_kernel(GemmArgs a) {
   __shared__ __align__(16) int8_t smem[kP5Stages * kP3Stage];
   __shared__ int pos8[2][kP5MaxCols];
@@ -1807,7 +1681,10 @@ gemm_prefill_v5_kernel(GemmArgs a) {
     auto step = [&](auto mode_tag, int s) {
       constexpr int MODE = decltype(mode_tag)::value;
       const int stage = s % P;
-      wait_vmcnt<6 * (P - 2)>();
+      // DUMP: every vector memory operation drained (stores and any spill
+      // traffic count in vmcnt too), so stage s has certainly landed
+      if constexpr (DUMP) wait_vmcnt<0>();
+      else wait_vmcnt<6 * (P - 2)>();
       asm volatile("s_barrier" ::: "memory");
       const int sn = min(s + P - 1, S - 1);
       constexpr bool is8 = MODE == 0;
@@ -1869,6 +1746,10 @@ gemm_prefill_v5_kernel(GemmArgs a) {
               "=&v"(bw[4]), "=&v"(bw[5]), "=&v"(bw[6]), "=&v"(bw[7])
             : "v"(w_rd + so), "v"(x_rd + so)
             : "memory");
+        if constexpr (DUMP)   // all 12 reads landed: the partial lgkmcnt waits below are then no-ops
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]), "+v"(ax[0]), "+v"(ax[1]),
+                         "+v"(ax[2]), "+v"(ax[3]), "+v"(bw[4]), "+v"(bw[5]), "+v"(bw[6]), "+v"(bw[7])::"memory");
         // wait for the reads up to token block tb (row 0) -- outstanding <= 7 - tb
         auto wait_tb = [&](int tb) {
           if (tb == 0) asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]), "+v"(ax[0]) :: "memory");
@@ -1877,7 +1758,7 @@ gemm_prefill_v5_kernel(GemmArgs a) {
           else asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ax[3]) :: "memory");
         };
         // one row tile's 16 MFMAs (+ epilogue), with a load part issued after the first 8
-        auto row_mfma = [&](auto j_tag, float sc, int part, bool first) {
+        auto row_mfma = [&](auto j_tag, float sc, int part, bool first, int pos) {
           constexpr int J = decltype(j_tag)::value;
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
@@ -1890,19 +1771,23 @@ gemm_prefill_v5_kernel(GemmArgs a) {
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
               const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[tb], bw[J + jb], v4i{0, 0, 0, 0}, 0, 0, 0);
+              dump_i32<DUMP>(a, pos, n0 + wave * 64 + tb * 16 + 4 * akq, jb * 16 + arow, d);
 #pragma unroll
               for (int v = 0; v < 4; ++v) acc[tb][J + jb][v] = fmaf((float)d[v], sc, acc[tb][J + jb][v]);
             }
           }
         };
-        if (h0) row_mfma(std::integral_constant<int, 0>{}, s0, 1, true);
+        if (h0) row_mfma(std::integral_constant<int, 0>{}, s0, 1, true, meta0 >> 9);
         else issue_part(sn, dst, dmeta, 1);
         // everything else (row 1's weights; row 0's operands when row 0 took no MFMAs)
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(bw[4]), "+v"(bw[5]), "+v"(bw[6]), "+v"(bw[7]), "+v"(ax[0]), "+v"(ax[1]), "+v"(ax[2]),
                        "+v"(ax[3]) :: "memory");
-        if (h1) row_mfma(std::integral_constant<int, 4>{}, s1, 2, false);
+        if (h1) row_mfma(std::integral_constant<int, 4>{}, s1, 2, false, __builtin_amdgcn_readfirstlane(m1) >> 9);
         else issue_part(sn, dst, dmeta, 2);
+        // gfx9 counts stores in vmcnt too: drain the dump's stores so the next
+        // step's vmcnt wait counts ring loads only
+        if constexpr (DUMP) wait_vmcnt<0>();
       } else {
         v4i ax[4], bw[4];
         asm volatile(
@@ -1995,14 +1880,6 @@ gemm_prefill_v5_kernel(GemmArgs a) {
 
 static int pick_tb(int n) { return n <= 16 ? 1 : (n <= 32 ? 2 : 4); }
 
-// The INT32 tile-product dump (test entry) runs gemm_rows_kernel's DUMP
-// instantiation: one j-block per workgroup, 16-token blocks, 4 waves.
-static hipError_t launch_dump(const GemmArgs& a, hipStream_t s) {
-  dim3 grid(a.n_tr * 4, (a.n + 15) / 16), block(4 * kWave);
-  hipLaunchKernelGGL((gemm_rows_kernel<Bf16, 1, true>), grid, block, 0, s, a);
-  return hipGetLastError();
-}
-
 static bool xvec_ok(const GemmArgs& a) {
   return a.k == a.n_tc * 64 && (a.ldq % 16) == 0 && aligned16(a.xq) &&
          (a.xf == nullptr || ((a.ldx % 8) == 0 && aligned16(a.xf)));
@@ -2052,12 +1929,8 @@ static int plan_max_waves(int jbw, int tb) {
 // falls back to gemm_splitk_kernel where gemm_decode_kernel cannot stage the
 // activation).  About UMAX tiles per wave; at most 8 waves for whole-tile
 // (JBW 4) workgroups.
-#ifndef TQ_DEC_UMAX_JB1
-#define TQ_DEC_UMAX_JB1 8
-#endif
-#ifndef TQ_DEC_UMAX_JB4
-#define TQ_DEC_UMAX_JB4 6
-#endif
+constexpr int kDecUmaxJb1 = 8;   // one-j-block workgroups: tiles per wave and batch
+constexpr int kDecUmaxJb4 = 6;   // whole-tile workgroups
 // Grids of more than kDecManyUnits one-j-block workgroups run several per CU;
 // there a wave count that is not a multiple of 4 (e.g. 6 waves for 48 column
 // tiles) leaves wave slots of the four SIMDs unusable, and only ~3 of the 4
@@ -2071,7 +1944,7 @@ static bool decode_wide_batches(int jbw, int tb, int units, int n_tc) {
 }
 static int decode_umax(int jbw, int tb, int units, int n_tc) {
   if (decode_wide_batches(jbw, tb, units, n_tc)) return n_tc <= 48 ? 12 : 16;
-  return jbw == 1 ? TQ_DEC_UMAX_JB1 : TQ_DEC_UMAX_JB4;
+  return jbw == 1 ? kDecUmaxJb1 : kDecUmaxJb4;
 }
 static int decode_waves(int jbw, int tb, int units, int n_tc) {
   const int umax = decode_umax(jbw, tb, units, n_tc);
@@ -2123,29 +1996,39 @@ static hipError_t launch_split_kernel(dim3 grid, dim3 block, size_t lds, hipStre
   return hipGetLastError();
 }
 
-template <class XT, bool FUSED, bool XVEC, int JBW>
+template <class XT, bool FUSED, bool XVEC, int JBW, bool DUMP>
 static hipError_t launch_split_v(const GemmArgs& a, const SplitPlan& p, dim3 grid, dim3 block, size_t lds,
                                  hipStream_t s) {
   constexpr int U1 = JBW == 1 ? 8 : 4, U2 = JBW == 1 ? 4 : 2, U4 = JBW == 1 ? 4 : 2;
   if constexpr (FUSED) {
     const int n = a.n;
-    if (n <= 1) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW>>(grid, block, lds, s, a);
-    if (n <= 2) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW>>(grid, block, lds, s, a);
-    if (n <= 4) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW>>(grid, block, lds, s, a);
-    if (n <= 8) return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW>>(grid, block, lds, s, a);
-    return launch_split_kernel<gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW>>(grid, block, lds,
-                                                                                                   s, a);
+    if (n <= 1)
+      return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 1, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+    if (n <= 2)
+      return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 2, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+    if (n <= 4)
+      return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 4, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+    if (n <= 8)
+      return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, true, 8, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+    return launch_split_kernel<gemm_splitk_kernel<XT, 1, (U1 > 4 ? 4 : U1), true, 16, XVEC, JBW, false, DUMP>>(
+        grid, block, lds, s, a);
   } else if (a.xblk > 0) {
     switch (p.tb) {
-      case 1: return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, true, JBW, true>>(grid, block, lds, s, a);
-      case 2: return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, true, JBW, true>>(grid, block, lds, s, a);
-      default: return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, true, JBW, true>>(grid, block, lds, s, a);
+      case 1:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, true, JBW, true, DUMP>>(grid, block, lds, s, a);
+      case 2:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, true, JBW, true, DUMP>>(grid, block, lds, s, a);
+      default:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, true, JBW, true, DUMP>>(grid, block, lds, s, a);
     }
   } else {
     switch (p.tb) {
-      case 1: return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
-      case 2: return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
-      default: return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW>>(grid, block, lds, s, a);
+      case 1:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 1, U1, false, 1, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+      case 2:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 2, U2, false, 1, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
+      default:
+        return launch_split_kernel<gemm_splitk_kernel<XT, 4, U4, false, 1, XVEC, JBW, false, DUMP>>(grid, block, lds, s, a);
     }
   }
 }
@@ -2155,7 +2038,7 @@ static size_t fused_lds_bytes(int n, int n_tc) {
   return (((size_t)n * n_tc * 64 + 15) & ~(size_t)15) + (size_t)n_tc * sizeof(float);
 }
 
-template <class XT, bool FUSED>
+template <class XT, bool FUSED, bool DUMP = false>
 static hipError_t launch_split(GemmArgs a, const SplitPlan& p, float* ws, hipStream_t s) {
   a.splits = p.S;
   const int units = a.n_tr * (4 / p.jbw);
@@ -2165,10 +2048,10 @@ static hipError_t launch_split(GemmArgs a, const SplitPlan& p, float* ws, hipStr
   size_t lds = (size_t)p.W * p.jbw * p.tb * 4 * 64 * sizeof(float);
   if (FUSED && fused_lds_bytes(a.n, a.n_tc) > lds) lds = fused_lds_bytes(a.n, a.n_tc);
   if (p.jbw == 4)
-    return a.xvec ? launch_split_v<XT, FUSED, true, 4>(a, p, grid, block, lds, s)
-                  : launch_split_v<XT, FUSED, false, 4>(a, p, grid, block, lds, s);
-  return a.xvec ? launch_split_v<XT, FUSED, true, 1>(a, p, grid, block, lds, s)
-                : launch_split_v<XT, FUSED, false, 1>(a, p, grid, block, lds, s);
+    return a.xvec ? launch_split_v<XT, FUSED, true, 4, DUMP>(a, p, grid, block, lds, s)
+                  : launch_split_v<XT, FUSED, false, 4, DUMP>(a, p, grid, block, lds, s);
+  return a.xvec ? launch_split_v<XT, FUSED, true, 1, DUMP>(a, p, grid, block, lds, s)
+                : launch_split_v<XT, FUSED, false, 1, DUMP>(a, p, grid, block, lds, s);
 }
 
 // Chooses the split plan and checks the workspace; without a (large enough)
@@ -2215,40 +2098,40 @@ static DecodePlan plan_decode(int n, int k, int n_tr, int n_tc, bool quant) {
   return p;
 }
 
-template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX>
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP>
 static hipError_t launch_decode_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
-  constexpr auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX>;
+  constexpr auto kern = gemm_decode_kernel<XT, TB, JBW, UMAX, QUANT, CMAX, DUMP>;
   const hipError_t e = allow_lds<kern>(p.lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(a.n_tr * (4 / JBW)), dim3(p.W * kWave), p.lds, s, a);
   return hipGetLastError();
 }
 
-template <class XT, int TB, int JBW, int UMAX, bool QUANT>
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, bool DUMP>
 static hipError_t launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   switch (p.cmax) {
-    case 1: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 1>(a, p, s);
-    case 2: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 2>(a, p, s);
-    case 4: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 4>(a, p, s);
+    case 1: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 1, DUMP>(a, p, s);
+    case 2: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 2, DUMP>(a, p, s);
+    case 4: return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 4, DUMP>(a, p, s);
     default:
-      if constexpr (!QUANT) return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 8>(a, p, s);
+      if constexpr (!QUANT) return launch_decode_one<XT, TB, JBW, UMAX, QUANT, 8, DUMP>(a, p, s);
       return hipErrorInvalidValue;   // QUANT plans stop at 4 chunks
   }
 }
 
-template <class XT, bool QUANT>
+template <class XT, bool QUANT, bool DUMP = false>
 static hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   if (p.jbw == 4) {
-    if constexpr (QUANT) return launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, true>(a, p, s);
-    else if (p.tb == 1) return launch_decode_c<XT, 1, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
-    else return launch_decode_c<XT, 2, 4, TQ_DEC_UMAX_JB4, false>(a, p, s);
+    if constexpr (QUANT) return launch_decode_c<XT, 1, 4, kDecUmaxJb4, true, DUMP>(a, p, s);
+    else if (p.tb == 1) return launch_decode_c<XT, 1, 4, kDecUmaxJb4, false, DUMP>(a, p, s);
+    else return launch_decode_c<XT, 2, 4, kDecUmaxJb4, false, DUMP>(a, p, s);
   }
-  // p.umax is TQ_DEC_UMAX_JB1 except for many-unit grids with one token block
-  if (p.tb == 1 && p.umax == 12) return launch_decode_c<XT, 1, 1, 12, QUANT>(a, p, s);
-  if (p.tb == 1 && p.umax == 16) return launch_decode_c<XT, 1, 1, 16, QUANT>(a, p, s);
-  if constexpr (QUANT) return launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, true>(a, p, s);
-  else if (p.tb == 1) return launch_decode_c<XT, 1, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
-  else return launch_decode_c<XT, 2, 1, TQ_DEC_UMAX_JB1, false>(a, p, s);
+  // p.umax is kDecUmaxJb1 except for many-unit grids with one token block
+  if (p.tb == 1 && p.umax == 12) return launch_decode_c<XT, 1, 1, 12, QUANT, DUMP>(a, p, s);
+  if (p.tb == 1 && p.umax == 16) return launch_decode_c<XT, 1, 1, 16, QUANT, DUMP>(a, p, s);
+  if constexpr (QUANT) return launch_decode_c<XT, 1, 1, kDecUmaxJb1, true, DUMP>(a, p, s);
+  else if (p.tb == 1) return launch_decode_c<XT, 1, 1, kDecUmaxJb1, false, DUMP>(a, p, s);
+  else return launch_decode_c<XT, 2, 1, kDecUmaxJb1, false, DUMP>(a, p, s);
 }
 
 }  // namespace tq
@@ -2271,6 +2154,10 @@ static int check_gemm_common(int n, int m, int k, int n_tr, int n_tc, int x_dtyp
   return TQ_OK;
 }
 
+// Launches the GEMM the automatic schedule picks for this shape (or, with
+// DUMP, that kernel's DUMP instantiation, bf16 activations only) and, when
+// `kernel` is non-null, stores its TQ_KERNEL_* family there.
+template <bool DUMP>
 static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
                            const int8_t* int8_tiles, const float* int8_scales,
                            const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
@@ -2280,11 +2167,12 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
                            int out_dtype, const void* bias, int n, int m, int k, int n_tr,
                            int n_tc, int split_k, int tile_layout, float* workspace,
                            int64_t workspace_elems, const int32_t* units, int n_units, int n_first,
-                           void* stream) {
+                           int32_t* dump, int dump_r0, int dump_n, int* kernel, void* stream) {
   const bool xblk = (tile_layout & TQ_XQ_TOKEN_BLOCKED) != 0;   // token-blocked codes
   tile_layout &= ~TQ_XQ_TOKEN_BLOCKED;
   int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
   if (rc) return rc;
+  if (DUMP && x_dtype != TQ_DTYPE_BF16) return TQ_ERR_DTYPE;
   if (units != nullptr && (n_units < 1 || n_units > n_tr || n_first < 0 || n_first > n_units))
     return TQ_ERR_ARG;
   if (xblk && (n > kDecodeMaxTokens || k != n_tc * 64)) return TQ_ERR_ARG;
@@ -2295,6 +2183,7 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
   const bool has16 = fp16_tiles != nullptr && fp16_tile_ids != nullptr && fp16_row_ptr != nullptr;
   if (has16 && (x_fp == nullptr || x_fp_stride_n < k)) return TQ_ERR_ARG;
   if (!aligned16(int8_tiles) || (has16 && !aligned16(fp16_tiles))) return TQ_ERR_ALIGN;
+  if (DUMP && (dump == nullptr || dump_r0 < 0 || dump_n < 1 || dump_n > n - dump_r0)) return TQ_ERR_ARG;
   GemmArgs a{};
   a.xq = x_int8; a.ldq = x_int8_stride_n; a.sx = sx;
   a.w8 = int8_tiles; a.sw8 = int8_scales; a.ids8 = int8_tile_ids; a.rp8 = int8_row_ptr;
@@ -2303,6 +2192,7 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
   a.ids16 = fp16_tile_ids; a.rp16 = fp16_row_ptr;
   a.out = static_cast<uint16_t*>(out); a.ldo = out_stride_n;
   a.bias = static_cast<const uint16_t*>(bias);
+  a.dump = dump; a.dump_r0 = dump_r0; a.dump_n = dump_n;
   a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
   a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
   a.layout = tile_layout;
@@ -2313,23 +2203,26 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
     if (!a.xvec || !aligned16(x_int8)) return TQ_ERR_ALIGN;
     a.xblk = (n + 15) / 16;
   }
+  int fam = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
-  if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec && !xblk) {
+  if (n <= kDecodeMaxTokens && split_k <= 1 && a.xvec && !xblk && plan_decode(n, k, n_tr, n_tc, false).ok) {
     const DecodePlan d = plan_decode(n, k, n_tr, n_tc, false);
-    if (d.ok)
-      return (int)((x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, false>(a, d, s)
-                                              : launch_decode<Fp16, false>(a, d, s));
-  }
-  if (n <= kDecodeMaxTokens) {
+    fam = TQ_KERNEL_DECODE;
+    if constexpr (DUMP) e = launch_decode<Bf16, false, true>(a, d, s);
+    else e = (x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, false>(a, d, s) : launch_decode<Fp16, false>(a, d, s);
+  } else if (n <= kDecodeMaxTokens) {
     SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
     rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
     if (rc) return rc;
-    e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, false>(a, p, workspace, s)
-                                   : launch_split<Fp16, false>(a, p, workspace, s);
+    fam = xblk ? TQ_KERNEL_SPLITK_TOKEN_BLOCKED : TQ_KERNEL_SPLITK;
+    if constexpr (DUMP) e = launch_split<Bf16, false, true>(a, p, workspace, s);
+    else e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, false>(a, p, workspace, s)
+                                        : launch_split<Fp16, false>(a, p, workspace, s);
   } else {
     dim3 grid(n_tr, (n + kPfTokens - 1) / kPfTokens), block(kPfThreads);
     const int64_t v5_blocks = (int64_t)(units != nullptr ? n_units : (n_tr + 1) / 2) * ((n + kPfTokens - 1) / kPfTokens);
+    const bool bf = DUMP || x_dtype == TQ_DTYPE_BF16;
     if (a.xvec && n_tc <= kP5MaxCols && (a.w16 == nullptr || a.xf != nullptr) && (int64_t)n_tr * n_tc < (1 << 22) &&
         v5_blocks < (1ll << 31)) {
       // DMA ring, 64 x 128 wave tiles, 16-bit tiles in the ring
@@ -2339,21 +2232,26 @@ static int gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n, const 
         a.units = units; a.n_units = n_units; a.n_first = n_first;
         g5 = dim3(n_units * ntb, 1);
       }
-      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v5_kernel<Bf16>, g5, dim3(kP5Threads), 0, s, a);
+      fam = TQ_KERNEL_PREFILL_V5;
+      if (bf) hipLaunchKernelGGL((gemm_prefill_v5_kernel<Bf16, DUMP>), g5, dim3(kP5Threads), 0, s, a);
       else hipLaunchKernelGGL(gemm_prefill_v5_kernel<Fp16>, g5, dim3(kP5Threads), 0, s, a);
     } else if (a.xvec && n_tc <= kP3MaxCols) {   // DMA path, two row tiles per workgroup
       const dim3 g3((n_tr + 1) / 2, (n + kPfTokens - 1) / kPfTokens);
-      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_v3_kernel<Bf16>, g3, dim3(kP3Threads), 0, s, a);
+      fam = TQ_KERNEL_PREFILL_V3;
+      if (bf) hipLaunchKernelGGL((gemm_prefill_v3_kernel<Bf16, DUMP>), g3, dim3(kP3Threads), 0, s, a);
       else hipLaunchKernelGGL(gemm_prefill_v3_kernel<Fp16>, g3, dim3(kP3Threads), 0, s, a);
     } else if (a.xvec) {   // DMA path: whole 16-byte activation chunks, aligned rows
-      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL((gemm_prefill_async_kernel<Bf16, kPfStages>), grid, block, 0, s, a);
+      fam = TQ_KERNEL_PREFILL_ASYNC;
+      if (bf) hipLaunchKernelGGL((gemm_prefill_async_kernel<Bf16, kPfStages, DUMP>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((gemm_prefill_async_kernel<Fp16, kPfStages>), grid, block, 0, s, a);
     } else {
-      if (x_dtype == TQ_DTYPE_BF16) hipLaunchKernelGGL(gemm_prefill_kernel<Bf16>, grid, block, 0, s, a);
+      fam = TQ_KERNEL_PREFILL_REGISTER;
+      if (bf) hipLaunchKernelGGL((gemm_prefill_kernel<Bf16, DUMP>), grid, block, 0, s, a);
       else hipLaunchKernelGGL(gemm_prefill_kernel<Fp16>, grid, block, 0, s, a);
     }
     e = hipGetLastError();
   }
+  if (kernel != nullptr) *kernel = fam;
   return (int)e;
 }
 
@@ -2366,10 +2264,10 @@ extern "C" int tq_gemm_mixed_rows(const int8_t* x_int8, int64_t x_int8_stride_n,
                                   int out_dtype, const void* bias, int n, int m, int k, int n_tr,
                                   int n_tc, int split_k, int tile_layout, float* workspace,
                                   int64_t workspace_elems, void* stream) {
-  return gemm_mixed_rows(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+  return gemm_mixed_rows<false>(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
                          x_fp, x_fp_stride_n, x_dtype, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out,
                          out_stride_n, out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
-                         workspace_elems, nullptr, 0, 0, stream);
+                         workspace_elems, nullptr, 0, 0, nullptr, 0, 0, nullptr, stream);
 }
 
 extern "C" int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx,
@@ -2382,10 +2280,10 @@ extern "C" int tq_gemm_mixed_rows_planned(const int8_t* x_int8, int64_t x_int8_s
                                           int n_tc, int split_k, int tile_layout, float* workspace,
                                           int64_t workspace_elems, const int32_t* prefill_units,
                                           int n_units, int n_first, void* stream) {
-  return gemm_mixed_rows(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+  return gemm_mixed_rows<false>(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
                          x_fp, x_fp_stride_n, x_dtype, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out,
                          out_stride_n, out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
-                         workspace_elems, prefill_units, n_units, n_first, stream);
+                         workspace_elems, prefill_units, n_units, n_first, nullptr, 0, 0, nullptr, stream);
 }
 
 // Prefill work plan (host code).  Cost of a unit in ring steps of a pair's
@@ -2480,6 +2378,56 @@ extern "C" int tq_linear_mixed_fused_max_tokens(int k) {
   return n;
 }
 
+template <bool DUMP>
+static int linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype, const int8_t* int8_tiles,
+                              const float* int8_scales, const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
+                              const void* fp16_tiles, const int32_t* fp16_tile_ids, const int32_t* fp16_row_ptr,
+                              void* out, int64_t out_stride_n, int out_dtype, const void* bias, int n, int m, int k,
+                              int n_tr, int n_tc, int split_k, int tile_layout, float* workspace,
+                              int64_t workspace_elems, int32_t* dump, int dump_r0, int dump_n, int* kernel,
+                              void* stream) {
+  int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
+  if (rc) return rc;
+  if (DUMP && x_dtype != TQ_DTYPE_BF16) return TQ_ERR_DTYPE;
+  if (n > kFusedMaxTokens || fused_lds_bytes(n, n_tc) > kFusedMaxLds) return TQ_ERR_ARG;
+  if (n == 0 || m == 0) return TQ_OK;
+  if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_fp == nullptr || x_fp_stride_n < k)
+    return TQ_ERR_ARG;
+  const bool has16 = fp16_tiles != nullptr && fp16_tile_ids != nullptr && fp16_row_ptr != nullptr;
+  if (!aligned16(int8_tiles) || (has16 && !aligned16(fp16_tiles))) return TQ_ERR_ALIGN;
+  if (DUMP && (dump == nullptr || dump_r0 < 0 || dump_n < 1 || dump_n > n - dump_r0)) return TQ_ERR_ARG;
+  GemmArgs a{};
+  a.w8 = int8_tiles; a.sw8 = int8_scales; a.ids8 = int8_tile_ids; a.rp8 = int8_row_ptr;
+  a.xf = static_cast<const uint16_t*>(x_fp); a.ldx = x_fp_stride_n;
+  a.w16 = has16 ? static_cast<const uint16_t*>(fp16_tiles) : nullptr;
+  a.ids16 = fp16_tile_ids; a.rp16 = fp16_row_ptr;
+  a.out = static_cast<uint16_t*>(out); a.ldo = out_stride_n;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.dump = dump; a.dump_r0 = dump_r0; a.dump_n = dump_n;
+  a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
+  a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
+  a.layout = tile_layout;
+  a.xvec = (k == n_tc * 64 && (x_fp_stride_n % 8) == 0 && aligned16(x_fp)) ? 1 : 0;
+  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (split_k <= 1 && a.xvec && plan_decode(n, k, n_tr, n_tc, true).ok) {
+    const DecodePlan d = plan_decode(n, k, n_tr, n_tc, true);
+    if (kernel != nullptr) *kernel = TQ_KERNEL_DECODE_QUANT;
+    if constexpr (DUMP) e = launch_decode<Bf16, true, true>(a, d, s);
+    else e = (x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, true>(a, d, s) : launch_decode<Fp16, true>(a, d, s);
+    return (int)e;
+  }
+  SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
+  rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
+  if (rc) return rc;
+  if (kernel != nullptr) *kernel = TQ_KERNEL_SPLITK_QUANT;
+  if constexpr (DUMP) e = launch_split<Bf16, true, true>(a, p, workspace, s);
+  else e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, true>(a, p, workspace, s)
+                                      : launch_split<Fp16, true>(a, p, workspace, s);
+  return (int)e;
+}
+
 extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
                                      const int8_t* int8_tiles, const float* int8_scales,
                                      const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
@@ -2488,39 +2436,10 @@ extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, in
                                      int out_dtype, const void* bias, int n, int m, int k, int n_tr,
                                      int n_tc, int split_k, int tile_layout, float* workspace,
                                      int64_t workspace_elems, void* stream) {
-  int rc = check_gemm_common(n, m, k, n_tr, n_tc, x_dtype, out_dtype, tile_layout);
-  if (rc) return rc;
-  if (n > kFusedMaxTokens || fused_lds_bytes(n, n_tc) > kFusedMaxLds) return TQ_ERR_ARG;
-  if (n == 0 || m == 0) return TQ_OK;
-  if (out == nullptr || out_stride_n < m || int8_row_ptr == nullptr || x_fp == nullptr || x_fp_stride_n < k)
-    return TQ_ERR_ARG;
-  const bool has16 = fp16_tiles != nullptr && fp16_tile_ids != nullptr && fp16_row_ptr != nullptr;
-  if (!aligned16(int8_tiles) || (has16 && !aligned16(fp16_tiles))) return TQ_ERR_ALIGN;
-  GemmArgs a{};
-  a.w8 = int8_tiles; a.sw8 = int8_scales; a.ids8 = int8_tile_ids; a.rp8 = int8_row_ptr;
-  a.xf = static_cast<const uint16_t*>(x_fp); a.ldx = x_fp_stride_n;
-  a.w16 = has16 ? static_cast<const uint16_t*>(fp16_tiles) : nullptr;
-  a.ids16 = fp16_tile_ids; a.rp16 = fp16_row_ptr;
-  a.out = static_cast<uint16_t*>(out); a.ldo = out_stride_n;
-  a.bias = static_cast<const uint16_t*>(bias);
-  a.n = n; a.m = m; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
-  a.out_bf16 = out_dtype == TQ_DTYPE_BF16;
-  a.layout = tile_layout;
-  a.xvec = (k == n_tc * 64 && (x_fp_stride_n % 8) == 0 && aligned16(x_fp)) ? 1 : 0;
-  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (split_k <= 1 && a.xvec) {
-    const DecodePlan d = plan_decode(n, k, n_tr, n_tc, true);
-    if (d.ok)
-      return (int)((x_dtype == TQ_DTYPE_BF16) ? launch_decode<Bf16, true>(a, d, s)
-                                              : launch_decode<Fp16, true>(a, d, s));
-  }
-  SplitPlan p = plan_split(n, n_tr, n_tc, split_k);
-  rc = resolve_plan(p, n, n_tr, split_k, workspace, workspace_elems);
-  if (rc) return rc;
-  hipError_t e = (x_dtype == TQ_DTYPE_BF16) ? launch_split<Bf16, true>(a, p, workspace, s)
-                                            : launch_split<Fp16, true>(a, p, workspace, s);
-  return (int)e;
+  return linear_mixed_fused<false>(x_fp, x_fp_stride_n, x_dtype, int8_tiles, int8_scales, int8_tile_ids,
+                                   int8_row_ptr, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out, out_stride_n,
+                                   out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
+                                   workspace_elems, nullptr, 0, 0, nullptr, stream);
 }
 
 extern "C" int tq_linear_forward(const tq_linear_desc* d) {
@@ -2541,25 +2460,29 @@ extern "C" int tq_linear_forward(const tq_linear_desc* d) {
                             d->tile_layout, d->workspace, d->workspace_elems, d->stream);
 }
 
-extern "C" int tq_gemm_tile_products_i32(const int8_t* x_int8, int64_t x_int8_stride_n,
-                                         const int8_t* int8_tiles, const int32_t* int8_tile_ids,
-                                         const int32_t* int8_row_ptr, int n, int k, int n_tr, int n_tc,
-                                         int tile_layout, int32_t* products, void* stream) {
-  if (n < 0 || k < 0 || n_tr < 0 || n_tc < 0) return TQ_ERR_ARG;
-  if ((int64_t)n_tc * 64 < k) return TQ_ERR_ARG;
-  if (tile_layout != TQ_LAYOUT_ROW_MAJOR && tile_layout != TQ_LAYOUT_MFMA) return TQ_ERR_DTYPE;
-  if (n == 0 || n_tr == 0) return TQ_OK;
-  if (x_int8 == nullptr || int8_row_ptr == nullptr || products == nullptr || x_int8_stride_n < k)
-    return TQ_ERR_ARG;
-  if (!aligned16(int8_tiles)) return TQ_ERR_ALIGN;
-  GemmArgs a{};
-  a.xq = x_int8; a.ldq = x_int8_stride_n;
-  a.w8 = int8_tiles; a.ids8 = int8_tile_ids; a.rp8 = int8_row_ptr;
-  a.dump = products;
-  a.n = n; a.m = n_tr * 64; a.k = k; a.n_tr = n_tr; a.n_tc = n_tc;
-  a.layout = tile_layout;
-  a.xvec = xvec_ok(a);
-  a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
-  a.sx = nullptr; a.sw8 = nullptr;  // the dump path reads no scales
-  return (int)launch_dump(a, static_cast<hipStream_t>(stream));
+extern "C" int tq_gemm_mixed_rows_products_i32(
+    const int8_t* x_int8, int64_t x_int8_stride_n, const float* sx, const int8_t* int8_tiles,
+    const float* int8_scales, const int32_t* int8_tile_ids, const int32_t* int8_row_ptr, const void* x_fp,
+    int64_t x_fp_stride_n, int x_dtype, const void* fp16_tiles, const int32_t* fp16_tile_ids,
+    const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n, int out_dtype, const void* bias, int n, int m,
+    int k, int n_tr, int n_tc, int split_k, int tile_layout, float* workspace, int64_t workspace_elems,
+    const int32_t* prefill_units, int n_units, int n_first, int32_t* products, int row0, int rows, int* kernel,
+    void* stream) {
+  return gemm_mixed_rows<true>(x_int8, x_int8_stride_n, sx, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr,
+                               x_fp, x_fp_stride_n, x_dtype, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out,
+                               out_stride_n, out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
+                               workspace_elems, prefill_units, n_units, n_first, products, row0, rows, kernel,
+                               stream);
+}
+
+extern "C" int tq_linear_mixed_fused_products_i32(
+    const void* x_fp, int64_t x_fp_stride_n, int x_dtype, const int8_t* int8_tiles, const float* int8_scales,
+    const int32_t* int8_tile_ids, const int32_t* int8_row_ptr, const void* fp16_tiles, const int32_t* fp16_tile_ids,
+    const int32_t* fp16_row_ptr, void* out, int64_t out_stride_n, int out_dtype, const void* bias, int n, int m,
+    int k, int n_tr, int n_tc, int split_k, int tile_layout, float* workspace, int64_t workspace_elems,
+    int32_t* products, int row0, int rows, int* kernel, void* stream) {
+  return linear_mixed_fused<true>(x_fp, x_fp_stride_n, x_dtype, int8_tiles, int8_scales, int8_tile_ids,
+                                  int8_row_ptr, fp16_tiles, fp16_tile_ids, fp16_row_ptr, out, out_stride_n,
+                                  out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
+                                  workspace_elems, products, row0, rows, kernel, stream);
 }

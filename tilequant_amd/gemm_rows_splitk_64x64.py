@@ -141,6 +141,7 @@ def gemm_mixed_rows_splitk(
     tile_layout: str = "row_major",
     prefill_plan: Optional[PrefillPlan] = None,
     x_int8_layout: str = "row_major",
+    _products=None,
 ) -> torch.Tensor:
     """Return x @ W^T (+ bias) for a packed mixed INT8/16-bit weight.
 
@@ -204,6 +205,7 @@ def gemm_mixed_rows_splitk(
             nat.ptr(fp16_row_ptr) if has16 else None,
             nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
             n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout] | layout_flag, ws_ptr, ws_elems)
+    units = None
     if prefill_plan is not None:
         units = prefill_plan.units
         if units.device != x_fp.device or units.dtype != torch.int32 or not units.is_contiguous():
@@ -211,6 +213,14 @@ def gemm_mixed_rows_splitk(
         if (prefill_plan.n_tr != n_tr or not 0 < units.numel() <= n_tr
                 or not 0 <= prefill_plan.n_first <= units.numel()):
             raise ValueError(f"prefill_plan covers {prefill_plan.n_tr} row tiles, the weight has {n_tr}")
+    if _products is not None:   # test-only DUMP launch (gemm_mixed_rows_products_i32)
+        prod, row0, rows, kernel = _products
+        rc = nat.lib().tq_gemm_mixed_rows_products_i32(
+            *args, nat.ptr(units), units.numel() if units is not None else 0,
+            prefill_plan.n_first if units is not None else 0, nat.ptr(prod), row0, rows, ctypes.byref(kernel),
+            nat.stream_handle(x_fp.device))
+        nat.check(rc, "tq_gemm_mixed_rows_products_i32")
+    elif units is not None:
         rc = nat.lib().tq_gemm_mixed_rows_planned(*args, nat.ptr(units), units.numel(), prefill_plan.n_first,
                                                   nat.stream_handle(x_fp.device))
         nat.check(rc, "tq_gemm_mixed_rows_planned")
@@ -239,6 +249,7 @@ def linear_mixed_fused(
     split_k: Optional[int] = None,
     out: Optional[torch.Tensor] = None,
     tile_layout: str = "row_major",
+    _products=None,
 ) -> torch.Tensor:
     """Activation quantization + mixed tile GEMM in ONE launch (decode sizes,
     at most FUSED_MAX_TOKENS rows).  Same result, bit for bit, as
@@ -266,41 +277,49 @@ def linear_mixed_fused(
     if n == 0 or M == 0:
         return out
     ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
-    rc = nat.lib().tq_linear_mixed_fused(
-        nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
-        nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
-        nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
-        nat.ptr(fp16_row_ptr) if has16 else None,
-        nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
-        n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems,
-        nat.stream_handle(x_fp.device))
-    nat.check(rc, "tq_linear_mixed_fused")
+    args = (nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
+            nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
+            nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
+            nat.ptr(fp16_row_ptr) if has16 else None,
+            nat.ptr(out), out.stride(0), nat.dtype_code(out_dtype), nat.ptr(bias),
+            n, M, K, n_tr, n_tc, int(split_k or 0), nat.TQ_LAYOUT[tile_layout], ws_ptr, ws_elems)
+    if _products is not None:   # test-only DUMP launch (gemm_mixed_rows_products_i32)
+        prod, row0, rows, kernel = _products
+        rc = nat.lib().tq_linear_mixed_fused_products_i32(*args, nat.ptr(prod), row0, rows, ctypes.byref(kernel),
+                                                          nat.stream_handle(x_fp.device))
+        nat.check(rc, "tq_linear_mixed_fused_products_i32")
+    else:
+        rc = nat.lib().tq_linear_mixed_fused(*args, nat.stream_handle(x_fp.device))
+        nat.check(rc, "tq_linear_mixed_fused")
     return out
 
 
-def gemm_tile_products_i32(
-    *,
-    x_int8: torch.Tensor,
-    int8_tiles: torch.Tensor,
-    int8_tile_ids: torch.Tensor,
-    int8_row_ptr: torch.Tensor,
-    K: int,
-    n_tr: int,
-    n_tc: int,
-    tile_layout: str = "row_major",
-) -> torch.Tensor:
-    """TEST ONLY: exact INT32 products [T8, N, 64] of every INT8 tile with every
-    token row, from the same device tile routine as the GEMM (the quantity the
-    reference's tl.dot produces at gemm_rows_splitk_64x64.py:134)."""
-    nat.require_device(x_int8, int8_tiles, int8_tile_ids, int8_row_ptr)
-    _check_tiles("int8_tiles", int8_tiles, torch.int8)
-    n = int(x_int8.shape[0])
-    out = torch.zeros((int8_tiles.shape[0], n, 64), device=x_int8.device, dtype=torch.int32)
-    if n == 0 or int8_tiles.shape[0] == 0:
-        return out
-    rc = nat.lib().tq_gemm_tile_products_i32(
-        nat.ptr(x_int8), x_int8.stride(0), nat.ptr(int8_tiles), nat.ptr(int8_tile_ids),
-        nat.ptr(int8_row_ptr), n, int(K), int(n_tr), int(n_tc), nat.TQ_LAYOUT[tile_layout],
-        nat.ptr(out), nat.stream_handle(x_int8.device))
-    nat.check(rc, "tq_gemm_tile_products_i32")
-    return out
+# TQ_KERNEL_* codes of include/tilequant.h
+KERNEL_FAMILIES = {1: "decode", 2: "decode_quant", 3: "splitk", 4: "splitk_token_blocked", 5: "splitk_quant",
+                   6: "prefill_v5", 7: "prefill_v3", 8: "prefill_async", 9: "prefill_register"}
+
+
+def gemm_mixed_rows_products_i32(*, rows: Optional[Tuple[int, int]] = None, fused: bool = False, **kwargs):
+    """TEST ONLY.  Runs ``gemm_mixed_rows_splitk(**kwargs)`` -- or, with
+    ``fused=True``, ``linear_mixed_fused(**kwargs)`` -- through the DUMP
+    instantiation of the very kernel the automatic schedule picks for those
+    arguments, and returns ``(out, products, kernel)``: the usual output, the
+    exact INT32 products int32 [T8, rows, 64] of every INT8 tile with token
+    rows ``row0 .. row0 + count - 1`` (``rows=(row0, count)``, default all) as
+    that kernel's v_mfma_i32_16x16x64_i8 produced them before the scale FMA,
+    and the kernel family's name (``KERNEL_FAMILIES``).  The quantity is the
+    reference's tl.dot(x_i8, w_i8^T) (gemm_rows_splitk_64x64.py:125-137).
+    bf16 activations only."""
+    x_fp = kwargs["x_fp"]
+    n = int(x_fp.shape[0])
+    row0, count = (0, n) if rows is None else (int(rows[0]), int(rows[1]))
+    if not (0 <= row0 and 1 <= count <= n - row0):
+        raise ValueError(f"rows must lie inside the {n} input rows, got {rows}")
+    t8 = int(kwargs["int8_tiles"].shape[0])
+    prod = torch.full((max(t8, 1), count, 64), -2**31, device=x_fp.device, dtype=torch.int32)
+    kernel = ctypes.c_int(0)
+    if fused:
+        out = linear_mixed_fused(**kwargs, _products=(prod, row0, count, kernel))
+    else:
+        out = gemm_mixed_rows_splitk(**kwargs, _products=(prod, row0, count, kernel))
+    return out, prod[:t8], KERNEL_FAMILIES.get(kernel.value, str(kernel.value))
