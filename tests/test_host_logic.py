@@ -133,11 +133,40 @@ def test_mask_io_roundtrip_and_errors(tmp_path):
 
 def test_mask_io_reads_released_archive_like_oracle():
     keep = GOLDEN / "llama32_3b_gi_keep01"
-    amap = mask_io._load_archive_map(keep, 64, 64)
+    arch = mask_io.open_archive(keep)
     oarch = om.read_archive(keep / "fp16_keep_ids_tile64x64.npz")
-    assert set(amap) == set(oarch)
-    for stem in list(amap)[:20]:
-        assert amap[stem][0] == oarch[stem][0] and np.array_equal(amap[stem][1], oarch[stem][1])
+    assert set(arch) == set(oarch) and len(arch) == 196
+    for stem in list(arch)[:20]:
+        assert arch[stem].grid == oarch[stem][0] and np.array_equal(arch[stem].ids, oarch[stem][1])
+        assert arch[stem].ids.dtype == np.uint16
+    assert mask_io.open_archive(keep) is arch   # parsed once per process
+
+
+def test_mask_io_rereads_a_rewritten_archive_and_uint32_ids(tmp_path):
+    """A second save replaces the parsed archive; grids above 65535 tiles
+    store uint32 ids (the released format's rule); stems are sorted."""
+    small = {"b_proj": np.eye(3, dtype=np.uint8), "a_proj": np.zeros((1, 2), np.uint8)}
+    mask_io.save_mask_keep_archive(tmp_path, small)
+    first = mask_io.open_archive(tmp_path)
+    assert list(first) == ["a_proj", "b_proj"] and first["b_proj"].ids.tolist() == [0, 4, 8]
+    big = np.zeros((256, 300), np.uint8)
+    big[255, 299] = 1
+    path = mask_io.save_mask_keep_archive(tmp_path, {"c_proj": big})
+    second = mask_io.open_archive(tmp_path)
+    assert second is not first and list(second) == ["c_proj"]
+    assert second["c_proj"].ids.dtype == np.uint32 and second["c_proj"].ids.tolist() == [256 * 300 - 1]
+    with np.load(path, allow_pickle=False) as npz:
+        assert npz["shape_0"].dtype == np.int32 and npz["ids_0"].dtype == np.uint32
+    with pytest.raises(ValueError, match="2D"):
+        mask_io.save_mask_keep_archive(tmp_path, {"d": np.zeros(3)})
+    with pytest.raises(ValueError, match="empty"):
+        mask_io.save_mask_keep_archive(tmp_path, {})
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    np.savez(bad / "fp16_keep_ids_tile64x64.npz", stems=np.asarray(["s"]), shape_0=np.asarray([2, 2, 1], np.int32),
+             ids_0=np.asarray([1], np.uint16))
+    with pytest.raises(RuntimeError, match="Invalid shape metadata"):
+        mask_io.load_mask_keep_stem_dict(bad)
 
 
 def test_iter_target_linears_on_llama_architecture():
