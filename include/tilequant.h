@@ -343,9 +343,10 @@ int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, c
  * process ends; shapes needing more
  * (tq_decode_attention_workspace_elems(batch, q_heads, max_len) > 4 Mi floats,
  * e.g. batch * q_heads > 504 at long lengths) return TQ_ERR_WORKSPACE.  The
- * stream must belong to the current device.  All calls on one GPU share the
- * array: calls that overlap in time on one GPU (different streams, threads or
- * processes) race and must be serialized by the caller.  Nothing in it needs
+ * stream must belong to the current device.  All calls of one process on one
+ * GPU share the array (each process that loads the library has its own copy):
+ * overlapping calls from the same process on one GPU (different streams or
+ * threads) race and must be serialized by the caller.  Nothing in it needs
  * clearing between calls (each call writes every record it reads).  Results
  * are bitwise those of tq_decode_attention. */
 int tq_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,

@@ -261,3 +261,28 @@ def test_cached_launch_path_equals_uncached_calls(fused_mode, bias, dtype_out):
     lin.to(torch.device("cuda", 0))   # _apply rebuilds nothing here, but the cache is dropped
     assert len(lin._launches) == 0
     assert torch.equal(lin(x), ref) and torch.equal(lin(x.view(1, 4, 3072)).view(4, -1), ref)
+
+
+@pytest.mark.parametrize("dtype_out", ["bf16", "fp16"])
+def test_cached_launch_sees_in_place_bias_updates(dtype_out):
+    """An in-place bias update between two eager decode calls reaches the
+    cached launch path (its descriptor may hold a converted copy of the bias:
+    fp16 outputs from a bf16 bias), exactly as the uncached path sees it."""
+    cfg = SimpleNamespace(quant_style="gi", dtype_out=dtype_out)
+    lin, W, ids16, b = _linear(256, 512, 0.05, 60, cfg, bias=True)
+    x = make_x(4, 512, seed=61).cuda()
+    y0 = lin(x)
+    with torch.no_grad():
+        lin.bias.data.copy_(lin.bias.data * -2 + 1)
+    y1 = lin(x)                       # cached path, same descriptor key but a new bias version
+    out_dtype = torch.bfloat16 if dtype_out == "bf16" else torch.float16
+    xq, sx = _codes(x)
+    ref = lin._gemm_bias(x_fp=x, x_int8=xq, sx=sx)   # uncached quantize + GEMM with the current bias
+    assert not torch.equal(y1, y0) and torch.equal(y1, ref) and y1.dtype == out_dtype
+    assert len(lin._launches) <= 2
+
+
+def _codes(x):
+    from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+
+    return quantize_activation_tile_absmax(x)

@@ -275,6 +275,22 @@ def test_state_dict_without_layout_record_loads_as_row_major():
     assert m.tile_layout == "mfma"
 
 
+def test_partial_state_dict_leaves_the_tile_layout_alone():
+    """A strict=False load of a dict that does not replace this module's tiles
+    (an unrelated parent-model subset, a bias-only dict) must not switch an
+    MFMA-order module to row-major: its tiles stay in the MFMA order."""
+    cfg = SimpleNamespace(dtype_out="bf16")
+    p, _ = _cpu_pack(128, 192, 0.3, 41)
+    p.tile_layout = "mfma"
+    parent = torch.nn.Sequential(torch.nn.Linear(4, 4), MixedLinear(p, torch.zeros(128, dtype=torch.bfloat16), cfg))
+    tiles = parent[1].int8_tiles.clone()
+    for partial in ({"0.weight": torch.ones(4, 4)}, {"1.bias": torch.ones(128, dtype=torch.bfloat16)}, {}):
+        parent.load_state_dict(partial, strict=False)
+        assert parent[1].tile_layout == "mfma", partial
+        assert torch.equal(parent[1].int8_tiles, tiles)
+    assert torch.equal(parent[1].bias, torch.ones(128, dtype=torch.bfloat16))
+
+
 def test_fused_decode_refuses_architectures_it_does_not_compute():
     """Qwen3 (per-head q/k RMSNorm), dynamic RoPE and partial rotary are
     rejected; Llama-3.2 (llama3 RoPE) and Qwen2 are accepted."""

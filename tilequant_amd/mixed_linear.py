@@ -206,18 +206,25 @@ def _quantize_for(module: nn.Module, x: torch.Tensor, x_work: torch.Tensor,
 # Eager inputs of fewer rows than this (and below the sibling-cache threshold,
 # so sharing semantics are unchanged) run through a cached launch descriptor.
 LAUNCH_CACHE_MAX_ROWS = ACTIVATION_QUANT_CACHE_MIN_ROWS - 1
+# Descriptors kept per module (each holds its own scratch codes); the oldest
+# is dropped beyond this.
+LAUNCH_CACHE_MAX_ENTRIES = 64
 
 
 class _Launch:
     """A validated tq_linear_desc for one (rows, layout, stream, weights) key
-    and the scratch it points to; per call only x, out change."""
+    and the scratch it points to; per call only x, out change.  ``bias_copy``
+    is the output-dtype copy of a bias of another dtype (None when the
+    descriptor points at the bias itself): it is refreshed from the live
+    parameter before every launch, so in-place bias updates are always seen."""
 
-    __slots__ = ("desc", "ref", "keep")
+    __slots__ = ("desc", "ref", "keep", "bias_copy")
 
-    def __init__(self, desc, keep) -> None:
+    def __init__(self, desc, keep, bias_copy=None) -> None:
         self.desc = desc
         self.ref = ctypes.byref(desc)
         self.keep = keep   # tensors the descriptor points to
+        self.bias_copy = bias_copy
 
 
 _BUFFERS = ("int8_tiles", "int8_scales", "int8_tile_ids", "int8_row_ptr", "int8_row_indices",
@@ -262,10 +269,12 @@ class MixedLinear(nn.Module):
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                               error_msgs):
-        # A state_dict without the layout record was written by the reference
-        # (or a module packed in its order): its tiles are row-major.
+        # A state_dict that replaces this module's tiles without the layout
+        # record was written by the reference (or a module packed in its
+        # order): its tiles are row-major.  A dict that does not carry the
+        # tiles (a partial strict=False load) leaves the layout alone.
         key = prefix + "_extra_state"
-        if key not in state_dict:
+        if key not in state_dict and (prefix + "int8_tiles" in state_dict or prefix + "fp16_tiles" in state_dict):
             self.tile_layout = "row_major"
         self._launches = {}
         self._plan = None
@@ -401,7 +410,7 @@ class MixedLinear(nn.Module):
             d.fp16_tiles, d.fp16_tile_ids = self.fp16_tiles.data_ptr(), self.fp16_tile_ids.data_ptr()
             d.fp16_row_ptr = self.fp16_row_ptr.data_ptr()
         d.bias = None if bias is None else bias.data_ptr()
-        return _Launch(d, keep)
+        return _Launch(d, keep, bias if bias is not None and bias is not self.bias else None)
 
     def _cached_forward(self, x_work: torch.Tensor) -> torch.Tensor:
         """Decode-size eager forward through a cached launch descriptor: one
@@ -417,7 +426,11 @@ class MixedLinear(nn.Module):
                0 if bias is None else bias.data_ptr(), out_dtype, self.tile_layout, fused, _blockable(x_work))
         launch = self._launches.get(key)
         if launch is None:
+            if len(self._launches) >= LAUNCH_CACHE_MAX_ENTRIES:
+                self._launches.pop(next(iter(self._launches)))
             launch = self._launches[key] = self._build_launch(x_work, stream, out_dtype, fused)
+        if launch.bias_copy is not None:
+            launch.bias_copy.copy_(bias)
         out = torch.empty((n, self.M_orig), device=dev, dtype=out_dtype)
         desc = launch.desc
         desc.x = x_work.data_ptr()
