@@ -78,6 +78,8 @@ def parse():
     ap.add_argument("--released-only", action="store_true", help="run only the released-maps section")
     ap.add_argument("--m-sweep", type=int, default=1,
                     help="also time the decode linear set at 1, 16 and 64 tokens (BASELINE configs[1]); 0 = skip")
+    ap.add_argument("--config0", type=int, default=1,
+                    help="BASELINE configs[0]: one 3072->3072 MixedLinear at 16 tokens, GPU beside the CPU path")
     ap.add_argument("--e2e-batch", type=int, default=4)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-output", type=int, default=256)
@@ -817,6 +819,105 @@ def cpu_baseline(args, layers, xs):
                 "note": "context: torch.nn.functional.linear in bf16 on the same sample and threads"}}
 
 
+def config0_measure(args, device):
+    """ONE MixedLinear 3072 -> 3072 (Llama-3.2-3B q_proj
+    shape), 16 tokens, keep01 uniform (24 of 2304 tiles in bf16), activations
+    N(0, 1) with 15 outlier channels x20.  GPU: the module's forward
+    (activation quantization + mixed tile GEMM, as MixedLinear schedules it)
+    replayed back to back in a HIP graph, HIP events on its stream, per-call
+    average; the same with fresh weights per call is not needed at 9.5 MB (the
+    weights stay in the Infinity Cache, as they would for a single layer
+    called repeatedly).  CPU: the reference's CPU path for the same call --
+    the activation quantization with its torch CPU ops (quant_utils.py:61-74,
+    103-115) and the tile GEMM in its order (oracle/tq_oracle.c, OpenMP) --
+    median of >= 20 calls after 3 warm-ups, on the process's threads."""
+    import numpy as np
+    import torch
+    from oracle import native as onat
+    from oracle import torch_ref
+    from tilequant_amd.mixed_linear import MixedLinear
+    from tilequant_amd.pack import pack_weight_from_tile_ids
+
+    m = k = HIDDEN
+    n = 16
+    g = torch.Generator().manual_seed(args.seed + 100)
+    W = (torch.randn((m, k), generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn((n, k), generator=g)
+    x[:, torch.randperm(k, generator=g)[: round(0.005 * k)]] *= 20
+    x = x.to(torch.bfloat16)
+    n_tr, n_tc = m // 64, k // 64
+    rng = np.random.default_rng(args.seed + 101)
+    ids16 = keep_ids(n_tr, n_tc, 0.01, rng)
+    ids8 = np.setdiff1d(np.arange(n_tr * n_tc), ids16)
+    cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
+    pack = pack_weight_from_tile_ids(W.to(device), n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.from_numpy(ids8),
+                                     fp16_tile_ids=torch.from_numpy(ids16), cfg=cfg, tile_layout="mfma")
+    lin = MixedLinear(pack, None, cfg)
+    xd = x.to(device)
+    reps, per_graph = 50, 100
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            lin(xd)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(per_graph):
+            lin(xd)
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            graph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    gpu_us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+    ops = 2 * n * m * k
+    packed = 4096 * len(ids8) + 8192 * len(ids16) + 4 * len(ids8)
+    # the reference's CPU path on the same call
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    before = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    op = None
+    try:
+        from oracle import numerics as nm
+        from oracle import packing as opk
+
+        op = opk.pack_weight(W.view(torch.int16).numpy().view(np.uint16), ids16)
+        w16 = nm.bf16_bits_to_f32(op.fp16_tiles)
+
+        def cpu_call():
+            xq, sx = torch_ref.act_quant(x)
+            return onat.gemm_mixed(xq.numpy(), sx.numpy(), x.float().numpy(), op.int8_tiles, op.int8_scales,
+                                   op.int8_tile_ids, op.int8_row_ptr, w16, op.fp16_tile_ids, op.fp16_row_ptr,
+                                   n_tr, n_tc, m, k)
+
+        for _ in range(3):
+            cpu_call()
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 20 or (time.perf_counter() - t_start < 2.0 and len(times) < 2000):
+            t0 = time.perf_counter()
+            cpu_call()
+            times.append(time.perf_counter() - t0)
+        cpu_us = statistics.median(times) * 1e6
+    finally:
+        torch.set_num_threads(before)
+    return {"shape": "3072x3072 MixedLinear, 16 tokens, keep01 uniform (24 bf16 tiles)",
+            "gpu": {"us_per_call": gpu_us, "tops": ops / (gpu_us * 1e-6) / 1e12,
+                    "gbps_packed_weights": packed / (gpu_us * 1e-6) / 1e9,
+                    "timing": f"MixedLinear forward x {per_graph} in one HIP graph, HIP events on its stream, "
+                              f"{reps} replays"},
+            "cpu_reference_path": {"us_per_call": cpu_us, "tops": ops / (cpu_us * 1e-6) / 1e12, "cores": threads,
+                                   "cpu_model": _cpu_model(), "reps": len(times),
+                                   "path": "torch CPU activation quantization (quant_utils.py:61-74, 103-115) + "
+                                           "tile GEMM in reference order (oracle/tq_oracle.c, OpenMP)"},
+            "gpu_speedup": cpu_us / gpu_us, "ops": ops, "packed_weight_bytes": packed}
+
+
 def released_maps_measure(args, device):
     """The released Llama-3.2-3B gi tile maps (keep01 for decode, keep05 for
     prefill) instead of seeded uniform ones: the decode linear set at
@@ -1129,6 +1230,7 @@ def main():
         del ws
 
     cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
+    config0 = config0_measure(args, device) if args.config0 else None
     m_sweep = decode_m_sweep(args, device, layers, info) if args.m_sweep else None
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
@@ -1170,6 +1272,7 @@ def main():
                                "step's 112 GEMM launches back to back (activations quantized beforehand); "
                                "per-launch average includes the inter-kernel gaps"},
         "dense_bf16": dense,
+        "config0": config0,
         "decode_m_sweep": m_sweep,
         "prefill": prefill,
         "qwen": qwen,

@@ -385,3 +385,108 @@ def test_llama32_3b_widths_one_layer_tight():
     for t in range(len(fused)):
         assert _rel(fused[t], module[t]) <= 3e-2 and _clear_argmax_agree(fused[t], module[t], 3e-2), t
         assert _rel(fused[t], eager[t]) <= 5e-2 and _clear_argmax_agree(fused[t], eager[t], 5e-2), t
+
+
+def test_llama32_3b_single_steps_from_identical_state():
+    """All 28 layers, batch 4, 2048-token prompt, 256 new tokens.  At decode
+    positions P, P + 64 and P + 254 (the last of the 255 decode steps) the fused
+    decoder's whole state (every
+    layer's K/V cache, the input token, the position and the valid lengths)
+    is copied into a decoder that replays the model's own modules, and each
+    runs ONE step from it (reference decode body: graph_decode.py:350-385), so
+    no divergence accumulates over steps.  Depth still amplifies: this
+    random-initialised 28-layer network turns a single fp32 reordering in one
+    RMSNorm into ~10% of the largest logit within one step.  So the floor is
+    measured at every position: the same module step from the same state with
+    every RMSNorm's mean of squares taken in float64.  Bars: fused-vs-module
+    logits within 1.5x that floor + 1e-2 (and 0.3 absolute), argmax equal
+    where the margin exceeds the floor; the K/V the step writes at layer 0,
+    before anything amplifies, equal within bf16 rounding (2e-2)."""
+    from transformers.models.llama import modeling_llama
+
+    from e2e_models import llama32_3b_config
+    from tilequant_amd import api
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+    from tilequant_amd.types import ApplyConfig
+
+    B, P, O = 4, 2048, 256
+    config = llama32_3b_config()
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), DEV,
+                                               seed=5, keep_frac=0.01)
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(6))
+
+    def load_state(dec, state):
+        with torch.inference_mode():
+            for layer, (k, v) in zip(dec.cache.layers, state[0]):
+                layer.keys.copy_(k)
+                layer.values.copy_(v)
+                # the static cache layer writes at its own device counter of the
+                # tokens it holds (kept equal to the position by the decoder)
+                layer.cumulative_length.copy_(state[2].to(layer.cumulative_length.dtype).view_as(
+                    layer.cumulative_length))
+            dec._token.copy_(state[1])
+            dec._position.copy_(state[2])
+            dec._decode_seq_used.copy_(state[3])
+            if len(state) > 4:
+                dec._generated.copy_(state[4])
+
+    def save_state(dec):
+        return ([(layer.keys.clone(), layer.values.clone()) for layer in dec.cache.layers], dec._token.clone(),
+                dec._position.clone(), dec._decode_seq_used.clone(), dec._generated.clone())
+
+    def entry(dec, pos, layer):
+        return dec.cache.layers[layer].keys[:, :, pos].clone(), dec.cache.layers[layer].values[:, :, pos].clone()
+
+    forward = modeling_llama.LlamaRMSNorm.forward
+
+    def norm_f64(self, hidden_states):
+        dt = hidden_states.dtype
+        h = hidden_states.to(torch.float32)
+        var = h.double().pow(2).mean(-1, keepdim=True).float()
+        return self.weight * (h * torch.rsqrt(var + self.variance_epsilon)).to(dt)
+
+    fused = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV)
+    assert fused._fused is not None and len(fused.cache.layers) == 28
+    fused.prefill(prompt)
+    done, report = 0, []
+    for target in (0, 64, 254):
+        if target > done:
+            fused.decode(target - done)
+            done = target
+        state = save_state(fused)
+        pos = int(state[2].item())
+        assert pos == P + target
+        fused.decode(1)
+        done += 1
+        lf = fused.last_logits[:, -1].float().clone()
+        kf0, vf0 = entry(fused, pos, 0)
+        after = save_state(fused)
+        fused.close()   # one decoder bound to the model at a time
+        ref = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV,
+                                             fused_decode=False, fused_prefill=False)
+        load_state(ref, state)
+        ref._graph.replay()
+        lm = ref._decode_logits[:, -1].float().clone()
+        km0, vm0 = entry(ref, pos, 0)
+        load_state(ref, state)
+        modeling_llama.LlamaRMSNorm.forward = norm_f64
+        try:
+            ref._decode_body()   # the module step eagerly, float64 norm sums
+        finally:
+            modeling_llama.LlamaRMSNorm.forward = forward
+        l64 = ref._decode_logits[:, -1].float().clone()
+        ref.close()
+        e, floor = _rel(lf, lm), _rel(l64, lm)
+        report.append((target, e, floor))
+        assert _rel(kf0, km0) <= 2e-2 and _rel(vf0, vm0) <= 2e-2, f"position P + {target}: layer-0 cache entry"
+        assert e <= 1.5 * floor + 1e-2 and e <= 0.3, f"position P + {target}: {e:.3e} vs floor {floor:.3e}"
+        assert _clear_argmax_agree(lf, lm, max(floor, 3e-2)), f"position P + {target}"
+        if target != 254:   # back to the fused decoder, at its own state after the step
+            fused = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B,
+                                                   device=DEV)
+            fused.prefill(prompt)   # sets the decoder up; its state is then replaced
+            load_state(fused, after)
+            fused._steps_done = done
+        del state, after
+    print("\nsingle steps (position - P, fused-vs-module, float64-norm floor): "
+          + ", ".join(f"({t}, {e:.2e}, {f:.2e})" for t, e, f in report))
