@@ -289,6 +289,8 @@ def qwen_measure(args, device):
     s = torch.cuda.Stream()
 
     def graph_time(fn, reps):
+        # the side stream must see the inputs the default stream produced (packs, codes)
+        s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             fn()
         torch.cuda.synchronize()
@@ -421,6 +423,7 @@ def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
     s = torch.cuda.Stream()
 
     def graph_ms(fn, reps):
+        s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             fn()
         torch.cuda.synchronize()
@@ -973,6 +976,7 @@ def released_maps_measure(args, device):
                                        M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
                                        out_dtype=torch.bfloat16, out=o, tile_layout=lin.tile_layout)
 
+        s.wait_stream(torch.cuda.current_stream())   # the codes come from the default stream
         with torch.cuda.stream(s):
             gemms()
         torch.cuda.synchronize()

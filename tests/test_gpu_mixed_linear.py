@@ -197,6 +197,7 @@ def test_down_width_fused_by_auto_policy_eager_and_graph(n):
     with torch.inference_mode():
         assert torch.equal(auto(x.view(1, n, 8192)).view(n, -1), ref)
     s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         auto(x)
     torch.cuda.synchronize()

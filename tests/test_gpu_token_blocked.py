@@ -161,6 +161,7 @@ def test_mixed_linear_token_blocked_rows_are_bitwise_row_major(m, k, n, blocked)
         assert torch.equal(lin(x.view(1, n, k)).view(n, -1), ref)
     # captured in a HIP graph (the quantize + GEMM path), replayed
     s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         lin(x)
     torch.cuda.synchronize()
