@@ -1030,7 +1030,7 @@ def attention_traffic_probe(device) -> None:
             qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), kc.data_ptr(),
             vc.data_ptr(), kc.stride(0), kc.stride(2), kc.stride(1), seq.data_ptr(), out.data_ptr(), out.stride(0),
             D, qo.data_ptr(), qo.stride(0), sx.data_ptr(), 0, B, hq, hkv, D, L, D ** -0.5, ws.data_ptr(),
-            ws.numel(), torch.cuda.current_stream().cuda_stream)
+            ws.numel(), None, torch.cuda.current_stream().cuda_stream)
         _native.check(rc, "tq_decode_attention_rope")
     torch.cuda.synchronize()
     src = torch.ones(TRAFFIC_COPY_BYTES // 4, device=device, dtype=torch.float32)

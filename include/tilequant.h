@@ -355,6 +355,31 @@ int tq_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_str
                                 int dtype, int batch, int q_heads, int kv_heads, int head_dim, int max_len,
                                 float scale, void* stream);
 
+/* ---- warming the next decode GEMM's weights into the right L2 ---------------
+ * On MI355X each of the 8 XCDs has its own L2, and workgroups are dealt to
+ * the XCDs round-robin by workgroup id.  The decode GEMM's schedule reads row
+ * tile r only from XCD r mod 8 (tq_gemm_l2_warm_ok says for which shapes).  A
+ * producer kernel that runs just before such a GEMM (the ones below that
+ * take a tq_l2_warm) can then spend its idle memory time reading the GEMM's
+ * packed tiles from the XCD that will need them: `blocks` extra workgroups
+ * (a multiple of 8, at most 1024) each touch every 64-byte sector of the row
+ * tiles r = (its XCD) + 8 j.  The outputs are unchanged; only where the bytes
+ * sit when the GEMM starts changes.  warm NULL or blocks == 0: no warm-up.
+ * No reference counterpart (a scheduling aid of this build). */
+typedef struct tq_l2_warm {
+  const void* int8_tiles;         /* the GEMM's packed INT8 tiles [T8, 64, 64] */
+  const void* fp16_tiles;         /* its 16-bit tiles [T16, 64, 64], or NULL */
+  const int32_t* int8_row_ptr;    /* [n_tr + 1] */
+  const int32_t* fp16_row_ptr;    /* [n_tr + 1]; NULL when fp16_tiles is NULL */
+  int n_tr;
+  int blocks;
+} tq_l2_warm;
+
+/* 1 when the automatic schedule of tq_gemm_mixed_rows for these arguments
+ * (split_k <= 1, row-major codes, 16-byte aligned rows with k == 64 n_tc)
+ * reads row tile r only from XCD r mod 8, else 0. */
+int tq_gemm_l2_warm_ok(int n, int k, int n_tr, int n_tc);
+
 /* As tq_decode_attention, and the attention output (the [batch, q_heads *
  * head_dim] input of the next projection) is also quantized like
  * tq_act_quant_fused: q_out int8 with row stride q_out_stride_b, sx_out
@@ -386,7 +411,8 @@ int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* co
                              int64_t cache_stride_l, int64_t cache_stride_h, const int32_t* seq_used, void* out,
                              int64_t out_stride_b, int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b,
                              float* sx_out, int dtype, int batch, int q_heads, int kv_heads, int head_dim,
-                             int max_len, float scale, float* workspace, int64_t workspace_elems, void* stream);
+                             int max_len, float scale, float* workspace, int64_t workspace_elems,
+                             const tq_l2_warm* warm, void* stream);
 
 /* ---- decode-step producers fused with the activation quantization ---------
  * Each computes a decoder-layer step that feeds a mixed tile GEMM and, when
@@ -403,11 +429,12 @@ int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, const void* co
 int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
                          const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out,
                          int64_t y_stride, int8_t* q_out, int64_t q_stride, float* sx_out, int dtype, int n,
-                         int k, void* stream);
+                         int k, const tq_l2_warm* warm, void* stream);
 
 /* y = round(round(silu(gate)) * up) for gate_up = [gate | up] of width 2 * inter. */
 int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride, int8_t* q_out,
-                      int64_t q_stride, float* sx_out, int dtype, int n, int inter, void* stream);
+                      int64_t q_stride, float* sx_out, int dtype, int n, int inter, const tq_l2_warm* warm,
+                      void* stream);
 
 /* RoPE (q * cos + rotate_half(q) * sin, head_dim 128) on the q and k heads of
  * a stacked [n, (q_heads + 2 kv_heads) * 128] q/k/v projection output; rotated

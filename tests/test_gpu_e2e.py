@@ -260,7 +260,7 @@ def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
     sx = torch.empty((k // 64,), dtype=torch.float32, device=DEV)
     rc = nat.lib().tq_add_rmsnorm_quant(x.data_ptr(), k, d.data_ptr() if with_delta else None, k,
                                         norm.weight.data_ptr(), 1e-5, h.data_ptr(), k, y.data_ptr(), k,
-                                        q.data_ptr(), k, sx.data_ptr(), 0, n, k,
+                                        q.data_ptr(), k, sx.data_ptr(), 0, n, k, None,
                                         torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
@@ -281,7 +281,7 @@ def test_silu_mul_quant_matches_module_and_quantizer(n, inter):
     q = torch.empty((n, inter), dtype=torch.int8, device=DEV)
     sx = torch.empty((inter // 64,), dtype=torch.float32, device=DEV)
     rc = nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y.data_ptr(), inter, q.data_ptr(), inter,
-                                     sx.data_ptr(), 0, n, inter, torch.cuda.current_stream().cuda_stream)
+                                     sx.data_ptr(), 0, n, inter, None, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
     assert _ulp_close(y, y_ref, 1.0)
@@ -339,7 +339,7 @@ def test_silu_mul_rows_matches_module(n, inter, dtype):
     if n <= 64 and inter % 64 == 0:
         y2 = torch.empty_like(y)
         rc = nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y2.data_ptr(), inter, None, inter, None,
-                                         nat.dtype_code(dtype), n, inter, torch.cuda.current_stream().cuda_stream)
+                                         nat.dtype_code(dtype), n, inter, None, torch.cuda.current_stream().cuda_stream)
         assert rc == 0
         torch.cuda.synchronize()
         assert torch.equal(y, y2)
@@ -490,7 +490,7 @@ def test_attention_rope_equals_rope_cache_then_attention(B, hq, hkv, L, pos, qua
         qkv.data_ptr(), qkv.stride(0), cos_t.data_ptr(), sin_t.data_ptr(), position.data_ptr(), kc2.data_ptr(),
         vc2.data_ptr(), kc2.stride(0), kc2.stride(2), kc2.stride(1), seq.data_ptr(), out2.data_ptr(), out2.stride(0),
         D, qo2.data_ptr() if quant else None, qo2.stride(0), sx2.data_ptr() if quant else None, code, B, hq, hkv, D,
-        L, D ** -0.5, ws.data_ptr(), ws.numel(), stream)
+        L, D ** -0.5, ws.data_ptr(), ws.numel(), None, stream)
     assert rc == 0
     torch.cuda.synchronize()
     assert torch.equal(out2, out1)
@@ -635,3 +635,110 @@ def test_fused_prefill_matches_module_prefill(family):
         for a, b in ((kf, km), (vf, vm)):
             assert float((a - b).abs().max()) <= 3e-2 * float(b.abs().max())
     assert torch.equal(rf, idf[:, :1]) and torch.equal(rm, idm[:, :1])
+
+
+@pytest.mark.parametrize("keep,blocks", [(0.05, 8), (0.05, 1024), (0.0, 64)])
+def test_l2_warm_leaves_producers_bitwise_unchanged(keep, blocks):
+    """The warm-up workgroups a producer runs for the next GEMM (tq_l2_warm)
+    only read that GEMM's tiles: the norm, SiLU * up and attention outputs,
+    codes, scales and cache contents are bitwise those of the launch without
+    them; the fewest (8) and the most (1024) warm-up workgroups, with and
+    without 16-bit tiles."""
+    import ctypes
+
+    from tilequant_amd.fused_decode import l2_warm_descriptor
+    from tilequant_amd.mixed_linear import MixedLinear
+    from tilequant_amd.pack import pack_weight_from_tile_ids
+    from types import SimpleNamespace
+
+    n_tr, n_tc = 80, 48
+    g = torch.Generator().manual_seed(71)
+    W = (torch.randn((n_tr * 64, n_tc * 64), generator=g) * 0.02).to(torch.bfloat16)
+    ids16 = torch.randperm(n_tr * n_tc, generator=g)[:int(keep * n_tr * n_tc)].sort().values
+    mask = torch.zeros(n_tr * n_tc, dtype=torch.bool)
+    mask[ids16] = True
+    pack = pack_weight_from_tile_ids(W.to(DEV), n_tr=n_tr, n_tc=n_tc, int8_tile_ids=torch.nonzero(~mask).flatten(),
+                                     fp16_tile_ids=ids16, cfg=SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    lin = MixedLinear(pack, None, SimpleNamespace(quant_style="gi", dtype_out="bf16"))
+    warm = l2_warm_descriptor(lin, 4)
+    assert warm is not None and (warm.fp16_tiles is None) == (keep == 0.0)
+    warm.blocks = blocks
+    stream = torch.cuda.current_stream().cuda_stream
+    n, k, inter = 4, 3072, 8192
+    x = (torch.randn((n, k), generator=g) * 3).to(torch.bfloat16).to(DEV)
+    d = (torch.randn((n, k), generator=g) * 2).to(torch.bfloat16).to(DEV)
+    wn = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16).to(DEV)
+    gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(torch.bfloat16).to(DEV)
+
+    def norm(wd):
+        h, y = torch.empty_like(x), torch.empty_like(x)
+        q, sx = torch.empty((n, k), dtype=torch.int8, device=DEV), torch.empty((k // 64,), device=DEV)
+        assert nat.lib().tq_add_rmsnorm_quant(x.data_ptr(), k, d.data_ptr(), k, wn.data_ptr(), 1e-5, h.data_ptr(), k,
+                                              y.data_ptr(), k, q.data_ptr(), k, sx.data_ptr(), 0, n, k, wd,
+                                              stream) == 0
+        return h, y, q, sx
+
+    def silu(wd):
+        y = torch.empty((n, inter), dtype=torch.bfloat16, device=DEV)
+        q, sx = torch.empty((n, inter), dtype=torch.int8, device=DEV), torch.empty((inter // 64,), device=DEV)
+        assert nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y.data_ptr(), inter, q.data_ptr(), inter,
+                                           sx.data_ptr(), 0, n, inter, wd, stream) == 0
+        return y, q, sx
+
+    B, hq, hkv, D, L = 4, 24, 8, 128, 700
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(torch.bfloat16).to(DEV)
+    kc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    vc0 = torch.randn((B, hkv, L, D), generator=g).to(torch.bfloat16).to(DEV)
+    cos_t = torch.randn((L, D), generator=g).to(torch.bfloat16).to(DEV)
+    sin_t = torch.randn((L, D), generator=g).to(torch.bfloat16).to(DEV)
+    position = torch.tensor([411], dtype=torch.int64, device=DEV)
+    seq = torch.full((B,), 412, dtype=torch.int32, device=DEV)
+    ws = decode_attention_workspace(B, hq, L, DEV)
+
+    def attention(wd, quant):
+        kc, vc = kc0.clone(), vc0.clone()
+        out = torch.empty((B, hq * D), dtype=torch.bfloat16, device=DEV)
+        qo = torch.empty((B, hq * D), dtype=torch.int8, device=DEV)
+        sx = torch.empty((hq * D // 64,), device=DEV)
+        assert nat.lib().tq_decode_attention_rope(
+            qkv.data_ptr(), qkv.stride(0), cos_t.data_ptr(), sin_t.data_ptr(), position.data_ptr(), kc.data_ptr(),
+            vc.data_ptr(), kc.stride(0), kc.stride(2), kc.stride(1), seq.data_ptr(), out.data_ptr(), out.stride(0), D,
+            qo.data_ptr() if quant else None, qo.stride(0), sx.data_ptr() if quant else None, 0, B, hq, hkv, D, L,
+            D ** -0.5, ws.data_ptr(), ws.numel(), wd, stream) == 0
+        return (out, qo, sx, kc, vc) if quant else (out, kc, vc)
+
+    for fn in (norm, silu, lambda wd: attention(wd, True), lambda wd: attention(wd, False)):
+        plain = fn(None)
+        warmed = fn(ctypes.byref(warm))
+        torch.cuda.synchronize()
+        for a, b in zip(plain, warmed):
+            assert torch.equal(a, b)
+
+
+def test_fused_decode_step_with_every_gemm_warmed_gives_the_same_logits(monkeypatch):
+    """Every producer warming its GEMM's weights (not only the default QKV)
+    leaves each decode step's logits and tokens bitwise unchanged."""
+    import tilequant_amd.fused_decode as fd
+    from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
+
+    monkeypatch.setattr(fd, "WARM_GEMMS", ("qkv", "o", "gate_up", "down"))
+    config = tiny_llama_config(layers=2)
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type="llama", dtype_out="bf16"), DEV,
+                                               keep_frac=0.05, seed=41)
+    B, P, O = 4, 64, 8
+    prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(42))
+    runs = {}
+    for warm in (False, True):
+        dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV,
+                                             l2_warm=warm)
+        n_desc = sum(v is not None for ly in dec._fused.layers for v in ly.warm.values())
+        assert n_desc == (8 if warm else 0)
+        dec.prefill(prompt)
+        logits = []
+        for _ in range(O - 1):
+            dec._graph.replay()
+            logits.append(dec._decode_logits.clone())
+        runs[warm] = (torch.stack(logits), dec._generated.clone())
+        dec.close()
+    assert torch.equal(runs[False][0], runs[True][0])
+    assert torch.equal(runs[False][1], runs[True][1])

@@ -136,3 +136,25 @@ def test_decode_attention_plan_balances_the_llama_decode_shape(lib):
     # B = 4 x 8 kv heads at 2304 keys: 24 splits of 3 waves = 768 workgroups, 3 per CU
     assert _attention_plan(lib, 4, 24, 8, 2304, True, 256) == (24, 3)
     assert lib.tq_decode_attention_plan(0, 24, 8, 2304, 1, 256, None, None) != 0
+
+
+def test_l2_warm_descriptor_validation_and_shape_query(lib):
+    """A tq_l2_warm the producers cannot use is rejected on the host, before
+    any launch; tq_gemm_l2_warm_ok follows the decode schedule's XCD mapping."""
+    fake = 1 << 20   # non-null, 16-byte aligned host values: nothing is dereferenced before the check
+    good = dict(int8_tiles=fake, fp16_tiles=None, int8_row_ptr=fake, fp16_row_ptr=None, n_tr=80, blocks=64)
+    bad = [dict(good, blocks=7), dict(good, blocks=-8), dict(good, blocks=2048), dict(good, n_tr=0),
+           dict(good, int8_row_ptr=None), dict(good, fp16_tiles=fake, fp16_row_ptr=None)]
+    for fields in bad:
+        w = nat.L2Warm(**fields)
+        assert lib.tq_add_rmsnorm_quant(fake, 3072, None, 0, fake, 1e-5, None, 0, fake, 3072, fake, 3072, fake, 0, 4,
+                                        3072, ctypes.byref(w), None) == -1, fields
+        assert lib.tq_silu_mul_quant(fake, 16384, fake, 8192, fake, 8192, fake, 0, 4, 8192, ctypes.byref(w),
+                                     None) == -1, fields
+    # one-j-block decode grids map row tile r to XCD r % 8 only when n_tr % 8 == 0
+    assert lib.tq_gemm_l2_warm_ok(4, 3072, 80, 48) == 1       # Llama-3.2-3B stacked QKV at 4 tokens
+    assert lib.tq_gemm_l2_warm_ok(4, 8192, 48, 128) == 1      # Down
+    assert lib.tq_gemm_l2_warm_ok(4, 3072, 50, 48) == 0
+    assert lib.tq_gemm_l2_warm_ok(12, 3072, 201, 48) == 1     # whole-tile workgroups: unit = row tile
+    assert lib.tq_gemm_l2_warm_ok(128, 3072, 80, 48) == 0     # prefill sizes: another kernel
+    assert lib.tq_gemm_l2_warm_ok(4, 3000, 80, 48) == 0       # k != 64 n_tc

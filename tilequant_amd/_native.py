@@ -13,7 +13,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtilequant_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TQ_DTYPE = {torch.bfloat16: 0, torch.float16: 1}
 TQ_LAYOUT = {"row_major": 0, "mfma": 1}
@@ -90,12 +90,13 @@ _SIGNATURES = {
     "tq_decode_attention_quant": (_i, [_p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
                                        _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
     "tq_decode_attention_rope": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
-                                      _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p]),
+                                      _p, _i64, _p, _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _i64, _p, _p]),
     "tq_greedy_step_workspace_elems": (_i64, [_i]),
     "tq_greedy_step": (_i, [_p, _i64, _i, _i, _i, _p, _i64, _p, _p, _p, _i64, _i, _p, _i, _p, _p]),
     "tq_add_rmsnorm_quant": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _p, _i64, _p,
-                                  _i, _i, _i, _p]),
-    "tq_silu_mul_quant": (_i, [_p, _i64, _p, _i64, _p, _i64, _p, _i, _i, _i, _p]),
+                                  _i, _i, _i, _p, _p]),
+    "tq_silu_mul_quant": (_i, [_p, _i64, _p, _i64, _p, _i64, _p, _i, _i, _i, _p, _p]),
+    "tq_gemm_l2_warm_ok": (_i, [_i, _i, _i, _i]),
     "tq_add_rmsnorm_rows": (_i, [_p, _i64, _p, _i64, _p, ctypes.c_float, _p, _i64, _p, _i64, _i, _i, _i, _p]),
     "tq_silu_mul_rows": (_i, [_p, _i64, _p, _i64, _i, _i, _i, _p]),
     "tq_rope_prefill": (_i, [_p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i, _i, _i,
@@ -125,6 +126,16 @@ class LinearDesc(ctypes.Structure):
 
 
 _SIGNATURES["tq_linear_forward"] = (_i, [ctypes.POINTER(LinearDesc)])
+
+
+class L2Warm(ctypes.Structure):
+    """Mirror of tq_l2_warm (include/tilequant.h): the next decode GEMM's
+    packed tiles and row pointers, and the producer's extra workgroup count.
+    Passed by address (the trailing ``warm`` argument of the producers); NULL
+    means no warm-up."""
+
+    _fields_ = [("int8_tiles", _p), ("fp16_tiles", _p), ("int8_row_ptr", _p), ("fp16_row_ptr", _p),
+                ("n_tr", _i), ("blocks", _i)]
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

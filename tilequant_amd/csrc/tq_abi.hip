@@ -1,7 +1,7 @@
 // tq_abi.hip -- ABI version and error strings of libtilequant_hip.so.
 #include "tq_common.h"
 
-extern "C" int tq_abi_version(void) { return 2; }
+extern "C" int tq_abi_version(void) { return 3; }
 
 extern "C" const char* tq_error_string(int code) {
   switch (code) {

@@ -443,7 +443,12 @@ __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d)
 
 template <class XT, int NB>
 __global__ void __launch_bounds__(kAttnD)
-attn_merge_kernel(AttnArgs a) {
+attn_merge_kernel(AttnArgs a, L2Warm warm) {
+  if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
+    __shared__ uint32_t warm_sink[64];
+    l2_warm_rows<kAttnD>(warm, warm_sink);
+    return;
+  }
   const int bh = blockIdx.x, d = threadIdx.x;
   const int b = bh / a.q_heads, h = bh - (bh / a.q_heads) * a.q_heads;
   const float* rec = a.part + (int64_t)bh * a.n_splits * (kAttnD + 2);
@@ -465,9 +470,14 @@ constexpr int kMergeQuantThreads = 256;   // 4 waves (row groups) x 64 dimension
 
 template <class XT, int NB, int RPW>
 __global__ void __launch_bounds__(kMergeQuantThreads)
-attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx) {
+attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, L2Warm warm) {
   constexpr int kGroups = kMergeQuantThreads / kWave;
   __shared__ float2 mls[kGroups * RPW][NB];
+  if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
+    __shared__ uint32_t warm_sink[64];
+    l2_warm_rows<kMergeQuantThreads>(warm, warm_sink);
+    return;
+  }
   __shared__ float red[kGroups];
   const int h = blockIdx.x >> 1, half = blockIdx.x & 1;
   const int t = threadIdx.x, lane = t & 63, rg = t >> 6;
@@ -560,33 +570,44 @@ attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* 
   if (t == 0) sx[2 * h + half] = s;
 }
 
+// The merge's own grid (workgroups before any warm-up ones).
+static int merge_blocks(const AttnArgs& a, bool quant) { return quant ? a.q_heads * 2 : a.batch * a.q_heads; }
+
 // Merge launches: NB = splits rounded up to 8 (at most kMergeBatch), so no
 // load of a batch is wasted on padding below kMergeBatch splits.
 template <class XT, int NB>
-static void launch_merge_nb(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, hipStream_t s) {
-  const dim3 gq(a.q_heads * 2), bq(kMergeQuantThreads);
+static void launch_merge_nb(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, const L2Warm& warm,
+                            hipStream_t s) {
+  const dim3 g(merge_blocks(a, q_out != nullptr) + warm.blocks), bq(kMergeQuantThreads);
   if (!q_out)
-    hipLaunchKernelGGL((attn_merge_kernel<XT, NB>), dim3(a.batch * a.q_heads), dim3(kAttnD), 0, s, a);
+    hipLaunchKernelGGL((attn_merge_kernel<XT, NB>), g, dim3(kAttnD), 0, s, a, warm);
   else if (a.batch <= 4)
-    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 1>), gq, bq, 0, s, a, q_out, ldq, sx);
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 1>), g, bq, 0, s, a, q_out, ldq, sx, warm);
   else if (a.batch <= 8)
-    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 2>), gq, bq, 0, s, a, q_out, ldq, sx);
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 2>), g, bq, 0, s, a, q_out, ldq, sx, warm);
   else
-    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 4>), gq, bq, 0, s, a, q_out, ldq, sx);
+    hipLaunchKernelGGL((attn_merge_quant_kernel<XT, NB, 4>), g, bq, 0, s, a, q_out, ldq, sx, warm);
 }
 
+// warm: its `first` must be merge_blocks(a, q_out != nullptr).
 template <class XT>
-static void launch_merge(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, hipStream_t s) {
+static void launch_merge(const AttnArgs& a, int8_t* q_out, int64_t ldq, float* sx, const L2Warm& warm,
+                         hipStream_t s) {
   switch ((min(a.n_splits, kMergeBatch) + 7) / 8) {
-    case 1: launch_merge_nb<XT, 8>(a, q_out, ldq, sx, s); break;
-    case 2: launch_merge_nb<XT, 16>(a, q_out, ldq, sx, s); break;
-    case 3: launch_merge_nb<XT, 24>(a, q_out, ldq, sx, s); break;
-    case 4: launch_merge_nb<XT, 32>(a, q_out, ldq, sx, s); break;
-    case 5: launch_merge_nb<XT, 40>(a, q_out, ldq, sx, s); break;
-    case 6: launch_merge_nb<XT, 48>(a, q_out, ldq, sx, s); break;
-    case 7: launch_merge_nb<XT, 56>(a, q_out, ldq, sx, s); break;
-    default: launch_merge_nb<XT, 64>(a, q_out, ldq, sx, s); break;
+    case 1: launch_merge_nb<XT, 8>(a, q_out, ldq, sx, warm, s); break;
+    case 2: launch_merge_nb<XT, 16>(a, q_out, ldq, sx, warm, s); break;
+    case 3: launch_merge_nb<XT, 24>(a, q_out, ldq, sx, warm, s); break;
+    case 4: launch_merge_nb<XT, 32>(a, q_out, ldq, sx, warm, s); break;
+    case 5: launch_merge_nb<XT, 40>(a, q_out, ldq, sx, warm, s); break;
+    case 6: launch_merge_nb<XT, 48>(a, q_out, ldq, sx, warm, s); break;
+    case 7: launch_merge_nb<XT, 56>(a, q_out, ldq, sx, warm, s); break;
+    default: launch_merge_nb<XT, 64>(a, q_out, ldq, sx, warm, s); break;
   }
+}
+
+// No warm-up: the merge's own grid only.
+static L2Warm no_warm(const AttnArgs& a, bool quant) {
+  return L2Warm{nullptr, nullptr, nullptr, nullptr, 0, 0, merge_blocks(a, quant)};
 }
 
 // Split plan.  Workgroups are dealt evenly to the compute units, so the
@@ -738,10 +759,10 @@ extern "C" int tq_decode_attention(const void* q, int64_t q_stride_b, int64_t q_
   const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16>(a, g1, s);
-    launch_merge<Bf16>(a, nullptr, 0, nullptr, s);
+    launch_merge<Bf16>(a, nullptr, 0, nullptr, no_warm(a, false), s);
   } else {
     launch_split<Fp16>(a, g1, s);
-    launch_merge<Fp16>(a, nullptr, 0, nullptr, s);
+    launch_merge<Fp16>(a, nullptr, 0, nullptr, no_warm(a, false), s);
   }
   return (int)hipGetLastError();
 }
@@ -763,10 +784,10 @@ extern "C" int tq_decode_attention_quant(const void* q, int64_t q_stride_b, int6
   const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16>(a, g1, s);
-    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, s);
+    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, no_warm(a, true), s);
   } else {
     launch_split<Fp16>(a, g1, s);
-    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, s);
+    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, no_warm(a, true), s);
   }
   return (int)hipGetLastError();
 }
@@ -778,7 +799,7 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
                                         int64_t out_stride_h, int8_t* q_out, int64_t q_out_stride_b,
                                         float* sx_out, int dtype, int batch, int q_heads, int kv_heads,
                                         int head_dim, int max_len, float scale, float* workspace,
-                                        int64_t workspace_elems, void* stream) {
+                                        int64_t workspace_elems, const tq_l2_warm* warm_in, void* stream) {
   if (q_out != nullptr && (batch > kMergeQuantMaxRows || sx_out == nullptr)) return TQ_ERR_ARG;
   if (batch > 0 && max_len > 0 && (!cos_table || !sin_table || !position)) return TQ_ERR_ARG;
   if ((cos_table && !aligned16(cos_table)) || (sin_table && !aligned16(sin_table))) return TQ_ERR_ALIGN;
@@ -793,14 +814,17 @@ extern "C" int tq_decode_attention_rope(const void* qkv, int64_t qkv_stride, con
   a.pos = position;
   a.k_out = static_cast<uint16_t*>(k_cache);
   a.v_out = static_cast<uint16_t*>(v_cache);
+  L2Warm warm;
+  const int wrc = l2_warm_args(warm_in, merge_blocks(a, q_out != nullptr), warm);
+  if (wrc) return wrc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 g1(a.n_splits, batch * kv_heads);
   if (dtype == TQ_DTYPE_BF16) {
     launch_split<Bf16, true>(a, g1, s);
-    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, s);
+    launch_merge<Bf16>(a, q_out, q_out_stride_b, sx_out, warm, s);
   } else {
     launch_split<Fp16, true>(a, g1, s);
-    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, s);
+    launch_merge<Fp16>(a, q_out, q_out_stride_b, sx_out, warm, s);
   }
   return (int)hipGetLastError();
 }

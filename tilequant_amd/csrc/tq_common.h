@@ -200,6 +200,82 @@ __device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
 
 __host__ __device__ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ---- L2 warm-up of the next decode GEMM's weights -------------------------
+// A producer kernel launched with `blocks` extra workgroups after its own
+// `first` ones hands those to l2_warm_rows.  Workgroups are dealt to the 8
+// XCDs round-robin by id, so workgroup b runs on XCD b % 8; the decode GEMM
+// reads row tile r only from XCD r % 8.  The blocks / 8 warm-up workgroups of
+// an XCD split each of that XCD's row tiles (r = XCD + 8 j) into equal
+// 64-byte-aligned shares, and every lane reads one dword of each 64-byte
+// sector of its share with an LDS DMA load (global_load_lds_dword) into a
+// 256-byte sink: nothing is kept in registers, so the loads of all rows go
+// out back to back and the workgroup waits once, at its end.  Each lane's
+// offset is checked against its share (global loads have no range check).
+struct L2Warm {
+  const int8_t* w8;
+  const int8_t* w16;
+  const int32_t* rp8;
+  const int32_t* rp16;
+  int n_tr, blocks, first;
+};
+
+template <int NT>
+__device__ __attribute__((always_inline)) inline void l2_warm_span(const int8_t* base, int64_t lo, int64_t hi,
+                                                                   uint32_t* sink) {
+  for (int64_t o = lo + (int64_t)threadIdx.x * 64; o < hi; o += (int64_t)NT * 64)
+    __builtin_amdgcn_global_load_lds(base + o, sink, 4, 0, 0);
+}
+
+// NT: the producer's threads per workgroup.  sink: 256 bytes of LDS (64
+// dwords), shared by all waves (the data is never read).  The row ranges of
+// up to 64 row tiles come with one vector load per pointer array (lane j: row
+// XCD + 8 j) before any DMA load is issued, so waiting for them never waits
+// for the DMA loads of earlier rows.
+template <int NT>
+__device__ __attribute__((always_inline)) inline void l2_warm_rows(const L2Warm& w, uint32_t* sink) {
+  const int p = (int)blockIdx.x - w.first;
+  const int xcd = blockIdx.x & 7, slot = p >> 3, per = w.blocks >> 3;
+  const int lane = threadIdx.x & 63;
+  const int32_t* rp16 = w.w16 != nullptr ? w.rp16 : w.rp8;
+  for (int r0 = xcd; r0 < w.n_tr; r0 += 8 * 64) {
+    const int rl = min(r0 + 8 * lane, w.n_tr - 1);
+    const int lo8v = w.rp8[rl], hi8v = w.rp8[rl + 1], lo16v = rp16[rl], hi16v = rp16[rl + 1];
+    const int nrows = min(64, (w.n_tr - r0 + 7) / 8);
+    for (int j = 0; j < nrows; ++j) {
+      const int lo8 = __builtin_amdgcn_readlane(lo8v, j), hi8 = __builtin_amdgcn_readlane(hi8v, j);
+      // shares counted in 64-byte sectors (64 per INT8 tile, 128 per 16-bit
+      // tile: below 2^27 for any row of fewer than 2^20 column tiles)
+      const uint32_t u8 = (uint32_t)(hi8 - lo8) * 64u, q8 = (u8 + per - 1) / (uint32_t)per;
+      l2_warm_span<NT>(w.w8 + (int64_t)lo8 * 4096, (int64_t)slot * q8 * 64,
+                       (int64_t)min(u8, (uint32_t)(slot + 1) * q8) * 64, sink);
+      if (w.w16 != nullptr) {
+        const int lo16 = __builtin_amdgcn_readlane(lo16v, j), hi16 = __builtin_amdgcn_readlane(hi16v, j);
+        const uint32_t u16 = (uint32_t)(hi16 - lo16) * 128u, q16 = (u16 + per - 1) / (uint32_t)per;
+        l2_warm_span<NT>(w.w16 + (int64_t)lo16 * 8192, (int64_t)slot * q16 * 64,
+                         (int64_t)min(u16, (uint32_t)(slot + 1) * q16) * 64, sink);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Host: the kernel-side form of a tq_l2_warm (blocks 0 when absent), after
+// checking it; `first` is the producer's own workgroup count.
+inline int l2_warm_args(const tq_l2_warm* in, int first, L2Warm& out) {
+  out = L2Warm{nullptr, nullptr, nullptr, nullptr, 0, 0, first};
+  if (in == nullptr || in->blocks == 0) return TQ_OK;
+  if (in->blocks < 0 || in->blocks > 1024 || (in->blocks & 7) != 0 || in->n_tr <= 0 || in->int8_row_ptr == nullptr ||
+      (in->fp16_tiles != nullptr && in->fp16_row_ptr == nullptr))
+    return TQ_ERR_ARG;
+  out.w8 = static_cast<const int8_t*>(in->int8_tiles);
+  out.w16 = static_cast<const int8_t*>(in->fp16_tiles);
+  out.rp8 = in->int8_row_ptr;
+  out.rp16 = in->fp16_row_ptr;
+  out.n_tr = in->n_tr;
+  out.blocks = in->blocks;
+  return TQ_OK;
+}
+
 // Workgroup barrier for LDS hand-offs that leaves outstanding global loads in
 // flight: waits only for this wave's LDS operations (lgkmcnt(0); vmcnt and
 // expcnt at their maxima in the gfx9 s_waitcnt encoding), then s_barrier.

@@ -97,9 +97,14 @@ __device__ inline float dot2sq(uint32_t w, float acc) {
 
 template <class XT>
 __global__ void __launch_bounds__(kFuseThreads)
-add_rmsnorm_quant_kernel(NormArgs a) {
+add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
   __shared__ float rinv[64];          // 1 / sqrt(mean(h^2) + eps) per row (n <= 64)
   __shared__ float red[kFuseThreads / kWave];
+  if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
+    __shared__ uint32_t warm_sink[64];
+    l2_warm_rows<kFuseThreads>(warm, warm_sink);
+    return;
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int c = blockIdx.x;
   const int cpr = a.k >> 3;           // 8-element chunks per row
@@ -212,8 +217,13 @@ struct SiluArgs {
 // 16-bit type, the product rounded again.  Workgroup c = 64-column tile c.
 template <class XT>
 __global__ void __launch_bounds__(kFuseThreads)
-silu_mul_quant_kernel(SiluArgs a) {
+silu_mul_quant_kernel(SiluArgs a, L2Warm warm) {
   __shared__ float red[kFuseThreads / kWave];
+  if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
+    __shared__ uint32_t warm_sink[64];
+    l2_warm_rows<kFuseThreads>(warm, warm_sink);
+    return;
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int col = blockIdx.x * 64 + lane;
   const int nper = (a.n + 3) >> 2;   // rows per wave (wave-uniform)
@@ -562,7 +572,7 @@ using namespace tq;
 extern "C" int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
                                     const void* weight, float eps, void* h_out, int64_t h_stride, void* y_out,
                                     int64_t y_stride, int8_t* q_out, int64_t q_stride, float* sx_out, int dtype,
-                                    int n, int k, void* stream) {
+                                    int n, int k, const tq_l2_warm* warm_in, void* stream) {
   if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
   if (n < 0 || k < 0 || n > 64 || (k % 64) != 0) return TQ_ERR_ARG;
   if (n == 0 || k == 0) return TQ_OK;
@@ -578,17 +588,21 @@ extern "C" int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void*
   a.h = static_cast<uint16_t*>(h_out); a.y = static_cast<uint16_t*>(y_out); a.q = q_out; a.sx = sx_out;
   a.ldx = x_stride; a.ldd = delta_stride; a.ldh = h_stride; a.ldy = y_stride; a.ldq = q_stride;
   a.n = n; a.k = k; a.eps = eps;
+  L2Warm warm;
+  const int rc = l2_warm_args(warm_in, k / 64, warm);
+  if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(k / 64 + warm.blocks);
   if (dtype == TQ_DTYPE_BF16)
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Bf16>, dim3(k / 64), dim3(kFuseThreads), 0, s, a);
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Bf16>, grid, dim3(kFuseThreads), 0, s, a, warm);
   else
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Fp16>, dim3(k / 64), dim3(kFuseThreads), 0, s, a);
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Fp16>, grid, dim3(kFuseThreads), 0, s, a, warm);
   return (int)hipGetLastError();
 }
 
 extern "C" int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y_out, int64_t y_stride,
                                  int8_t* q_out, int64_t q_stride, float* sx_out, int dtype, int n, int inter,
-                                 void* stream) {
+                                 const tq_l2_warm* warm_in, void* stream) {
   if (dtype != TQ_DTYPE_BF16 && dtype != TQ_DTYPE_FP16) return TQ_ERR_DTYPE;
   if (n < 0 || inter < 0 || n > 64 || (inter % 64) != 0) return TQ_ERR_ARG;
   if (n == 0 || inter == 0) return TQ_OK;
@@ -600,11 +614,15 @@ extern "C" int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y
   SiluArgs a{};
   a.gu = static_cast<const uint16_t*>(gate_up); a.y = static_cast<uint16_t*>(y_out); a.q = q_out; a.sx = sx_out;
   a.ldg = gu_stride; a.ldy = y_stride; a.ldq = q_stride; a.n = n; a.inter = inter;
+  L2Warm warm;
+  const int rc = l2_warm_args(warm_in, inter / 64, warm);
+  if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(inter / 64 + warm.blocks);
   if (dtype == TQ_DTYPE_BF16)
-    hipLaunchKernelGGL(silu_mul_quant_kernel<Bf16>, dim3(inter / 64), dim3(kFuseThreads), 0, s, a);
+    hipLaunchKernelGGL(silu_mul_quant_kernel<Bf16>, grid, dim3(kFuseThreads), 0, s, a, warm);
   else
-    hipLaunchKernelGGL(silu_mul_quant_kernel<Fp16>, dim3(inter / 64), dim3(kFuseThreads), 0, s, a);
+    hipLaunchKernelGGL(silu_mul_quant_kernel<Fp16>, grid, dim3(kFuseThreads), 0, s, a, warm);
   return (int)hipGetLastError();
 }
 

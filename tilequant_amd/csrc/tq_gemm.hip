@@ -663,7 +663,10 @@ gemm_decode_kernel(GemmArgs a) {
       row_rsrc(has16 ? (const void*)(a.w16 + (int64_t)lo16 * 4096) : (const void*)a.rp8, n16 * 8192);
   const __amdgpu_buffer_rsrc_t i16rs = row_rsrc(has16 ? (const void*)(a.ids16 + lo16) : (const void*)a.rp8, n16 * 4);
   const int first16 = (wave - (n8 % W) + W) % W;
-  const int id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + min(lane, U16 - 1) * W) * 4, 0, 0);
+  // Lane i: the id of the wave's 16-bit tile i (position first16 + i W), for
+  // its first 64 tiles -- the prefetched ones and the first window of the
+  // loop below, which then needs no ids round trip of its own.
+  const int id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + lane * W) * 4, 0, 0);
   v4i b16p[U16][JBW][2];
   auto load_w16_at = [&](v4i (&dst)[JBW][2], int q) {
 #pragma unroll
@@ -800,24 +803,27 @@ gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
   for (int u = 0; u < U16; ++u)
     if (first16 + u * W < n16) tile16(b16p[u], __builtin_amdgcn_readlane(id16l, u));
-  // The wave's remaining 16-bit tiles (positions q0 + i W, ascending: the
-  // same order as one at a time): the ids of up to 64 come with one vector
-  // load, then each batch of U16B tiles issues its weights and activation
-  // operands together -- one round trip per batch instead of two per tile
-  // (rows that are mostly 16-bit, as clustered masks give, have dozens).
-  // Rows past n read row n - 1: their products land in output rows that are
-  // never stored.
+  // The wave's remaining 16-bit tiles (tile indices t >= U16, positions
+  // first16 + t W, ascending: the same order as one at a time), in windows of
+  // tile indices [t0, next multiple of 64): the first window's ids are lanes
+  // U16.. of id16l, each later window's come with one vector load.  Each
+  // batch of U16B tiles then issues its weights and activation operands
+  // together -- one round trip per batch instead of two per tile (rows that
+  // are mostly 16-bit, as clustered masks give, have dozens).  Rows past n
+  // read row n - 1: their products land in output rows that are never stored.
   constexpr int U16B = JBW == 1 ? 4 : 2;
-  for (int q0 = first16 + U16 * W; q0 < n16; q0 += 64 * W) {
-    const int idv = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (q0 + lane * W) * 4, 0, 0);
-    const int cnt = min(64, (n16 - q0 + W - 1) / W);
+  for (int t0 = U16; first16 + t0 * W < n16; t0 = (t0 & ~63) + 64) {
+    const int q0 = first16 + t0 * W;
+    const int lane0 = t0 & 63;   // lane of the window's first id
+    const int idv = t0 < 64 ? id16l : __builtin_amdgcn_raw_buffer_load_b32(i16rs, (q0 + lane * W) * 4, 0, 0);
+    const int cnt = min(64 - lane0, (n16 - q0 + W - 1) / W);
     for (int i0 = 0; i0 < cnt; i0 += U16B) {
       v4i bb[U16B][JBW][2], ab[U16B][TB][2];
 #pragma unroll
       for (int u = 0; u < U16B; ++u) {
         const int i = min(i0 + u, cnt - 1);   // past the end: the last tile again, not used
         load_w16_at(bb[u], q0 + i * W);
-        const int c = col_of(__builtin_amdgcn_readlane(idv, i), rbase, n_tc);
+        const int c = col_of(__builtin_amdgcn_readlane(idv, lane0 + i), rbase, n_tc);
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
@@ -2358,6 +2364,16 @@ extern "C" int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* 
   }
   *n_first = 0;
   return split_any ? n : 0;   // 0: the plain pair order is the plan
+}
+
+// gemm_decode_kernel takes row tile r on workgroups b with b % 8 == r % 8:
+// whole-tile workgroups (JBW 4) are unit = b = r, and one-j-block workgroups
+// are dealt so that the four j-blocks of r run on XCD r % 8 when n_tr % 8 == 0
+// (the identity order otherwise spreads them over four XCDs).
+extern "C" int tq_gemm_l2_warm_ok(int n, int k, int n_tr, int n_tc) {
+  if (n < 1 || n > kDecodeMaxTokens || n_tr < 1 || n_tc < 1 || k != 64 * n_tc) return 0;
+  const DecodePlan d = plan_decode(n, k, n_tr, n_tc, false);
+  return d.ok && (d.jbw == 4 || (n_tr & 7) == 0) ? 1 : 0;
 }
 
 extern "C" int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc) {

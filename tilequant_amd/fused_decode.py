@@ -30,6 +30,7 @@ runs the Hugging Face modules inside its captured decode graph
 """
 from __future__ import annotations
 
+import ctypes
 from typing import List, Optional
 
 import torch
@@ -70,6 +71,37 @@ class _Layer:
         act = getattr(getattr(mlp, "config", None), "hidden_act", "silu")
         if act not in ("silu", "swish"):
             raise ValueError(f"fused decode supports SiLU MLPs, got {act}")
+        # L2 warm-up descriptors of the four GEMMs (set by FusedDecodeStep)
+        self.warm = {"qkv": None, "o": None, "gate_up": None, "down": None}
+
+
+# Warm-up sizing: about this many bytes of an XCD's share per warm-up workgroup,
+# at most this many workgroups per XCD.
+WARM_BYTES_PER_BLOCK = 64 * 1024
+WARM_MAX_BLOCKS_PER_XCD = 128
+# GEMMs whose weights are warmed.  Measured on MI355X (Llama-3.2-3B keep01, B=4,
+# 2304-token cache; TPOT, ms): none 1.905, QKV 1.888, QKV+O+Down 1.893-1.912,
+# Down 1.936, all four 2.12.  Only the QKV weights (16 MB) arrive within the
+# norm kernel that precedes them; O (inside the short attention merge), Gate/Up
+# (50 MB: more than the XCDs' L2) and Down (25 MB inside the 4.7 us SiLU
+# kernel) stretch their producer by more than their GEMM gains.
+WARM_GEMMS = ("qkv",)
+
+
+def l2_warm_descriptor(lin: nn.Module, n_rows: int) -> Optional[nat.L2Warm]:
+    """The tq_l2_warm of a MixedLinear's decode GEMM at ``n_rows`` rows, or
+    None: a dense projection, or a shape whose GEMM schedule does not read
+    row tile r from XCD r mod 8 only (tq_gemm_l2_warm_ok).  The descriptor
+    holds raw pointers into the module's buffers: rebuild it if they change."""
+    if not isinstance(lin, MixedLinear):
+        return None
+    if not nat.lib().tq_gemm_l2_warm_ok(int(n_rows), lin.K_orig, lin.n_tr, lin.n_tc):
+        return None
+    t8, t16 = int(lin.int8_tiles.shape[0]), int(lin.fp16_tiles.shape[0])
+    per_xcd_bytes = (4096 * t8 + 8192 * t16) / 8
+    per = max(1, min(WARM_MAX_BLOCKS_PER_XCD, -(-int(per_xcd_bytes) // WARM_BYTES_PER_BLOCK)))
+    return nat.L2Warm(nat.ptr(lin.int8_tiles), nat.ptr(lin.fp16_tiles) if t16 else None, nat.ptr(lin.int8_row_ptr),
+                      nat.ptr(lin.fp16_row_ptr) if t16 else None, lin.n_tr, 8 * per)
 
 
 # Architectures whose decoder layer is exactly what the fused step computes:
@@ -103,7 +135,8 @@ def check_fused_architecture(cfg, attention_module: nn.Module) -> None:
 class FusedDecodeStep:
     """Decode forward for a bound model and static cache (batch fixed)."""
 
-    def __init__(self, model: nn.Module, cache, batch: int, max_cache_len: int, device: torch.device) -> None:
+    def __init__(self, model: nn.Module, cache, batch: int, max_cache_len: int, device: torch.device,
+                 l2_warm: bool = True) -> None:
         cfg = model.config.get_text_config(decoder=True)
         check_fused_architecture(cfg, model.model.layers[0].self_attn)
         self.model = model
@@ -121,6 +154,11 @@ class FusedDecodeStep:
             raise ValueError("fused decode serves at most 16 sequences")
         self.inter = int(cfg.intermediate_size)
         self.layers: List[_Layer] = [_Layer(l) for l in self.text.layers]
+        # Each GEMM's packed weights are read, by the producer kernel that runs
+        # just before it (norm, attention merge, SiLU * up), into the L2 of the
+        # XCD that will read them (tq_l2_warm): that producer leaves the
+        # memory system idle, and the GEMM then starts on warm lines.
+        self.set_l2_warm(l2_warm)
         self.dtype = self.text.embed_tokens.weight.dtype
         self.code = nat.dtype_code(self.dtype)
         self.scale = float(self.text.layers[0].self_attn.scaling)
@@ -152,13 +190,26 @@ class FusedDecodeStep:
         self.cos_table = cos.reshape(self.L, self.head_dim).contiguous()
         self.sin_table = sin.reshape(self.L, self.head_dim).contiguous()
 
+    def set_l2_warm(self, enabled: bool) -> None:
+        """Switch the L2 warm-up of the GEMM weights on or off (outputs are the
+        same either way); takes effect for steps issued or captured later."""
+        self.l2_warm = bool(enabled)
+        for ly in self.layers:
+            for name in ly.warm:
+                on = self.l2_warm and name in WARM_GEMMS
+                ly.warm[name] = l2_warm_descriptor(getattr(ly, name), self.B) if on else None
+
     # -- kernels -------------------------------------------------------------
-    def _norm(self, x, delta, ln, h_out, y_out, q_out, sx_out) -> None:
+    @staticmethod
+    def _warm_arg(warm: Optional[nat.L2Warm]):
+        return ctypes.byref(warm) if warm is not None else None
+
+    def _norm(self, x, delta, ln, h_out, y_out, q_out, sx_out, warm=None) -> None:
         rc = nat.lib().tq_add_rmsnorm_quant(
             nat.ptr(x), x.stride(0), nat.ptr(delta), delta.stride(0) if delta is not None else 0,
             nat.ptr(ln.weight), float(ln.variance_epsilon), nat.ptr(h_out), h_out.stride(0) if h_out is not None else 0,
             nat.ptr(y_out), y_out.stride(0), nat.ptr(q_out), q_out.stride(0) if q_out is not None else 0,
-            nat.ptr(sx_out), self.code, self.B, self.hidden, nat.stream_handle(self.device))
+            nat.ptr(sx_out), self.code, self.B, self.hidden, self._warm_arg(warm), nat.stream_handle(self.device))
         nat.check(rc, "tq_add_rmsnorm_quant")
 
     def _linear(self, lin: nn.Module, x, xq, sx, out) -> None:
@@ -192,7 +243,7 @@ class FusedDecodeStep:
             h_new = self.h[k]
             q8 = self._quantized(ly.qkv)
             self._norm(cur, delta, ly.ln1, h_new if delta is not None else None, self.y,
-                       self.yq if q8 else None, self.ysx if q8 else None)
+                       self.yq if q8 else None, self.ysx if q8 else None, ly.warm["qkv"])
             resid = h_new if delta is not None else cur
             self._linear(ly.qkv, self.y, self.yq, self.ysx, self.qkv_out)
             layer_cache = self.cache.layers[li]
@@ -207,18 +258,20 @@ class FusedDecodeStep:
                 nat.ptr(self.attn), self.attn.stride(0), self.head_dim,
                 nat.ptr(self.aq) if q8o else None, self.aq.stride(0), nat.ptr(self.asx) if q8o else None,
                 self.code, B, self.hq, self.hkv, self.head_dim, self.L, self.scale, nat.ptr(self.attn_ws),
-                self.attn_ws.numel(), stream)
+                self.attn_ws.numel(), self._warm_arg(ly.warm["o"]), stream)
             nat.check(rc, "tq_decode_attention_rope")
             self._linear(ly.o, self.attn, self.aq, self.asx, self.o_out)
             k ^= 1
             h2 = self.h[k]
             q8g = self._quantized(ly.gate_up)
-            self._norm(resid, self.o_out, ly.ln2, h2, self.y, self.yq if q8g else None, self.ysx if q8g else None)
+            self._norm(resid, self.o_out, ly.ln2, h2, self.y, self.yq if q8g else None, self.ysx if q8g else None,
+                       ly.warm["gate_up"])
             self._linear(ly.gate_up, self.y, self.yq, self.ysx, self.gu)
             q8d = self._quantized(ly.down)
             rc = nat.lib().tq_silu_mul_quant(nat.ptr(self.gu), self.gu.stride(0), nat.ptr(self.m), self.m.stride(0),
                                              nat.ptr(self.mq) if q8d else None, self.mq.stride(0),
-                                             nat.ptr(self.msx) if q8d else None, self.code, B, self.inter, stream)
+                                             nat.ptr(self.msx) if q8d else None, self.code, B, self.inter,
+                                             self._warm_arg(ly.warm["down"]), stream)
             nat.check(rc, "tq_silu_mul_quant")
             self._linear(ly.down, self.m, self.mq, self.msx, self.d_out)
             cur, delta = h2, self.d_out

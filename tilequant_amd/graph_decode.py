@@ -132,7 +132,7 @@ class CudaGraphGreedyDecoder:
 
     def __init__(self, model: torch.nn.Module, *, prompt_tokens: int, max_new_tokens: int, batch_size: int = 1,
                  device="cuda", prefill_only: bool = False, fused_decode: bool = True,
-                 fused_prefill: bool = True) -> None:
+                 fused_prefill: bool = True, l2_warm: bool = True) -> None:
         if prompt_tokens < 1:
             raise ValueError("prompt_tokens must be positive")
         if batch_size < 1:
@@ -194,7 +194,8 @@ class CudaGraphGreedyDecoder:
             from .fused_decode import FusedDecodeStep
 
             try:
-                self._fused = FusedDecodeStep(model, self.cache, self.batch_size, self.max_cache_len, self.device)
+                self._fused = FusedDecodeStep(model, self.cache, self.batch_size, self.max_cache_len, self.device,
+                                              l2_warm=l2_warm)
             except (ValueError, AttributeError):
                 self._fused = None
         # The prompt forward from the row-parallel glue kernels where the
@@ -256,10 +257,15 @@ class CudaGraphGreedyDecoder:
     @torch.inference_mode()
     def prepare(cls, model: torch.nn.Module, *, prompt_tokens: int = 128, max_new_tokens: int = 512,
                 batch_size: int = 1, device="cuda", prefill_only: bool = False,
-                fused_decode: bool = True, fused_prefill: bool = True) -> "CudaGraphGreedyDecoder":
-        """Allocate, warm up and capture the prefill and decode graphs."""
+                fused_decode: bool = True, fused_prefill: bool = True,
+                l2_warm: bool = True) -> "CudaGraphGreedyDecoder":
+        """Allocate, warm up and capture the prefill and decode graphs.
+        ``l2_warm`` (fused decode step only): the producer kernel before each
+        GEMM reads that GEMM's weights into the L2 of the XCD that will use
+        them; the tokens and logits are the same either way."""
         dec = cls(model, prompt_tokens=prompt_tokens, max_new_tokens=max_new_tokens, batch_size=batch_size,
-                  device=device, prefill_only=prefill_only, fused_decode=fused_decode, fused_prefill=fused_prefill)
+                  device=device, prefill_only=prefill_only, fused_decode=fused_decode, fused_prefill=fused_prefill,
+                  l2_warm=l2_warm)
         try:
             dec._capture()
         except BaseException:
