@@ -71,6 +71,8 @@ def parse():
                     help="run only three eager decode-attention calls (RoPE form with the INT8 merge; B=4, 24/8 "
                          "heads, 2304 keys) and a 256 MiB copy: the workload of the FETCH_SIZE pass behind "
                          "profiles/decode_attention_traffic.md")
+    ap.add_argument("--trace-split", metavar="KERNEL_TRACE_CSV",
+                    help="per-layer split of the prompt forwards in a rocprofv3 kernel trace (no GPU needed)")
     ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="read the two --pmc passes' counter_collection.csv and write " + TRAFFIC_FILE)
     ap.add_argument("--released-maps", type=int, default=1,
@@ -137,6 +139,70 @@ def traffic_summarize(args):
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps(out))
+
+
+# kernel-name classes of the captured prompt forward (--trace-split) and of the decode step
+PREFILL_CLASSES = (("gemm_tilequant", ("gemm_prefill",)), ("gemm_hipblaslt", ("Cijk_",)),
+                   ("quantization", ("act_absmax", "act_quant", "act_scales")),
+                   ("attention", ("attn_fwd", "flash", "fmha")),
+                   ("glue", ("add_rmsnorm_rows", "rope_prefill", "silu_mul_rows")))
+DECODE_MARKERS = ("gemm_decode", "attn_split", "attn_merge", "add_rmsnorm_quant", "silu_mul_quant",
+                  "argmax_partial", "greedy_finish", "gemm_splitk")
+
+
+def trace_split(path, layers=LAYERS):
+    """Per-layer split of the prompt forwards in a rocprofv3 --kernel-trace
+    CSV: prefills are maximal runs of kernels without a decode-step kernel
+    that hold a RoPE launch per layer; each one's kernel time by class
+    (GEMM, quantization, attention, glue, other) and its GPU span, median
+    over the prefills of each model (TileQuant: a prefill with
+    gemm_prefill kernels; dense: without)."""
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    segs, cur = [], []
+    for start, end, name in rows:
+        if any(m in name for m in DECODE_MARKERS):
+            if cur:
+                segs.append(cur)
+            cur = []
+        else:
+            cur.append((start, end, name))
+    if cur:
+        segs.append(cur)
+    per_model = {"tilequant": [], "dense": []}
+    for seg in segs:
+        if sum("rope_prefill" in n for _, _, n in seg) < layers:
+            continue
+        # the prompt forward itself: from its first glue kernel's layer (embedding etc. just before) to the end
+        first = next(i for i, (_, _, n) in enumerate(seg) if "add_rmsnorm_rows" in n)
+        seg = seg[max(0, first - 2):]
+        cls = {c: 0.0 for c, _ in PREFILL_CLASSES}
+        cls["other"] = 0.0
+        for start, end, name in seg:
+            for c, keys in PREFILL_CLASSES:
+                if any(k in name for k in keys):
+                    cls[c] += (end - start) / 1e6
+                    break
+            else:
+                cls["other"] += (end - start) / 1e6
+        model = "tilequant" if cls["gemm_tilequant"] > 0 else "dense"
+        span = (seg[-1][1] - seg[0][0]) / 1e6
+        per_model[model].append({"span_ms": span, "kernel_ms": cls})
+    out = {}
+    for model, segs_m in per_model.items():
+        if not segs_m:
+            continue
+        med = lambda xs: statistics.median(xs)   # noqa: E731
+        classes = {c: med([s["kernel_ms"][c] for s in segs_m]) for c in segs_m[0]["kernel_ms"]}
+        out[model] = {"prefills": len(segs_m), "span_ms": med([s["span_ms"] for s in segs_m]),
+                      "kernel_ms": classes, "per_layer_us": {c: v * 1e3 / layers for c, v in classes.items()},
+                      "gaps_ms": med([s["span_ms"] - sum(s["kernel_ms"].values()) for s in segs_m])}
+    print(json.dumps(out, indent=1))
+    return out
 
 
 def traffic_for(args):
@@ -352,11 +418,33 @@ def qwen_measure(args, device):
             gemm_ms = graph_time(gemms, 10)
             n_launch = len(layers) * len(groups)
             achieved = packed / n_launch / (gemm_ms / n_launch / 1e3) / 1e9
+
+            # per projection group: its launches of every layer in one graph (cold weights: each
+            # layer's copy is distinct), average duration and HBM fraction on its packed bytes
+            group_us, group_frac = {}, {}
+            for gname, _, _ in groups:
+                def group_gemms(gname=gname):
+                    for i, mods in enumerate(layers):
+                        lin = mods[gname]
+                        xq, sx = quant[gname]
+                        gemm_mixed_rows_splitk(x_fp=xs[gname], x_int8=xq, sx=sx, int8_tiles=lin.int8_tiles,
+                                               int8_scales=lin.int8_scales, int8_tile_ids=lin.int8_tile_ids,
+                                               int8_row_ptr=lin.int8_row_ptr, fp16_tiles=lin.fp16_tiles,
+                                               fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
+                                               M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
+                                               out_dtype=torch.bfloat16, out=outs[(i, gname)],
+                                               tile_layout=lin.tile_layout)
+                us = graph_time(group_gemms, 10) * 1e3 / len(layers)
+                lin0 = layers[0][gname]
+                gbytes = 4096 * int(lin0.int8_tiles.shape[0]) + 8192 * int(lin0.fp16_tiles.shape[0]) \
+                    + 4 * int(lin0.int8_tiles.shape[0])
+                group_us[gname] = us
+                group_frac[gname] = gbytes / (us / 1e6) / 1e9 / HBM_PEAK_GBPS
             dec = {"layers": len(layers), "packed_bytes": packed, "bf16_tiles": t16,
                    "max_bf16_tiles_per_row_tile": max_row16, "ms_per_step": step_ms,
                    "tops": ops / (step_ms / 1e3) / 1e12, "gbps_packed_weights": packed / (step_ms / 1e3) / 1e9,
                    "gemm_avg_launch_us": gemm_ms * 1e3 / n_launch, "gemm_gbps": achieved,
-                   "gemm_hbm_frac": achieved / HBM_PEAK_GBPS}
+                   "gemm_hbm_frac": achieved / HBM_PEAK_GBPS, "group_us": group_us, "group_hbm_frac": group_frac}
             del outs, quant
             # prefill: one layer, 8192 tokens
             mods = layers[0]
@@ -1044,6 +1132,9 @@ def attention_traffic_probe(device) -> None:
 
 def main():
     args = parse()
+    if args.trace_split:
+        trace_split(args.trace_split, args.layers)
+        return
     if args.traffic_summarize:
         traffic_summarize(args)
         return
