@@ -301,6 +301,7 @@ INT8_PEAK_TOPS = 5030.0   # dense INT8 MFMA, 256 CU x 2.4 GHz x 8192 ops/clk
 
 # Qwen2.5 linear shapes (hidden, kv out, mlp)
 QWEN = (("qwen2.5-7b", 3584, 512, 18944), ("qwen2.5-14b", 5120, 1024, 13824))
+QWEN_MIN_LAYERS = 12
 
 
 def _groups_of(hidden, kv, mlp):
@@ -340,9 +341,10 @@ def _clustered_pack(m, k, frac, gen, cpu_gen, device, cfg):
 def qwen_measure(args, device):
     """Qwen2.5-7B / 14B linear shapes with clustered
     keep10 / keep20 masks.  Decode (4 tokens): a HIP graph of quantize + GEMM
-    over whole layers, as many layers as needed to stream more than 512 MB of
-    distinct packed weights; GEMM kernel time from a graph of the GEMM launches
-    alone.  Prefill (8192 tokens): one layer through MixedLinear."""
+    over whole layers, at least QWEN_MIN_LAYERS distinct layers and more than
+    512 MB of packed weights; GEMM kernel time from a graph of the GEMM
+    launches alone, and per projection group from a graph of that group's
+    launches.  Prefill (8192 tokens): one layer through MixedLinear."""
     import statistics as st
     import torch
     from tilequant_amd.gemm_rows_splitk_64x64 import gemm_mixed_rows_splitk
@@ -382,7 +384,9 @@ def qwen_measure(args, device):
             cpu_gen = torch.Generator(device="cpu")
             cpu_gen.manual_seed(args.seed + 12)
             layers, packed, t16, max_row16 = [], 0, 0, 0
-            while packed <= 512 * 1024 * 1024:
+            # enough distinct layers that the per-group graphs (one launch per layer) are not
+            # dominated by the graph replay's own overhead, and the weights stream cold
+            while packed <= 512 * 1024 * 1024 or len(layers) < QWEN_MIN_LAYERS:
                 mods = {}
                 for name, widths, k in groups:
                     packs = [_clustered_pack(m, k, keep, gen, cpu_gen, device, cfg) for m in widths]
