@@ -196,6 +196,19 @@ int tq_gemm_prefill_plan(const int32_t* int8_row_ptr, const int32_t* int8_tile_i
                          const int32_t* fp16_row_ptr, int n_tr, int n_tc, int32_t* units, int max_units,
                          int* n_first);
 
+/* Workspace (fp32 elements, zero-filled before first use, one per stream) that
+ * tq_linear_mixed_fused needs for these arguments: the split-K counters and
+ * partials (split_k > 1), or the cooperative launch's counters, codes and
+ * scales (see tq_linear_mixed_fused); 0 when it needs none.  Without it the
+ * call still runs, with a launch that needs none. */
+int64_t tq_linear_mixed_fused_workspace_elems(int n, int m, int k, int n_tr, int n_tc, int split_k);
+
+/* TEST-ONLY.  Poll budget of the cooperative launches of tq_linear_mixed_fused
+ * in this process: polls >= 0 (0 makes every GEMM workgroup quantize the
+ * activation itself instead of waiting for the producers; the outputs are the
+ * same), < 0 restores the default.  No reference counterpart. */
+void tq_test_set_coop_spin(int polls);
+
 /* Largest n tq_linear_mixed_fused accepts for input width k: at most 16, and
  * the n x ceil(k/64)*64 int8 codes (+ scales) must fit 64 KiB of LDS. */
 int tq_linear_mixed_fused_max_tokens(int k);
@@ -206,7 +219,17 @@ int tq_linear_mixed_fused_max_tokens(int k);
  * column tiles of its own split (same closed form) instead of reading codes
  * from memory.  No reference counterpart: the reference always runs the two
  * kernels (src/models/mixed_linear.py:233-239 -> quant_utils.py:119-134 and
- * gemm_rows_splitk_64x64.py:225-323).  Workspace as for tq_gemm_mixed_rows. */
+ * gemm_rows_splitk_64x64.py:225-323).  Where the rows x columns are too
+ * many for the LDS-staged quantizing kernel (e.g. 8+ rows of a 3072-wide
+ * input, 4 rows of Gate/Up), and a workspace of
+ * tq_linear_mixed_fused_workspace_elems is given, the launch is cooperative
+ * instead of split-K: 8 extra workgroups quantize the activation once into the
+ * workspace, and the GEMM workgroups, whose weight loads are already in
+ * flight, read the codes when the producers are done (a bounded wait; past it
+ * a workgroup quantizes by itself).  Same codes either way, so the outputs
+ * equal the two-launch sequence's bitwise.  Launches on one stream share its
+ * workspace in turn (each leaves the flags and counts zero); launches that
+ * overlap on one workspace race. */
 int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
                           const int8_t* int8_tiles, const float* int8_scales,
                           const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
@@ -270,7 +293,8 @@ enum {
   TQ_KERNEL_PREFILL_V5 = 6,             /* prefill DMA ring, two row tiles, 16-bit tiles in the ring */
   TQ_KERNEL_PREFILL_V3 = 7,             /* prefill DMA ring for k > 19456 */
   TQ_KERNEL_PREFILL_ASYNC = 8,          /* prefill DMA ring for k > 32768 */
-  TQ_KERNEL_PREFILL_REGISTER = 9        /* prefill through registers (unaligned rows or k % 64 != 0) */
+  TQ_KERNEL_PREFILL_REGISTER = 9,       /* prefill through registers (unaligned rows or k % 64 != 0) */
+  TQ_KERNEL_DECODE_COOP = 10            /* LDS-staged decode kernel, codes from its producer workgroups */
 };
 
 /* TEST-ONLY.  tq_gemm_mixed_rows_planned (prefill_units may be NULL, then it

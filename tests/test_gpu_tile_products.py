@@ -151,9 +151,10 @@ def test_config0_products_every_decode_kernel():
     P, kern = _run_fused(pack, xd, split_k=2)
     _assert_products(P, ref, f"{kern} split_k=2")
     seen.add(kern)
-    # at 16 rows the one-launch path is the split-K kernel (16 rows x 3072
-    # columns exceed the LDS-staged kernel's 4 chunks per thread); 4 rows take
-    # the LDS-staged one, with scales over those 4 rows
+    # at 16 rows the one-launch path is the cooperative kernel (16 rows x 3072
+    # columns exceed the LDS-staged kernel's 4 chunks per thread, so producer
+    # workgroups quantize into the workspace); 4 rows take the LDS-staged
+    # quantizing kernel, with scales over those 4 rows
     x4 = x[:4].contiguous()
     xq4_ref, _ = nm.act_quant(values(x4))
     P, kern = _run_fused(pack, x4.to(DEV))
@@ -162,7 +163,8 @@ def test_config0_products_every_decode_kernel():
     # a window of rows: only those rows are written
     P, kern = _run_codes(pack, xd, xq, sx, rows=(5, 7))
     _assert_products(P, ref[:, 5:12], f"{kern} rows 5..11")
-    assert seen == {"decode", "splitk", "splitk_token_blocked", "decode_quant", "splitk_quant"}, seen
+    assert seen == {"decode", "splitk", "splitk_token_blocked", "decode_quant", "splitk_quant",
+                    "decode_coop"}, seen
 
 
 # ---- configs[1] -------------------------------------------------------------------------------

@@ -99,6 +99,31 @@ def test_workspace_sizing(lib):
     assert lib.tq_gemm_workspace_elems(100, 3072, 48, 48, 0) == 0     # general kernel: none
 
 
+def test_fused_workspace_sizing(lib):
+    """linear_mixed_fused's workspace: the split-K one, or for a cooperative
+    launch (a shape the LDS-staged quantizing kernel cannot take: too many
+    rows x columns for its chunks per thread) a 4096-entry head of flags and
+    counts, the int8 codes [n][k] rounded up to 16 bytes, then n_tc scales."""
+    def coop(n, k, n_tc):
+        return 4096 + (n * k + 15) // 16 * 4 + n_tc
+    q = lib.tq_linear_mixed_fused_workspace_elems
+    # Llama-3.2-3B Q/K/V (5120 x 3072): the quantizing kernel up to 4 rows
+    # (no workspace), cooperative at 8 and 16
+    for n in (1, 2, 4):
+        assert q(n, 5120, 3072, 80, 48, 0) == 0
+    assert q(8, 5120, 3072, 80, 48, 0) == coop(8, 3072, 48) == 4096 + 6144 + 48
+    assert q(16, 3072, 3072, 48, 48, 0) == coop(16, 3072, 48)
+    # Gate/Up (16384 x 3072): 12-tile batches leave no room at 4 rows
+    assert q(4, 16384, 3072, 256, 48, 0) == coop(4, 3072, 48)
+    assert q(2, 16384, 3072, 256, 48, 0) == 0
+    # Qwen2.5-14B Q/K/V at 16 rows: beyond the fused path's 64 KiB of codes
+    assert q(16, 7168, 5120, 112, 80, 0) == 0
+    # an explicit split is the split-K kernel's workspace only
+    assert q(8, 5120, 3072, 80, 48, 2) == lib.tq_gemm_workspace_elems(8, 5120, 80, 48, 2) > 0
+    assert q(0, 5120, 3072, 80, 48, 0) == 0
+    assert q(100, 5120, 3072, 80, 48, 0) == 0
+
+
 def _attention_plan(lib, batch, q_heads, kv_heads, max_len, rope, cus):
     s, w = ctypes.c_int(0), ctypes.c_int(0)
     rc = lib.tq_decode_attention_plan(batch, q_heads, kv_heads, max_len, int(rope), cus, ctypes.byref(s),

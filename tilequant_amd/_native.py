@@ -50,6 +50,8 @@ _SIGNATURES = {
                                 _i, _i, _i, _i, _i,
                                 _i, _i, _p, _i64, _p]),
     "tq_linear_mixed_fused_max_tokens": (_i, [_i]),
+    "tq_linear_mixed_fused_workspace_elems": (_i64, [_i, _i, _i, _i, _i, _i]),
+    "tq_test_set_coop_spin": (None, [_i]),
     "tq_gemm_mixed_rows_planned": (_i, [_p, _i64, _p,
                                         _p, _p, _p, _p,
                                         _p, _i64, _i,

@@ -73,7 +73,23 @@ struct GemmArgs {
   // n_first units take all their token blocks before the others start.
   const int32_t* units;
   int n_units, n_first;
+  // Cooperative quantize + GEMM (gemm_decode_kernel<..., COOP>): the first
+  // coop_p workgroups write the activation codes to xq / sx; coop is the
+  // workspace head of ready flags and counts (kCoop* below); a GEMM workgroup
+  // waits at most coop_spin polls, then quantizes locally.
+  int32_t* coop;
+  int coop_p, coop_spin;
 };
+
+// COOP workspace head (int32 entries, zero between launches): GEMM workgroup
+// c polls the ready flag of group g = c % kCoopGroups at kCoopStride * g, and
+// counts itself passed right after it; the producers count themselves done at
+// kCoopCount.  One flag per group and one 128-byte line per flag: a single
+// flag polled by every workgroup of a large grid serialises the polls (and
+// the counts) at one memory channel.
+constexpr int kCoopGroups = 64;
+constexpr int kCoopStride = 32;
+constexpr int kCoopCount = kCoopGroups * kCoopStride;
 
 constexpr int32_t kUnitSingle = 1 << 30;
 
@@ -560,6 +576,97 @@ gemm_splitk_kernel(GemmArgs a) {
 
 constexpr int kDecCodesMax = 96 * 1024;   // LDS bytes for staged codes
 
+// ---- cooperative activation quantization (COOP decode launches) -------------
+// The decode GEMM's input codes are a function of all n rows of each 64-column
+// tile (the scale is the tile's absmax over every row), so a GEMM workgroup
+// cannot start its MFMAs before the whole tile is quantized.  Two launches
+// (quantizer, then GEMM) pay a launch; quantizing in every GEMM workgroup
+// repeats the work hundreds of times.  COOP launches do it once: producer
+// workgroup p < P quantizes column tiles [n_tc p / P, n_tc (p + 1) / P) with
+// the closed form of tq_act_quant, stores codes and scales with write-through
+// (agent-scope, sc1) stores, waits until they are acknowledged and counts
+// itself done; the GEMM workgroups issue their weight loads first and fetch
+// the codes, with agent-scope loads, once all P producers are done.
+
+// Group g of a COOP launch is passed by each of its GEMM workgroups (after its
+// last poll) and by the last producer (after raising the flag); whoever
+// brings the count to the group's size + 1 zeroes the flag and the count, so
+// no poll and no count of this launch lands after the reset.
+__device__ inline void coop_pass(const GemmArgs& a, int g) {
+  const int consumers = (int)gridDim.x - a.coop_p;
+  const int size = consumers / kCoopGroups + (g < consumers % kCoopGroups ? 1 : 0);
+  int32_t* f = a.coop + g * kCoopStride;
+  const int prev = __hip_atomic_fetch_add(f + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (prev == size) {
+    __hip_atomic_store(f, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(f + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Producer p: codes of its column tiles, over all n <= 16 rows, into a.xq
+// (row stride a.ldq) and a.sx.  dsm holds [tiles] absmax bit patterns.
+template <class XT>
+__device__ void coop_produce(const GemmArgs& a, int p, int8_t* dsm) {
+  const int P = a.coop_p;
+  const int c0 = (int)((int64_t)a.n_tc * p / P), c1 = (int)((int64_t)a.n_tc * (p + 1) / P);
+  const int nt = c1 - c0;
+  const int T = blockDim.x;
+  uint32_t* amax = reinterpret_cast<uint32_t*>(dsm);
+  for (int i = threadIdx.x; i < nt; i += T) amax[i] = 0u;
+  __syncthreads();
+  // item i = ((row * nt) + tile) * 8 + chunk: the 8 chunks of a (row, tile)
+  // are 8 aligned consecutive lanes (items and T are multiples of 8)
+  const int items = a.n * nt * 8;
+  auto x_at = [&](int i, int& row, int& c, int& col) {
+    row = i / (nt * 8);
+    const int rem = i - row * nt * 8;
+    c = c0 + (rem >> 3);
+    col = c * 64 + (rem & 7) * 8;
+    return *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + col);
+  };
+  for (int i = threadIdx.x; i < items; i += T) {
+    int row, c, col;
+    const u32x4 x = x_at(i, row, c, col);
+    uint32_t m = __float_as_uint(max8<XT>(x, 0.0f));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));    // quad_perm 1,0,3,2
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));    // quad_perm 2,3,0,1
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    if ((threadIdx.x & 7) == 0) __hip_atomic_fetch_max(amax + (c - c0), m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t qr = row_rsrc(a.xq, (int)((int64_t)(a.n - 1) * a.ldq + a.k));
+  for (int i = threadIdx.x; i < items; i += T) {
+    int row, c, col;
+    const u32x4 x = x_at(i, row, c, col);
+    const float s = act_scale_from_absmax<XT>(__uint_as_float(amax[c - c0]));
+    const CodeScale cq(s, 1.0f / s);
+    const u32x2 q = codes8<XT>(x, cq);
+    // write-through to the coherence point (sc1), like the agent-scope stores
+    __builtin_amdgcn_raw_buffer_store_b64(q, qr, (int)((int64_t)row * a.ldq + col), 0, 16);
+  }
+  for (int t = threadIdx.x; t < nt; t += T) {
+    const float s = act_scale_from_absmax<XT>(__uint_as_float(amax[t]));
+    __hip_atomic_store(const_cast<float*>(a.sx) + c0 + t, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // every store acknowledged before the count moves (gfx9 stores count in vmcnt)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    int prev = 0;
+    if (threadIdx.x == 0) prev = __hip_atomic_fetch_add(a.coop + kCoopCount, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev == P - 1) {
+      // the last producer: every code and scale is acknowledged.  Zero the
+      // count (all P have landed), raise the 64 groups' flags (lane g: group
+      // g), and once they are acknowledged count itself into every group.
+      if (threadIdx.x == 0) __hip_atomic_store(a.coop + kCoopCount, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.coop + threadIdx.x * kCoopStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      coop_pass(a, threadIdx.x);
+    }
+  }
+}
+
 
 // Byte offset of this lane's 16-byte B-operand chunk of j-block jb, k-half h
 // inside a 16-bit tile (the element offsets of load_w16, times two).
@@ -575,22 +682,40 @@ __device__ inline int w8_lane_offset(int layout, int lane) {
   return layout == TQ_LAYOUT_MFMA ? lane * 16 : (lane & 15) * 64 + (lane >> 4) * 16;
 }
 
-template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP = false>
+// COOP (one token block, one-j-block workgroups, codes not quantized in the
+// workgroup): a cooperative quantize + GEMM launch.  Workgroups below a.coop_p
+// are producers (coop_produce); the others are GEMM units with one extra
+// wave, the loader, beyond the W waves that take tiles.  The loader polls the
+// producers' count (bounded by a.coop_spin), then every thread loads the codes
+// with agent-scope loads into LDS -- or, if the count never arrived, the
+// workgroup quantizes the activation itself (same closed form, same codes).
+// The W tile waves issue their weights first, so the wait overlaps them.
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP = false, bool COOP = false>
 __global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
 gemm_decode_kernel(GemmArgs a) {
+  static_assert(!COOP || (!QUANT && TB == 1 && JBW == 1), "cooperative launches: codes from producers, n <= 16");
   extern __shared__ __align__(16) int8_t dsm[];
   constexpr int NJG = 4 / JBW;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int T = blockDim.x, W = T >> 6;
+  const int T = blockDim.x, W = COOP ? (T >> 6) - 1 : (T >> 6);
+  int bid = blockIdx.x;
+  if constexpr (COOP) {
+    if (bid < a.coop_p) {
+      coop_produce<XT>(a, bid, dsm);
+      return;
+    }
+    bid -= a.coop_p;   // coop_p % 8 == 0: the unit keeps its XCD
+  }
+  const bool loader = COOP && wave == W;
   // Workgroups are dealt to the 8 XCDs round-robin, so ids b, b+8, b+16, b+24
   // share an XCD: with one j-block per workgroup they take the four quarters
   // of the same row tile, back to back (each 4 KiB tile is then read by one
   // XCD in close succession instead of by four; a bijection on the units
   // when n_tr % 8 == 0, the identity otherwise).
-  int unit = blockIdx.x;
+  int unit = bid;
   if (NJG == 4 && (a.n_tr & 7) == 0) {
-    const int b = blockIdx.x, xcd = b & 7, slot = b >> 3;
+    const int b = bid, xcd = b & 7, slot = b >> 3;
     unit = (((slot >> 2) << 3) + xcd) * 4 + (slot & 3);
   }
   const int r = unit / NJG, jb0 = (unit - (unit / NJG) * NJG) * JBW;
@@ -608,17 +733,19 @@ gemm_decode_kernel(GemmArgs a) {
   const int cpr = QUANT ? (a.k >> 3) : (a.k >> 4);   // chunks per row
   const int total = a.n * cpr;
   u32x4 xr[CMAX];
-#pragma unroll
-  for (int j = 0; j < CMAX; ++j) {
-    const int i = min((int)threadIdx.x + j * T, total - 1);
-    const int row = i / cpr, ch = i - row * cpr;
-    if constexpr (QUANT) xr[j] = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
-    else xr[j] = *reinterpret_cast<const u32x4*>(a.xq + (int64_t)row * a.ldq + ch * 16);
-  }
   float sxr[2] = {0.0f, 0.0f};
-  if constexpr (!QUANT) {
+  if constexpr (!COOP) {   // COOP: the codes are read once the producers are done
 #pragma unroll
-    for (int h = 0; h < 2; ++h) sxr[h] = a.sx[min((int)threadIdx.x + h * T, n_tc - 1)];
+    for (int j = 0; j < CMAX; ++j) {
+      const int i = min((int)threadIdx.x + j * T, total - 1);
+      const int row = i / cpr, ch = i - row * cpr;
+      if constexpr (QUANT) xr[j] = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
+      else xr[j] = *reinterpret_cast<const u32x4*>(a.xq + (int64_t)row * a.ldq + ch * 16);
+    }
+    if constexpr (!QUANT) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) sxr[h] = a.sx[min((int)threadIdx.x + h * T, n_tc - 1)];
+    }
   }
 
   // ---- 2. this wave's first batch of INT8 tiles, issued unconditionally:
@@ -649,7 +776,7 @@ gemm_decode_kernel(GemmArgs a) {
                                                wrs, (q0 + u * W) * 4096 + woff + (jb0 + j) * 1024, 0, 0));
   };
   const int first_q = wave;
-  load_batch(first_q);
+  if (!loader) load_batch(first_q);   // the COOP loader wave takes no tiles
 
   // The first U16 16-bit tiles of this wave (their rotation continues after
   // the INT8 tiles), prefetched the same way.  Without 16-bit tiles the
@@ -666,7 +793,8 @@ gemm_decode_kernel(GemmArgs a) {
   // Lane i: the id of the wave's 16-bit tile i (position first16 + i W), for
   // its first 64 tiles -- the prefetched ones and the first window of the
   // loop below, which then needs no ids round trip of its own.
-  const int id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + lane * W) * 4, 0, 0);
+  int id16l = 0;
+  if (!loader) id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + lane * W) * 4, 0, 0);
   v4i b16p[U16][JBW][2];
   auto load_w16_at = [&](v4i (&dst)[JBW][2], int q) {
 #pragma unroll
@@ -676,10 +804,74 @@ gemm_decode_kernel(GemmArgs a) {
         dst[j][h] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
                                                 w16rs, q * 8192 + w16_lane_offset(a.layout, jb0 + j, h, lane), 0, 0));
   };
+  if (!loader) {
 #pragma unroll
-  for (int u = 0; u < U16; ++u) load_w16_at(b16p[u], first16 + u * W);
+    for (int u = 0; u < U16; ++u) load_w16_at(b16p[u], first16 + u * W);
+  }
 
   // ---- 3. activation -> LDS
+  bool staged = false;   // COOP fallback: the workgroup quantized into LDS itself
+  if constexpr (COOP) {
+    // the loader polls the producers' count; its verdict goes to every wave
+    // through LDS (the barrier waits for LDS operations only: the weights
+    // stay in flight)
+    __shared__ int coop_ready;
+    if (loader) {
+      int ready = 0;
+      for (int it = 0; it < a.coop_spin; ++it) {
+        if (__hip_atomic_load(a.coop + (bid % kCoopGroups) * kCoopStride, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT) != 0) {
+          ready = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (lane == 0) coop_ready = ready;
+    }
+    lds_barrier();
+    if (coop_ready) {
+      // the codes (and scales) the producers wrote through to the coherence
+      // point, read past this XCD's L2 (sc1), CMAX 16-byte chunks per thread
+      // the codes are the workspace's [n][k] (row stride k: 32-bit offsets)
+      const __amdgpu_buffer_rsrc_t xqr = row_rsrc(a.xq, a.n * a.k);
+      const __amdgpu_buffer_rsrc_t sxr_rs = row_rsrc(a.sx, n_tc * 4);
+#pragma unroll
+      for (int j = 0; j < CMAX; ++j) {
+        const int i = min((int)threadIdx.x + j * T, total - 1);
+        xr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xqr, i * 16, 0, 16));
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        sxr[h] = __int_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(sxr_rs, min((int)threadIdx.x + h * T, n_tc - 1) * 4, 0, 16));
+    } else {
+      // the producers' count never arrived within the poll budget: quantize
+      // here (the closed form of tq_act_quant: the codes are the same)
+      uint32_t* amx = reinterpret_cast<uint32_t*>(sxl + n_tc);   // [n_tc]
+      const int cq8 = a.k >> 3;                                  // 8-value chunks per row
+      for (int c = threadIdx.x; c < n_tc; c += T) amx[c] = 0u;
+      lds_barrier();
+      for (int i = threadIdx.x; i < a.n * cq8; i += T) {   // 8 chunks of a (row, tile): 8 aligned lanes
+        const int row = i / cq8, ch = i - row * cq8;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
+        uint32_t m = __float_as_uint(max8<XT>(x, 0.0f));
+        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));    // quad_perm 1,0,3,2
+        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));    // quad_perm 2,3,0,1
+        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));   // row_half_mirror
+        if ((threadIdx.x & 7) == 0) __hip_atomic_fetch_max(amx + (ch >> 3), m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      lds_barrier();
+      for (int c = threadIdx.x; c < n_tc; c += T) sxl[c] = act_scale_from_absmax<XT>(__uint_as_float(amx[c]));
+      lds_barrier();
+      for (int i = threadIdx.x; i < a.n * cq8; i += T) {
+        const int row = i / cq8, ch = i - row * cq8;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
+        const float sc = sxl[ch >> 3];
+        *reinterpret_cast<u32x2*>(codes + row * ldc + ch * 8) = codes8<XT>(x, CodeScale(sc, 1.0f / sc));
+      }
+      staged = true;
+    }
+  }
   // One thread per 8-element chunk of a row (T == cpr): thread t holds chunk t
   // of rows 0 .. n-1 (slot j = row j), so the 8 chunks of column tile t / 8
   // sit in 8 aligned consecutive lanes.  Absmax over the thread's rows, then
@@ -740,7 +932,7 @@ gemm_decode_kernel(GemmArgs a) {
       const CodeScale cq(sxl[c], rcpl[c]);
       *reinterpret_cast<u32x2*>(codes + row * ldc + ch * 8) = codes8<XT>(xr[j], cq);
     }
-  } else {
+  } else if (!staged) {
 #pragma unroll
     for (int j = 0; j < CMAX; ++j) {
       const int i = min((int)threadIdx.x + j * T, total - 1);
@@ -759,6 +951,7 @@ gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[j][tb] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  if (!loader) {   // the COOP loader wave has no tiles: its partial is not summed
   // ---- 4. INT8 tiles: A operand from LDS
   for (int q0 = first_q; q0 < n8; q0 += UMAX * W) {
     if (q0 != first_q) load_batch(q0);
@@ -845,16 +1038,20 @@ gemm_decode_kernel(GemmArgs a) {
     }
   }
 
+  }   // !loader
+
   // ---- waves -> LDS (reusing the code area) -> sum in wave order -> store
   constexpr int E = JBW * TB * 4 * 64;   // (j, tb, v, lane)
   float* red = reinterpret_cast<float*>(dsm);
   lds_barrier();   // every wave is done reading codes and scales
+  if (!loader) {
 #pragma unroll
-  for (int j = 0; j < JBW; ++j)
+    for (int j = 0; j < JBW; ++j)
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb)
+      for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[wave * E + ((j * TB + tb) * 4 + v) * 64 + lane] = acc[j][tb][v];
+        for (int v = 0; v < 4; ++v) red[wave * E + ((j * TB + tb) * 4 + v) * 64 + lane] = acc[j][tb][v];
+  }
   lds_barrier();
   for (int e = threadIdx.x; e < E; e += T) {
     const int ln = e & 63, t = e >> 6, v = t & 3, tb = (t >> 2) % TB, j = (t >> 2) / TB;
@@ -872,6 +1069,9 @@ gemm_decode_kernel(GemmArgs a) {
       if (a.bias) y = Fp16::from_f32(Fp16::to_f32(y) + Fp16::to_f32(a.bias[col]));
     }
     a.out[(int64_t)row * a.ldo + col] = y;
+  }
+  if constexpr (COOP) {
+    if (threadIdx.x == 0) coop_pass(a, bid % kCoopGroups);
   }
 }
 
@@ -2125,6 +2325,85 @@ static hipError_t launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStr
   }
 }
 
+// ---- cooperative quantize + GEMM plan ----------------------------------------
+// COOP launches (gemm_decode_kernel<..., COOP>, one token block, one-j-block
+// units) take the one-launch shapes the LDS-staged quantizing decode kernel
+// cannot (too many rows x columns for its chunks per thread), which otherwise
+// go to the quantizing split-K kernel.  Measured on MI355X (cold weights, per
+// launch): Llama-3.2-3B Q/K/V at 8 rows 10.4 us vs 18.0, at 16 rows 12.5 vs
+// 22.7; Gate/Up at 4 rows 20.9 vs 22.3; Qwen2.5-7B Gate/Up at 4 rows 44.0 vs
+// 54.2.  Where the LDS-staged kernel applies it stays: its workgroups start
+// their MFMAs without the hand-off's round trips (write-through codes, a
+// count, a flag, a poll and coherent reloads, ~3-5 us), e.g. Q/K/V at one row
+// 8.4 us vs 9.7 cooperative.  Producers: 8 (one per XCD, so the units keep
+// their XCD).  Workspace (fp32 elements): the
+// flags and counts (kCoopCount + 1 entries, inside the split-K counter region:
+// both leave it zero), then the codes [n][k] and the scales [n_tc].
+constexpr int kCoopProducers = 8;
+constexpr int kCoopSpin = 4096;   // polls (plus s_sleep) before a workgroup quantizes itself
+// The codes go where split-K launches put their scratch partials: after the
+// counter region, which must stay zero between launches.
+constexpr int64_t kCoopHead = kCounterCap;
+static_assert(kCoopCount + 1 <= kCoopHead && kCoopGroups == 64, "COOP flags: one per lane, inside the head");
+// Poll budget of COOP launches (-1: kCoopSpin); tests set 0 to make every
+// GEMM workgroup take its quantize-locally path.
+static std::atomic<int> g_coop_spin{-1};
+
+struct CoopPlan {
+  DecodePlan d;   // W = tile waves; the launch adds the loader wave
+  bool ok;
+};
+
+static CoopPlan plan_coop(int n, int k, int n_tr, int n_tc) {
+  CoopPlan c{};
+  c.ok = false;
+  if (n < 1 || n > kFusedMaxTokens || k != 64 * n_tc) return c;
+  c.d = plan_decode(n, k, n_tr, n_tc, false);
+  if (!c.d.ok || c.d.jbw != 1 || c.d.tb != 1 || c.d.W > 15) return c;
+  if (plan_decode(n, k, n_tr, n_tc, true).ok) return c;   // the LDS-staged quantizing kernel takes it
+  // codes chunks per thread with the loader wave; the fallback's absmax array after the scales
+  const int64_t T = (int64_t)(c.d.W + 1) * kWave;
+  const int64_t per = ((int64_t)n * k / 16 + T - 1) / T;
+  c.d.cmax = per <= 1 ? 1 : (per <= 2 ? 2 : (per <= 4 ? 4 : 8));
+  if (per > 8 || n_tc > 2 * T || (c.d.umax == 16 && per > 4)) return c;   // (16-tile batches + 8 chunks spill)
+  const int64_t codes = (int64_t)n * (k + 16), meta = (int64_t)n_tc * 8, red = (int64_t)c.d.W * 1024;
+  const int64_t prod = (int64_t)(n_tc / kCoopProducers + 1) * 4;
+  c.d.lds = (size_t)std::max({codes + meta, red, prod});
+  c.ok = c.d.lds <= kDecCodesMax + 16 * 1024;
+  return c;
+}
+
+static int64_t coop_workspace_elems(int n, int k, int n_tc) {
+  return kCoopHead + (((int64_t)n * k + 15) / 16) * 4 + n_tc;
+}
+
+template <class XT, int UMAX, int CMAX, bool DUMP>
+static hipError_t launch_coop_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  constexpr auto kern = gemm_decode_kernel<XT, 1, 1, UMAX, false, CMAX, DUMP, true>;
+  const hipError_t e = allow_lds<kern>(p.lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(a.coop_p + a.n_tr * 4), dim3((p.W + 1) * kWave), p.lds, s, a);
+  return hipGetLastError();
+}
+
+template <class XT, int UMAX, bool DUMP>
+static hipError_t launch_coop_c(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  switch (p.cmax) {
+    case 1: return launch_coop_one<XT, UMAX, 1, DUMP>(a, p, s);
+    case 2: return launch_coop_one<XT, UMAX, 2, DUMP>(a, p, s);
+    case 4: return launch_coop_one<XT, UMAX, 4, DUMP>(a, p, s);
+    default: return launch_coop_one<XT, UMAX, 8, DUMP>(a, p, s);
+  }
+}
+
+// a.xq / a.sx / a.coop point into the workspace (coop_workspace_elems).
+template <class XT, bool DUMP = false>
+static hipError_t launch_coop(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  if (p.umax == 12) return launch_coop_c<XT, 12, DUMP>(a, p, s);
+  if (p.umax == 16) return launch_coop_c<XT, 16, DUMP>(a, p, s);
+  return launch_coop_c<XT, kDecUmaxJb1, DUMP>(a, p, s);
+}
+
 template <class XT, bool QUANT, bool DUMP = false>
 static hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
   if (p.jbw == 4) {
@@ -2427,6 +2706,22 @@ static int linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dty
   a.ovec = (a.ldo % 8) == 0 && aligned16(a.out);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
+  if (split_k <= 1 && a.xvec && workspace != nullptr && ((uintptr_t)workspace & 15u) == 0) {
+    const CoopPlan c = plan_coop(n, k, n_tr, n_tc);
+    if (c.ok && workspace_elems >= coop_workspace_elems(n, k, n_tc)) {
+      a.coop = reinterpret_cast<int32_t*>(workspace);
+      a.coop_p = kCoopProducers;
+      const int spin = g_coop_spin.load(std::memory_order_relaxed);
+      a.coop_spin = spin >= 0 ? spin : kCoopSpin;
+      a.xq = reinterpret_cast<int8_t*>(workspace + kCoopHead);
+      a.ldq = k;
+      a.sx = workspace + kCoopHead + (((int64_t)n * k + 15) / 16) * 4;
+      if (kernel != nullptr) *kernel = TQ_KERNEL_DECODE_COOP;
+      if constexpr (DUMP) e = launch_coop<Bf16, true>(a, c.d, s);
+      else e = (x_dtype == TQ_DTYPE_BF16) ? launch_coop<Bf16>(a, c.d, s) : launch_coop<Fp16>(a, c.d, s);
+      return (int)e;
+    }
+  }
   if (split_k <= 1 && a.xvec && plan_decode(n, k, n_tr, n_tc, true).ok) {
     const DecodePlan d = plan_decode(n, k, n_tr, n_tc, true);
     if (kernel != nullptr) *kernel = TQ_KERNEL_DECODE_QUANT;
@@ -2443,6 +2738,17 @@ static int linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dty
                                       : launch_split<Fp16, true>(a, p, workspace, s);
   return (int)e;
 }
+
+extern "C" int64_t tq_linear_mixed_fused_workspace_elems(int n, int m, int k, int n_tr, int n_tc, int split_k) {
+  if (n <= 0 || n_tr <= 0 || n_tc <= 0 || n > kDecodeMaxTokens) return 0;
+  int64_t need = split_workspace_elems(plan_split(n, n_tr, n_tc, split_k), n, n_tr);
+  (void)m;
+  if (split_k <= 1 && n <= kFusedMaxTokens && fused_lds_bytes(n, n_tc) <= kFusedMaxLds && plan_coop(n, k, n_tr, n_tc).ok)
+    need = std::max(need, coop_workspace_elems(n, k, n_tc));
+  return need;
+}
+
+extern "C" void tq_test_set_coop_spin(int polls) { g_coop_spin.store(polls < 0 ? -1 : polls); }
 
 extern "C" int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
                                      const int8_t* int8_tiles, const float* int8_scales,

@@ -68,6 +68,15 @@ def _workspace(device, n, M, n_tr, n_tc, split_k):
     return (nat.ptr(ws), ws.numel()) if ws is not None else (None, 0)
 
 
+def _fused_workspace(device, n, M, K, n_tr, n_tc, split_k):
+    """The per-stream workspace linear_mixed_fused needs: split-K counters and
+    partials, or the cooperative launch's counters, codes and scales."""
+    elems = int(nat.lib().tq_linear_mixed_fused_workspace_elems(int(n), int(M), int(K), int(n_tr), int(n_tc),
+                                                                int(split_k or 0)))
+    ws = _WORKSPACE.get(device, elems)
+    return (nat.ptr(ws), ws.numel()) if ws is not None else (None, 0)
+
+
 class PrefillPlan:
     """Work plan for the prefill GEMM over one packed weight: ``units`` (a
     device int32 tensor) lists row-tile pairs and single row tiles (value
@@ -255,7 +264,10 @@ def linear_mixed_fused(
     at most FUSED_MAX_TOKENS rows).  Same result, bit for bit, as
     ``quantize_activation_tile_absmax`` followed by ``gemm_mixed_rows_splitk``
     with the same ``split_k``; no reference counterpart (the reference always
-    launches the two kernels, mixed_linear.py:233-239)."""
+    launches the two kernels, mixed_linear.py:233-239).  Shapes with too many
+    rows x columns for the LDS-staged quantizing kernel run cooperatively: 8
+    workgroups quantize once into the per-stream workspace while the GEMM
+    workgroups' weight loads are in flight (tq_linear_mixed_fused)."""
     nat.require_device(x_fp, int8_tiles, int8_scales, int8_tile_ids, int8_row_ptr, fp16_tiles, fp16_tile_ids,
                        fp16_row_ptr, bias, out)
     n = int(x_fp.shape[0])
@@ -276,7 +288,7 @@ def linear_mixed_fused(
         raise ValueError("bias must be a contiguous tensor of out_dtype with M entries")
     if n == 0 or M == 0:
         return out
-    ws_ptr, ws_elems = _workspace(x_fp.device, n, M, n_tr, n_tc, split_k)
+    ws_ptr, ws_elems = _fused_workspace(x_fp.device, n, M, K, n_tr, n_tc, split_k)
     args = (nat.ptr(x_fp), x_fp.stride(0), nat.dtype_code(x_fp.dtype),
             nat.ptr(int8_tiles), nat.ptr(int8_scales), nat.ptr(int8_tile_ids), nat.ptr(int8_row_ptr),
             nat.ptr(fp16_tiles) if has16 else None, nat.ptr(fp16_tile_ids) if has16 else None,
@@ -296,7 +308,7 @@ def linear_mixed_fused(
 
 # TQ_KERNEL_* codes of include/tilequant.h
 KERNEL_FAMILIES = {1: "decode", 2: "decode_quant", 3: "splitk", 4: "splitk_token_blocked", 5: "splitk_quant",
-                   6: "prefill_v5", 7: "prefill_v3", 8: "prefill_async", 9: "prefill_register"}
+                   6: "prefill_v5", 7: "prefill_v3", 8: "prefill_async", 9: "prefill_register", 10: "decode_coop"}
 
 
 def gemm_mixed_rows_products_i32(*, rows: Optional[Tuple[int, int]] = None, fused: bool = False, **kwargs):

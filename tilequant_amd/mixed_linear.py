@@ -40,8 +40,8 @@ import torch
 import torch.nn as nn
 
 from . import _native as nat
-from .gemm_rows_splitk_64x64 import (PrefillPlan, fused_max_tokens, gemm_mixed_rows_splitk, linear_mixed_fused,
-                                     prefill_plan)
+from .gemm_rows_splitk_64x64 import (PrefillPlan, _fused_workspace, _workspace, fused_max_tokens,
+                                     gemm_mixed_rows_splitk, linear_mixed_fused, prefill_plan)
 from .pack import Pack, concat_packs_along_rows
 from .quantize_activation import quantize_activation_token_blocked, token_blocked_elems
 from .quant_utils import (
@@ -410,6 +410,14 @@ class MixedLinear(nn.Module):
             d.fp16_tiles, d.fp16_tile_ids = self.fp16_tiles.data_ptr(), self.fp16_tile_ids.data_ptr()
             d.fp16_row_ptr = self.fp16_row_ptr.data_ptr()
         d.bias = None if bias is None else bias.data_ptr()
+        # the per-stream workspace the uncached calls use (split-K partials and
+        # counters; the cooperative launch's counters, codes and scales), so an
+        # eager call takes the same kernels as a captured one
+        if fused:
+            d.workspace, d.workspace_elems = _fused_workspace(dev, n, self.M_orig, self.K_orig, self.n_tr,
+                                                              self.n_tc, 0)
+        else:
+            d.workspace, d.workspace_elems = _workspace(dev, n, self.M_orig, self.n_tr, self.n_tc, 0)
         return _Launch(d, keep, bias if bias is not None and bias is not self.bias else None)
 
     def _cached_forward(self, x_work: torch.Tensor) -> torch.Tensor:
