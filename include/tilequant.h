@@ -229,7 +229,10 @@ int tq_linear_mixed_fused_max_tokens(int k);
  * a workgroup quantizes by itself).  Same codes either way, so the outputs
  * equal the two-launch sequence's bitwise.  Launches on one stream share its
  * workspace in turn (each leaves the flags and counts zero); launches that
- * overlap on one workspace race. */
+ * overlap on one workspace race.  At 1-2 rows (and where neither the plain
+ * kernel nor a cooperative launch applies) the quantizing kernel may carry
+ * k / 512 extra helper waves that quantize while its tile waves issue their
+ * weights; same tile order, same outputs. */
 int tq_linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dtype,
                           const int8_t* int8_tiles, const float* int8_scales,
                           const int32_t* int8_tile_ids, const int32_t* int8_row_ptr,
@@ -294,7 +297,8 @@ enum {
   TQ_KERNEL_PREFILL_V3 = 7,             /* prefill DMA ring for k > 19456 */
   TQ_KERNEL_PREFILL_ASYNC = 8,          /* prefill DMA ring for k > 32768 */
   TQ_KERNEL_PREFILL_REGISTER = 9,       /* prefill through registers (unaligned rows or k % 64 != 0) */
-  TQ_KERNEL_DECODE_COOP = 10            /* LDS-staged decode kernel, codes from its producer workgroups */
+  TQ_KERNEL_DECODE_COOP = 10,           /* LDS-staged decode kernel, codes from its producer workgroups */
+  TQ_KERNEL_DECODE_QUANT_HELP = 11      /* quantizing decode kernel, helper waves quantize */
 };
 
 /* TEST-ONLY.  tq_gemm_mixed_rows_planned (prefill_units may be NULL, then it

@@ -126,12 +126,14 @@ def test_coop_graph_replays_with_eager_work_between():
         assert torch.equal(linear_mixed_fused(**kw), ref)   # eager calls between replays
 
 
-@pytest.mark.parametrize("n_tr,n", [(48, 4), (80, 4), (80, 1), (256, 2)])
-def test_shapes_the_quantizing_kernel_takes_keep_it(n_tr, n):
+@pytest.mark.parametrize("n_tr,n,family", [(48, 4, "decode_quant"), (80, 4, "decode_quant"),
+                                           (48, 1, "decode_quant_help"), (256, 2, "decode_quant")])
+def test_shapes_the_quantizing_kernel_takes_keep_it(n_tr, n, family):
     """Where the LDS-staged quantizing kernel fits (O and Q/K/V up to 4 rows,
-    Gate/Up up to 2), it runs: no producers, no hand-off round trips."""
+    Gate/Up up to 2), it runs -- with helper waves at 1-2 rows of 6-wave
+    workgroups: no producers, no hand-off round trips."""
     _, _, pack = _pack(n_tr, 48, 0.02, seed=11 + n)
     x = make_x(n, 3072, seed=12 + n).to(DEV)
     y, _, fam = gemm_mixed_rows_products_i32(fused=True, **_kw(pack, x))
-    assert fam == "decode_quant"
+    assert fam == family
     assert torch.equal(y, _two_launch(pack, x))

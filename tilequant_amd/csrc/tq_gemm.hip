@@ -690,15 +690,25 @@ __device__ inline int w8_lane_offset(int layout, int lane) {
 // with agent-scope loads into LDS -- or, if the count never arrived, the
 // workgroup quantizes the activation itself (same closed form, same codes).
 // The W tile waves issue their weights first, so the wait overlaps them.
-template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP = false, bool COOP = false>
+//
+// HELP (QUANT, one token block, one-j-block workgroups): k / 512 helper waves
+// beyond the W tile waves load the raw activation and quantize it by lanes
+// (one thread per 8-column chunk of a row) into LDS while the tile waves wait
+// on their weight issue, which the memory system throttles for microseconds;
+// in the plain QUANT kernel the same quantization runs in the tile waves after
+// their issue, on the critical path.  Same W, same per-wave tile order, same
+// codes: bitwise the plain kernel's outputs.
+template <class XT, int TB, int JBW, int UMAX, bool QUANT, int CMAX, bool DUMP = false, bool COOP = false,
+          bool HELP = false>
 __global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
 gemm_decode_kernel(GemmArgs a) {
   static_assert(!COOP || (!QUANT && TB == 1 && JBW == 1), "cooperative launches: codes from producers, n <= 16");
+  static_assert(!HELP || (QUANT && !COOP && TB == 1 && JBW == 1 && UMAX <= 8), "helper waves: lane quantizer");
   extern __shared__ __align__(16) int8_t dsm[];
   constexpr int NJG = 4 / JBW;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int T = blockDim.x, W = COOP ? (T >> 6) - 1 : (T >> 6);
+  const int T = blockDim.x, W = (T >> 6) - (COOP ? 1 : (HELP ? (a.k >> 9) : 0));
   int bid = blockIdx.x;
   if constexpr (COOP) {
     if (bid < a.coop_p) {
@@ -708,6 +718,10 @@ gemm_decode_kernel(GemmArgs a) {
     bid -= a.coop_p;   // coop_p % 8 == 0: the unit keeps its XCD
   }
   const bool loader = COOP && wave == W;
+  const bool idle = (COOP || HELP) && wave >= W;   // no tiles: the COOP loader, the HELP helpers
+  // HELP: helper thread tq of Tq = k / 8 takes chunk tq of every row
+  const int tq = HELP ? (int)threadIdx.x - W * 64 : (int)threadIdx.x;
+  const int Tq = HELP ? T - W * 64 : T;
   // Workgroups are dealt to the 8 XCDs round-robin, so ids b, b+8, b+16, b+24
   // share an XCD: with one j-block per workgroup they take the four quarters
   // of the same row tile, back to back (each 4 KiB tile is then read by one
@@ -734,10 +748,10 @@ gemm_decode_kernel(GemmArgs a) {
   const int total = a.n * cpr;
   u32x4 xr[CMAX];
   float sxr[2] = {0.0f, 0.0f};
-  if constexpr (!COOP) {   // COOP: the codes are read once the producers are done
+  if (!COOP && (!HELP || idle)) {   // COOP: the codes are read once the producers are done
 #pragma unroll
     for (int j = 0; j < CMAX; ++j) {
-      const int i = min((int)threadIdx.x + j * T, total - 1);
+      const int i = min(tq + j * Tq, total - 1);
       const int row = i / cpr, ch = i - row * cpr;
       if constexpr (QUANT) xr[j] = *reinterpret_cast<const u32x4*>(a.xf + (int64_t)row * a.ldx + ch * 8);
       else xr[j] = *reinterpret_cast<const u32x4*>(a.xq + (int64_t)row * a.ldq + ch * 16);
@@ -748,6 +762,34 @@ gemm_decode_kernel(GemmArgs a) {
     }
   }
 
+  // Quantization by lanes (one thread per 8-element chunk of a row, Tq == cpr):
+  // thread tq holds chunk tq of rows 0 .. n-1 (slot j = row j), so the 8
+  // chunks of column tile tq / 8 sit in 8 aligned consecutive lanes.  Absmax
+  // over the thread's rows, then over the 8 lanes by DPP; every lane of the
+  // group derives the scale, 1 / scale and its codes from the same bits -- no
+  // LDS atomics.  Same maximum (bit patterns of non-negative floats), same
+  // scale, same codes as the general path of step 3.
+  auto quantize_by_lanes = [&]() {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < CMAX; ++j)
+      if (j < a.n) m = max(m, __float_as_uint(max8<XT>(xr[j], 0.0f)));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));    // quad_perm 1,0,3,2
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));    // quad_perm 2,3,0,1
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    const float s = act_scale_from_absmax<XT>(__uint_as_float(m));
+    const CodeScale cq(s, 1.0f / s);
+#pragma unroll
+    for (int j = 0; j < CMAX; ++j)
+      if (j < a.n) *reinterpret_cast<u32x2*>(codes + j * ldc + tq * 8) = codes8<XT>(xr[j], cq);
+    if ((tq & 7) == 0) sxl[tq >> 3] = s;
+  };
+  // HELP: the helper waves' activation loads are their only loads, so they
+  // quantize as soon as those arrive, before any row-pointer round trip.
+  if constexpr (HELP) {
+    if (idle) quantize_by_lanes();
+  }
+
   // ---- 2. this wave's first batch of INT8 tiles, issued unconditionally:
   //         buffer loads bounded to the row's own tiles return 0 past its end
   //         instead of faulting, so no branch guards them and the waits below
@@ -756,6 +798,17 @@ gemm_decode_kernel(GemmArgs a) {
   //         back with v_readlane): scalar loads would share lgkmcnt with the
   //         LDS traffic, so every lds_barrier() below would wait for them.
   const int lo8 = a.rp8[r], hi8 = a.rp8[r + 1];
+  // The row's 16-bit range: HELP kernels load it with the INT8 range (their
+  // tile waves go from the weight issue straight to the staging barrier);
+  // the others after issuing their INT8 weights, which then do not wait for
+  // it (measured 0.3-0.5 us faster per launch).
+  const bool has16 = a.w16 != nullptr;
+  const int32_t* rp16p = has16 ? a.rp16 : a.rp8;
+  int lo16 = 0, n16 = 0;
+  if constexpr (HELP) {
+    lo16 = rp16p[r];
+    n16 = has16 ? rp16p[r + 1] - lo16 : 0;
+  }
   const int n8 = hi8 - lo8;
   const __amdgpu_buffer_rsrc_t wrs = row_rsrc(a.w8 + (int64_t)lo8 * 4096, n8 * 4096);
   const __amdgpu_buffer_rsrc_t irs = row_rsrc(a.ids8 + lo8, n8 * 4);
@@ -776,16 +829,16 @@ gemm_decode_kernel(GemmArgs a) {
                                                wrs, (q0 + u * W) * 4096 + woff + (jb0 + j) * 1024, 0, 0));
   };
   const int first_q = wave;
-  if (!loader) load_batch(first_q);   // the COOP loader wave takes no tiles
+  if (!idle) load_batch(first_q);   // the COOP loader and HELP helper waves take no tiles
 
   // The first U16 16-bit tiles of this wave (their rotation continues after
   // the INT8 tiles), prefetched the same way.  Without 16-bit tiles the
   // ranges are empty and these loads touch no memory.
   constexpr int U16 = JBW == 1 ? 2 : 1;
-  const bool has16 = a.w16 != nullptr;
-  const int32_t* rp16p = has16 ? a.rp16 : a.rp8;
-  const int lo16 = rp16p[r];
-  const int n16 = has16 ? rp16p[r + 1] - lo16 : 0;
+  if constexpr (!HELP) {
+    lo16 = rp16p[r];
+    n16 = has16 ? rp16p[r + 1] - lo16 : 0;
+  }
   const __amdgpu_buffer_rsrc_t w16rs =
       row_rsrc(has16 ? (const void*)(a.w16 + (int64_t)lo16 * 4096) : (const void*)a.rp8, n16 * 8192);
   const __amdgpu_buffer_rsrc_t i16rs = row_rsrc(has16 ? (const void*)(a.ids16 + lo16) : (const void*)a.rp8, n16 * 4);
@@ -794,7 +847,7 @@ gemm_decode_kernel(GemmArgs a) {
   // its first 64 tiles -- the prefetched ones and the first window of the
   // loop below, which then needs no ids round trip of its own.
   int id16l = 0;
-  if (!loader) id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + lane * W) * 4, 0, 0);
+  if (!idle) id16l = __builtin_amdgcn_raw_buffer_load_b32(i16rs, (first16 + lane * W) * 4, 0, 0);
   v4i b16p[U16][JBW][2];
   auto load_w16_at = [&](v4i (&dst)[JBW][2], int q) {
 #pragma unroll
@@ -804,7 +857,7 @@ gemm_decode_kernel(GemmArgs a) {
         dst[j][h] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
                                                 w16rs, q * 8192 + w16_lane_offset(a.layout, jb0 + j, h, lane), 0, 0));
   };
-  if (!loader) {
+  if (!idle) {
 #pragma unroll
     for (int u = 0; u < U16; ++u) load_w16_at(b16p[u], first16 + u * W);
   }
@@ -872,35 +925,18 @@ gemm_decode_kernel(GemmArgs a) {
       staged = true;
     }
   }
-  // One thread per 8-element chunk of a row (T == cpr): thread t holds chunk t
-  // of rows 0 .. n-1 (slot j = row j), so the 8 chunks of column tile t / 8
-  // sit in 8 aligned consecutive lanes.  Absmax over the thread's rows, then
-  // over the 8 lanes by DPP; every lane of the group derives the scale,
-  // 1 / scale and its codes from the same bits -- no LDS atomics and one
-  // barrier instead of four.  Same maximum (bit patterns of non-negative
-  // floats), same scale, same codes as the general path below.  The
-  // many-unit batches (UMAX 12 / 16) run 4 waves on more than 32 column
+  // Quantization by lanes (quantize_by_lanes) where the workgroup has one
+  // thread per 8-element chunk of a row (T == cpr): one barrier instead of
+  // four.  The many-unit batches (UMAX 12 / 16) run 4 waves on more than 32 column
   // tiles, so T < cpr there: not compiled in (it would cost them registers).
   // Measured on MI355X (Llama-3.2-3B projections, cold weights): 0.4-1.8 us
   // faster per launch at 2-4 rows; at one row 0.2 us faster with 16 waves
   // (four barriers cost more there) but 0.1-0.3 us slower with 6, so one-row
   // launches of fewer than 16 waves keep the general path.
   constexpr bool kQuantByLanes = QUANT && UMAX <= 8;
-  if (kQuantByLanes && T == cpr && (a.n >= 2 || T >= 1024)) {
-    uint32_t m = 0u;
-#pragma unroll
-    for (int j = 0; j < CMAX; ++j)
-      if (j < a.n) m = max(m, __float_as_uint(max8<XT>(xr[j], 0.0f)));
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));    // quad_perm 1,0,3,2
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));    // quad_perm 2,3,0,1
-    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));   // row_half_mirror
-    const float s = act_scale_from_absmax<XT>(__uint_as_float(m));
-    const CodeScale cq(s, 1.0f / s);
-#pragma unroll
-    for (int j = 0; j < CMAX; ++j)
-      if (j < a.n) *reinterpret_cast<u32x2*>(codes + j * ldc + (int)threadIdx.x * 8) = codes8<XT>(xr[j], cq);
-    if ((threadIdx.x & 7) == 0) sxl[threadIdx.x >> 3] = s;
-  } else if constexpr (QUANT) {
+  if (kQuantByLanes && (HELP || (T == cpr && (a.n >= 2 || T >= 1024)))) {
+    if constexpr (!HELP) quantize_by_lanes();   // HELP: the helpers did it before step 2
+  } else if constexpr (QUANT && !HELP) {
     for (int c = threadIdx.x; c < n_tc; c += T) amax[c] = 0u;
     lds_barrier();
 #pragma unroll
@@ -951,7 +987,7 @@ gemm_decode_kernel(GemmArgs a) {
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[j][tb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (!loader) {   // the COOP loader wave has no tiles: its partial is not summed
+  if (!idle) {   // the COOP loader and HELP helpers have no tiles: no partial of theirs is summed
   // ---- 4. INT8 tiles: A operand from LDS
   for (int q0 = first_q; q0 < n8; q0 += UMAX * W) {
     if (q0 != first_q) load_batch(q0);
@@ -1038,13 +1074,13 @@ gemm_decode_kernel(GemmArgs a) {
     }
   }
 
-  }   // !loader
+  }   // !idle
 
   // ---- waves -> LDS (reusing the code area) -> sum in wave order -> store
   constexpr int E = JBW * TB * 4 * 64;   // (j, tb, v, lane)
   float* red = reinterpret_cast<float*>(dsm);
   lds_barrier();   // every wave is done reading codes and scales
-  if (!loader) {
+  if (!idle) {
 #pragma unroll
     for (int j = 0; j < JBW; ++j)
 #pragma unroll
@@ -2325,6 +2361,81 @@ static hipError_t launch_decode_c(const GemmArgs& a, const DecodePlan& p, hipStr
   }
 }
 
+// ---- quantizing decode kernel with helper waves ------------------------------
+// gemm_decode_kernel<..., QUANT, ..., HELP>: the plain (non-quantizing) decode
+// plan's W tile waves -- so the sums are the two-launch path's, bit for bit --
+// plus k / 512 helper waves that quantize by lanes, one thread per 8-column
+// chunk of a row, all n <= 8 rows (CMAX = n rounded up), as soon as their
+// activation loads arrive.  For one-j-block workgroups with 8-tile batches and
+// at most 16 waves in all (Llama-3.2-3B Q/K/V and O: 6 + 6; Qwen2.5-7B: 7 + 7),
+// at 1-2 rows and where the plain quantizing kernel does not fit.  Measured on
+// MI355X (cold weights, per launch, plain -> helpers): Llama Q/K/V at one row
+// 8.42 -> 7.46 us, O 6.12 -> 5.29; at 2 rows 8.51 -> 8.53 and 6.09 -> 5.93;
+// at 4 rows Q/K/V 10.14 -> 10.00 but O 7.04 -> 7.30 (the helpers' quantization
+// then runs while the tile waves issue their weights and slows that issue),
+// so 4 rows keep the plain kernel.
+static DecodePlan plan_help(int n, int k, int n_tr, int n_tc) {
+  DecodePlan p = plan_decode(n, k, n_tr, n_tc, false);
+  const bool shape = p.ok && p.jbw == 1 && p.tb == 1 && p.umax == kDecUmaxJb1 && n <= 8 && (k & 511) == 0 &&
+                     p.W + k / 512 <= 16 && (n <= 2 || !plan_decode(n, k, n_tr, n_tc, true).ok);
+  p.ok = false;
+  if (!shape) return p;
+  p.cmax = n <= 1 ? 1 : (n <= 2 ? 2 : (n <= 4 ? 4 : 8));
+  const int64_t codes = (int64_t)n * (k + 16), meta = (int64_t)n_tc * 4 * 3, red = (int64_t)p.W * 1024;
+  p.lds = (size_t)std::max(codes + meta, red);
+  p.ok = codes <= kDecCodesMax;
+  return p;
+}
+
+static int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Launches the helper-wave kernel, or returns hipErrorNotSupported (nothing
+// launched) when its grid would not be resident at once: the helper waves
+// cost registers, and a second round of workgroups costs far more than the
+// helpers save (Qwen2.5-7B Q/K/V: 14-wave workgroups, two per CU needed).
+template <class XT, int CMAX, bool DUMP>
+static hipError_t launch_help_one(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  constexpr auto kern = gemm_decode_kernel<XT, 1, 1, kDecUmaxJb1, true, CMAX, DUMP, false, true>;
+  const int threads = (p.W + a.k / 512) * kWave;
+  const hipError_t e = allow_lds<kern>(p.lds);
+  if (e != hipSuccess) return e;
+  // resident workgroups per CU, cached per (waves, KiB of LDS): the query is
+  // host work every eager launch would repeat
+  static std::atomic<int> cache[17][161];
+  const size_t kib = (p.lds + 1023) / 1024;
+  std::atomic<int>* slot = (threads / kWave <= 16 && kib <= 160) ? &cache[threads / kWave][kib] : nullptr;
+  int per_cu = slot ? slot->load(std::memory_order_relaxed) : 0;
+  if (per_cu <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, kib * 1024) != hipSuccess) per_cu = 0;
+    if (slot && per_cu > 0) slot->store(per_cu, std::memory_order_relaxed);
+  }
+  if ((int64_t)per_cu * device_cus() < (int64_t)a.n_tr * 4) return hipErrorNotSupported;
+  hipLaunchKernelGGL(kern, dim3(a.n_tr * 4), dim3(threads), p.lds, s, a);
+  return hipGetLastError();
+}
+
+template <class XT, bool DUMP = false>
+static hipError_t launch_help(const GemmArgs& a, const DecodePlan& p, hipStream_t s) {
+  switch (p.cmax) {
+    case 1: return launch_help_one<XT, 1, DUMP>(a, p, s);
+    case 2: return launch_help_one<XT, 2, DUMP>(a, p, s);
+    case 4: return launch_help_one<XT, 4, DUMP>(a, p, s);
+    default: return launch_help_one<XT, 8, DUMP>(a, p, s);
+  }
+}
+
 // ---- cooperative quantize + GEMM plan ----------------------------------------
 // COOP launches (gemm_decode_kernel<..., COOP>, one token block, one-j-block
 // units) take the one-launch shapes the LDS-staged quantizing decode kernel
@@ -2720,6 +2831,17 @@ static int linear_mixed_fused(const void* x_fp, int64_t x_fp_stride_n, int x_dty
       if constexpr (DUMP) e = launch_coop<Bf16, true>(a, c.d, s);
       else e = (x_dtype == TQ_DTYPE_BF16) ? launch_coop<Bf16>(a, c.d, s) : launch_coop<Fp16>(a, c.d, s);
       return (int)e;
+    }
+  }
+  if (split_k <= 1 && a.xvec) {
+    const DecodePlan h = plan_help(n, k, n_tr, n_tc);
+    if (h.ok) {
+      if constexpr (DUMP) e = launch_help<Bf16, true>(a, h, s);
+      else e = (x_dtype == TQ_DTYPE_BF16) ? launch_help<Bf16>(a, h, s) : launch_help<Fp16>(a, h, s);
+      if (e != hipErrorNotSupported) {   // not resident at once: the plain quantizing kernel below
+        if (kernel != nullptr) *kernel = TQ_KERNEL_DECODE_QUANT_HELP;
+        return (int)e;
+      }
     }
   }
   if (split_k <= 1 && a.xvec && plan_decode(n, k, n_tr, n_tc, true).ok) {

@@ -308,7 +308,8 @@ def linear_mixed_fused(
 
 # TQ_KERNEL_* codes of include/tilequant.h
 KERNEL_FAMILIES = {1: "decode", 2: "decode_quant", 3: "splitk", 4: "splitk_token_blocked", 5: "splitk_quant",
-                   6: "prefill_v5", 7: "prefill_v3", 8: "prefill_async", 9: "prefill_register", 10: "decode_coop"}
+                   6: "prefill_v5", 7: "prefill_v3", 8: "prefill_async", 9: "prefill_register", 10: "decode_coop",
+                   11: "decode_quant_help"}
 
 
 def gemm_mixed_rows_products_i32(*, rows: Optional[Tuple[int, int]] = None, fused: bool = False, **kwargs):
