@@ -137,3 +137,23 @@ def test_shapes_the_quantizing_kernel_takes_keep_it(n_tr, n, family):
     y, _, fam = gemm_mixed_rows_products_i32(fused=True, **_kw(pack, x))
     assert fam == family
     assert torch.equal(y, _two_launch(pack, x))
+
+
+def test_coop_and_split_k_launches_share_one_stream_workspace():
+    """The cooperative launch's flags and counts sit in the split-K counter
+    region of the same per-stream workspace; each kind of launch leaves that
+    region zero, so alternating them on one stream changes no output."""
+    _, _, pack_c = _pack(256, 48, 0.01, seed=61)        # Gate/Up shape: cooperative at 4 rows
+    _, _, pack_s = _pack(48, 48, 0.02, seed=62)         # O shape: explicit split_k = 4
+    x_c = make_x(4, 3072, seed=63).to(DEV)
+    x_s = make_x(4, 3072, seed=64).to(DEV)
+    ref_c = _two_launch(pack_c, x_c)
+    xq, sx = quantize_activation_tile_absmax(x_s)
+    ref_s = gemm_mixed_rows_splitk(x_int8=xq, sx=sx, split_k=4, **_kw(pack_s, x_s))
+    kw_c = _kw(pack_c, x_c)
+    for _ in range(3):
+        _, _, fam = gemm_mixed_rows_products_i32(fused=True, **kw_c)
+        assert fam == "decode_coop"
+        assert torch.equal(linear_mixed_fused(**kw_c), ref_c)
+        assert torch.equal(gemm_mixed_rows_splitk(x_int8=xq, sx=sx, split_k=4, **_kw(pack_s, x_s)), ref_s)
+        assert torch.equal(linear_mixed_fused(split_k=4, **_kw(pack_s, x_s)), ref_s)
