@@ -40,6 +40,7 @@ import torch
 import torch.nn as nn
 
 from . import _native as nat
+from ._config import cfg_value
 from .gemm_rows_splitk_64x64 import (PrefillPlan, _fused_workspace, _workspace, fused_max_tokens,
                                      gemm_mixed_rows_splitk, linear_mixed_fused, prefill_plan)
 from .pack import Pack, concat_packs_along_rows
@@ -92,11 +93,6 @@ def _linear_forward():
 
 _LINEAR_FORWARD = [None]
 
-
-def _cfg_get(cfg: Any, key: str, default=None):
-    if isinstance(cfg, dict):
-        return cfg.get(key, default)
-    return getattr(cfg, key, default)
 
 
 def _view_key(t: torch.Tensor) -> Tuple[Any, ...]:
@@ -289,11 +285,11 @@ class MixedLinear(nn.Module):
                     **{name: getattr(self, name) for name in _BUFFERS}, tile_layout=self.tile_layout)
 
     def _out_dtype(self) -> torch.dtype:
-        dtype_out = _cfg_get(self.cfg, "dtype_out", "fp16")
+        dtype_out = cfg_value(self.cfg, "dtype_out", "fp16")
         return torch.bfloat16 if dtype_out in ("bf16", torch.bfloat16) else torch.float16
 
     def _activation_row_chunk_size(self) -> int:
-        return max(1, int(_cfg_get(self.cfg, "activation_row_chunk_size", DEFAULT_ACTIVATION_ROW_CHUNK_SIZE)))
+        return max(1, int(cfg_value(self.cfg, "activation_row_chunk_size", DEFAULT_ACTIVATION_ROW_CHUNK_SIZE)))
 
     def _out_bias(self, out_dtype: torch.dtype) -> Optional[torch.Tensor]:
         bias = self.bias
@@ -349,7 +345,7 @@ class MixedLinear(nn.Module):
         return limit
 
     def _fused_rows_for_cfg(self) -> int:
-        mode = _cfg_get(self.cfg, "fused_decode", None)
+        mode = cfg_value(self.cfg, "fused_decode", None)
         if mode is False:
             return 0
         if mode is None or mode == "auto":

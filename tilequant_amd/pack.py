@@ -25,6 +25,7 @@ from typing import Any, Dict, Optional, Sequence
 import torch
 
 from . import _native as nat
+from ._config import cfg_value
 
 TILE_LAYOUTS = ("row_major", "mfma")
 
@@ -50,11 +51,6 @@ class Pack:
     fp16_row_indices: torch.Tensor
     tile_layout: str = "row_major"
 
-
-def _cfg_get(cfg: Any, key: str, default=None):
-    if isinstance(cfg, dict):
-        return cfg.get(key, default)
-    return getattr(cfg, key, default)
 
 
 def _order_tile_ids_row_major(tile_ids: torch.Tensor) -> torch.Tensor:
@@ -98,10 +94,10 @@ def _pack_weight_with_tile_ids(
 ) -> Pack:
     if W_fp.dim() != 2:
         raise ValueError(f"Expected W to be 2D, got shape={tuple(W_fp.shape)}")
-    tile_m = int(_cfg_get(cfg, "tile_m", 64))
-    tile_n = int(_cfg_get(cfg, "tile_n", 64))
-    use_pad = bool(_cfg_get(cfg, "pad_to_tile", True))
-    quant_style = str(_cfg_get(cfg, "quant_style", "gi")).lower()
+    tile_m = int(cfg_value(cfg, "tile_m", 64))
+    tile_n = int(cfg_value(cfg, "tile_n", 64))
+    use_pad = bool(cfg_value(cfg, "pad_to_tile", True))
+    quant_style = str(cfg_value(cfg, "quant_style", "gi")).lower()
     if quant_style not in ("gi", "iaa"):
         raise ValueError(f"Unsupported quant_style={quant_style}. Expected one of: gi, iaa")
     if (tile_m, tile_n) != (64, 64):
