@@ -14,8 +14,8 @@
 // sharing kv head kvh, and writes a partial (running max m, sum l,
 // unnormalised o[D]) per query head; a second kernel merges the splits of
 // each (b, h) in split order.  Empty splits write m = -inf, l = 0.
-//   loads: all K and V rows of a wave's 32 keys are issued at entry (8 + 8
-//       16-byte loads per lane), so the chunk costs one memory round trip.
+//   loads: all K rows of a wave's 32 keys are issued at entry (8 16-byte
+//       loads per lane), its V rows (8 more) right after the QK MFMAs.
 //   QK on the matrix cores: per 16-key block, 4 v_mfma_f32_16x16x32 with the
 //       keys as A rows and the G query heads as B columns; each A operand is a
 //       plain 16-byte load of a key row.  The kernel is VALU-bound once its
@@ -185,8 +185,8 @@ attn_split_kernel(AttnArgs a) {
   const int kl = lane >> 4, ch = lane & 15;   // PV layout: keys 8 kl .. 8 kl + 7, 8-element chunk ch
   const int mr = lane & 15, mg = lane >> 4;   // MFMA layout: row / column index, k group
 
-  // ---- every load of the workgroup is issued up front: q, then all K and V
-  //      rows of this wave's keys (keys past the valid length are not read).
+  // ---- the loads go out up front: q, then all K rows of this wave's keys
+  //      (keys past the valid length are not read); the V rows after the QK.
   //      MFMA step ks covers dimensions 32 ks .. 32 ks + 31: lane (mr, mg)
   //      holds chunk 4 ks + mg of key mr of a 16-key block (A operand) and of
   //      query head mr (B operand; columns >= G repeat head G - 1, unused).
@@ -238,9 +238,6 @@ attn_split_kernel(AttnArgs a) {
     for (int ks = 0; ks < 4; ++ks)
       kb[blk][ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                   krs, kv_off(wkey0 + 16 * blk + mr, 4 * ks + mg), 0, 0));
-#pragma unroll
-  for (int i = 0; i < kSteps; ++i)
-    vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, kv_off(wkey0 + 8 * kl + i, ch), 0, 0));
   __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first use
 
   // RoPE form: the workgroup whose chunk holds the new position writes the
@@ -285,6 +282,19 @@ attn_split_kernel(AttnArgs a) {
     for (int ks = 0; ks < 4; ++ks)
       snew = mfma16<XT>(__builtin_bit_cast(v4i, kn[ks]), __builtin_bit_cast(v4i, qa[ks]), snew);
   }
+  // The value rows go out only now.  Every workgroup requests its K and V at
+  // once and the memory system accepts the loads only as earlier ones return,
+  // so a wave with V loads still waiting to issue could not start its QK on
+  // keys that had long arrived (measured on MI355X, configs[4] decode shape:
+  // split + merge 15.2 -> 14.1 us per layer; after the softmax 14.1, half
+  // before and half after the QK 14.5).  In the RoPE form the split that
+  // writes the new token's v may read that row back here: the value it reads
+  // is replaced by vnw in the PV either way.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i)
+    vw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, kv_off(wkey0 + 8 * kl + i, ch), 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- this wave's softmax over its 32 keys: lane (mr, mg) holds 8 scores of
   //      head mr; max and sum over them, then over the 4 lanes of the head
