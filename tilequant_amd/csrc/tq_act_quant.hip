@@ -84,6 +84,7 @@ template <class T>
 __global__ void __launch_bounds__(kQuantThreads)
 act_quant_fused_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, int nb) {
   __shared__ float red[kQuantThreads / kWave];
+  TQ_ARGS_IN_SGPRS("s"(v.x), "s"(v.sn), "s"(v.sk), "s"(v.n), "s"(v.k), "s"(q), "s"(ldq), "s"(sx), "s"(nb));
   const int c = blockIdx.x, t = threadIdx.x;
   const bool qvec = ((ldq % 8) == 0) && (((uintptr_t)q & 7u) == 0);
   if (v.n <= 2 * kRowsPerPass && tile_vec_ok(v, c) && (nb > 0 || qvec)) {
@@ -144,6 +145,7 @@ constexpr int kSmallMaxRows = 8;
 template <class T>
 __global__ void __launch_bounds__(kQuantThreads)
 act_quant_small_kernel(XView v, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, int n_tc) {
+  TQ_ARGS_IN_SGPRS("s"(v.x), "s"(v.sn), "s"(v.n), "s"(q), "s"(ldq), "s"(sx), "s"(n_tc));
   const int lane = threadIdx.x & (kWave - 1);
   const int c = blockIdx.x * (kQuantThreads / kWave) + (threadIdx.x >> 6);
   if (c >= n_tc) return;   // whole waves

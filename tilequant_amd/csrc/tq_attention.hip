@@ -173,6 +173,10 @@ attn_split_kernel(AttnArgs a) {
   __shared__ __align__(16) float wo[kWaves][KG][G][kAttnD];
   __shared__ float wml[kWaves][G][2];       // per-wave max, sum
   __shared__ __align__(16) float pl[kWaves][G][kKeysW];   // per-wave probabilities [head][key]
+  TQ_ARGS_IN_SGPRS("s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.k), "s"(a.v), "s"(a.kv_sb), "s"(a.kv_sl),
+                   "s"(a.kv_sh), "s"(a.seq_used), "s"(a.part), "s"(a.q_heads), "s"(a.kv_heads), "s"(a.max_len),
+                   "s"(a.n_splits), "s"(a.scale_log2));
+  if constexpr (ROPE) TQ_ARGS_IN_SGPRS("s"(a.cos), "s"(a.sin), "s"(a.pos), "s"(a.k_out), "s"(a.v_out));
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int s = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads, kvh = blockIdx.y - (blockIdx.y / a.kv_heads) * a.kv_heads;
@@ -454,6 +458,8 @@ __device__ inline float merge_splits(const AttnArgs& a, const float* rec, int d)
 template <class XT, int NB>
 __global__ void __launch_bounds__(kAttnD)
 attn_merge_kernel(AttnArgs a, L2Warm warm) {
+  TQ_ARGS_IN_SGPRS("s"(a.part), "s"(a.out), "s"(a.o_sb), "s"(a.o_sh), "s"(a.q_heads), "s"(a.n_splits),
+                   "s"(warm.first));
   if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
     __shared__ uint32_t warm_sink[64];
     l2_warm_rows<kAttnD>(warm, warm_sink);
@@ -483,6 +489,8 @@ __global__ void __launch_bounds__(kMergeQuantThreads)
 attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* __restrict__ sx, L2Warm warm) {
   constexpr int kGroups = kMergeQuantThreads / kWave;
   __shared__ float2 mls[kGroups * RPW][NB];
+  TQ_ARGS_IN_SGPRS("s"(a.part), "s"(a.out), "s"(a.o_sb), "s"(a.o_sh), "s"(a.batch), "s"(a.q_heads),
+                   "s"(a.n_splits), "s"(q), "s"(ldq), "s"(sx), "s"(warm.first));
   if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
     __shared__ uint32_t warm_sink[64];
     l2_warm_rows<kMergeQuantThreads>(warm, warm_sink);
@@ -490,7 +498,9 @@ attn_merge_quant_kernel(AttnArgs a, int8_t* __restrict__ q, int64_t ldq, float* 
   }
   __shared__ float red[kGroups];
   const int h = blockIdx.x >> 1, half = blockIdx.x & 1;
-  const int t = threadIdx.x, lane = t & 63, rg = t >> 6;
+  // the row group is wave-uniform: as a scalar, the buffer resources below
+  // are too (else every load of them is wrapped in a readfirstlane loop)
+  const int t = threadIdx.x, lane = t & 63, rg = __builtin_amdgcn_readfirstlane(t >> 6);
   const int d = half * 64 + lane;
   const int S = a.n_splits;
   const int64_t rec_elems = (int64_t)S * (kAttnD + 2);   // one (b, h)'s records

@@ -276,6 +276,14 @@ inline int l2_warm_args(const tq_l2_warm* in, int first, L2Warm& out) {
   return TQ_OK;
 }
 
+// Kernel arguments into SGPRs at kernel entry, all in one scalar round trip:
+// TQ_ARGS_IN_SGPRS("s"(a.x), "s"(a.n), ...).  Left alone, the compiler loads
+// each argument just before its first use, so a uniform branch or an early
+// return between two uses puts a whole scalar memory round trip in front of
+// the kernel's first vector load (the decode glue kernels paid two or three
+// of them).
+#define TQ_ARGS_IN_SGPRS(...) asm volatile("" ::__VA_ARGS__)
+
 // Workgroup barrier for LDS hand-offs that leaves outstanding global loads in
 // flight: waits only for this wave's LDS operations (lgkmcnt(0); vmcnt and
 // expcnt at their maxima in the gfx9 s_waitcnt encoding), then s_barrier.

@@ -95,11 +95,25 @@ __device__ inline float dot2sq(uint32_t w, float acc) {
   }
 }
 
-template <class XT>
+// Byte offset of element (row, col) of a [*, k] matrix with row stride ld
+// (elements), or an offset past any buffer range for rows >= n: the load
+// reads 0 and the store is dropped, with no branch.  Rows < n fit 31 bits
+// (the host checks ((n - 1) * ld + k) * esize < 2^31).
+__device__ inline int row_off(int row, int n, int64_t ld, int col, int esize) {
+  return row < n ? (int)(((int64_t)row * ld + col) * esize) : 0x7fffffff;
+}
+
+// workgroup c: every row's sum of squares over all k columns (each wave takes
+// rows wave, wave + 4, ...), then the 64 columns of tile c for every row:
+// thread t takes rows wave + 4 i, i < TR (TR >= n / 4, a template constant so
+// that no slot costs a branch), column c * 64 + t % 64.
+template <class XT, bool HAS_DELTA, int TR>
 __global__ void __launch_bounds__(kFuseThreads)
 add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
   __shared__ float rinv[64];          // 1 / sqrt(mean(h^2) + eps) per row (n <= 64)
   __shared__ float red[kFuseThreads / kWave];
+  TQ_ARGS_IN_SGPRS("s"(a.x), "s"(a.delta), "s"(a.w), "s"(a.h), "s"(a.y), "s"(a.q), "s"(a.sx), "s"(a.ldx),
+                   "s"(a.ldd), "s"(a.ldh), "s"(a.ldy), "s"(a.ldq), "s"(a.n), "s"(a.k), "s"(a.eps), "s"(warm.first));
   if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
     __shared__ uint32_t warm_sink[64];
     l2_warm_rows<kFuseThreads>(warm, warm_sink);
@@ -110,23 +124,16 @@ add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
   const int cpr = a.k >> 3;           // 8-element chunks per row
   const __amdgpu_buffer_rsrc_t xr = rows_rsrc(a.x, a.ldx, a.n, a.k, 2);
   const __amdgpu_buffer_rsrc_t dr = rows_rsrc(a.delta, a.ldd, a.n, a.k, 2);
-  const bool has_delta = a.delta != nullptr;   // without it h = x (not x + 0: -0 stays -0)
-  // This workgroup's tile (thread t -> rows wave + 4i, column c*64 + t%64),
-  // loaded first: it does not depend on the row norms, so its round trip
-  // overlaps the row loads below.
+  // This workgroup's tile, loaded first: it does not depend on the row norms,
+  // so its round trip overlaps the row loads below.  Without a delta h = x
+  // (not x + 0: -0 stays -0).
   const int col = c * 64 + lane;
-  const int nper = (a.n + 3) >> 2;    // tile rows per wave (wave-uniform)
-  uint32_t xt[16], dt[16];   // one register per value: no packing right after each load
+  uint32_t xt[TR], dt[TR];   // one register per value: no packing right after each load
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    xt[i] = 0;
-    dt[i] = 0;
-    if (i < nper) {
-      const int off = (int)(((int64_t)(wave + 4 * i) * a.ldx + col) * 2);
-      const int offd = (int)(((int64_t)(wave + 4 * i) * a.ldd + col) * 2);
-      xt[i] = __builtin_amdgcn_raw_buffer_load_b16(xr, off, 0, 0);
-      dt[i] = __builtin_amdgcn_raw_buffer_load_b16(dr, offd, 0, 0);
-    }
+  for (int i = 0; i < TR; ++i) {
+    const int row = wave + 4 * i;
+    xt[i] = __builtin_amdgcn_raw_buffer_load_b16(xr, row_off(row, a.n, a.ldx, col, 2), 0, 0);
+    dt[i] = HAS_DELTA ? __builtin_amdgcn_raw_buffer_load_b16(dr, row_off(row, a.n, a.ldd, col, 2), 0, 0) : 0u;
   }
   const uint16_t wraw = a.w[col];
   // Passes of kNormBatch chunks per lane: all loads of a pass are issued
@@ -145,9 +152,11 @@ add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
       for (int j = 0; j < kNormBatch; ++j) {
         const int ch = c0 + j * kWave + lane;
         const int ox = ch < cpr ? (int)(((int64_t)row * a.ldx + ch * 8) * 2) : 0x7fffffff;
-        const int od = ch < cpr ? (int)(((int64_t)row * a.ldd + ch * 8) * 2) : 0x7fffffff;
         xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ox, 0, 0));
-        dv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, od, 0, 0));
+        if constexpr (HAS_DELTA) {
+          const int od = ch < cpr ? (int)(((int64_t)row * a.ldd + ch * 8) * 2) : 0x7fffffff;
+          dv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, od, 0, 0));
+        }
       }
 #pragma unroll
       for (int j = 0; j < kNormBatch; ++j) {
@@ -155,10 +164,13 @@ add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
         for (int i = 0; i < 4; ++i) {
           // h of two elements, rounded as a pair (one v_cvt_pk_*), then both
           // squares in one v_dot2 (exact products, fp32 sums)
-          const uint32_t xw = xv[j][i], dw = dv[j][i];
-          const uint32_t hp = has_delta ? XT::pack2(XT::to_f32((uint16_t)xw) + XT::to_f32((uint16_t)dw),
-                                                    XT::to_f32((uint16_t)(xw >> 16)) + XT::to_f32((uint16_t)(dw >> 16)))
-                                        : xw;
+          const uint32_t xw = xv[j][i];
+          uint32_t hp = xw;
+          if constexpr (HAS_DELTA) {
+            const uint32_t dw = dv[j][i];
+            hp = XT::pack2(XT::to_f32((uint16_t)xw) + XT::to_f32((uint16_t)dw),
+                           XT::to_f32((uint16_t)(xw >> 16)) + XT::to_f32((uint16_t)(dw >> 16)));
+          }
           ssj[j] = dot2sq<XT>(hp, ssj[j]);
         }
       }
@@ -169,38 +181,31 @@ add_rmsnorm_quant_kernel(NormArgs a, L2Warm warm) {
   }
   lds_barrier();
   // tile c (rows >= n: zero values, stores dropped by the ranges)
-  const __amdgpu_buffer_rsrc_t hr = rows_rsrc(a.delta ? a.h : nullptr, a.ldh, a.n, a.k, 2);
+  const __amdgpu_buffer_rsrc_t hr = rows_rsrc(HAS_DELTA ? a.h : nullptr, a.ldh, a.n, a.k, 2);
   const __amdgpu_buffer_rsrc_t yr = rows_rsrc(a.y, a.ldy, a.n, a.k, 2);
   float am = 0.0f;
-  float yv[16];
+  float yv[TR];
   const float wv = XT::to_f32(wraw);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    yv[i] = 0.0f;
-    if (i < nper) {
-      const int row = wave + 4 * i;
-      const bool live = row < a.n;
-      const float xf = XT::to_f32((uint16_t)xt[i]);
-      const float hv = has_delta ? XT::round(xf + XT::to_f32((uint16_t)dt[i])) : xf;
-      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(hv), hr, (int)(((int64_t)row * a.ldh + col) * 2), 0, 0);
-      const float nrm = XT::round(hv * (live ? rinv[row] : 0.0f));   // hidden_states.to(input_dtype)
-      const float y = XT::round(wv * nrm);                          // weight * hidden_states
-      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, (int)(((int64_t)row * a.ldy + col) * 2), 0, 0);
-      yv[i] = live ? y : 0.0f;
-      am = fmaxf(am, fabsf(yv[i]));
-    }
+  for (int i = 0; i < TR; ++i) {
+    const int row = wave + 4 * i;
+    const bool live = row < a.n;
+    const float xf = XT::to_f32((uint16_t)xt[i]);
+    const float hv = HAS_DELTA ? XT::round(xf + XT::to_f32((uint16_t)dt[i])) : xf;
+    __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(hv), hr, row_off(row, a.n, a.ldh, col, 2), 0, 0);
+    const float nrm = XT::round(hv * (live ? rinv[row] : 0.0f));   // hidden_states.to(input_dtype)
+    const float y = XT::round(wv * nrm);                          // weight * hidden_states
+    __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, row_off(row, a.n, a.ldy, col, 2), 0, 0);
+    yv[i] = live ? y : 0.0f;
+    am = fmaxf(am, fabsf(yv[i]));
   }
   if (a.q == nullptr) return;
   const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
   const CodeScale cs(s);
   const __amdgpu_buffer_rsrc_t qr = rows_rsrc(a.q, a.ldq, a.n, a.k, 1);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (i < nper) {
-      const int row = wave + 4 * i;
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, (int)((int64_t)row * a.ldq + col), 0, 0);
-    }
-  }
+  for (int i = 0; i < TR; ++i)
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, row_off(wave + 4 * i, a.n, a.ldq, col, 1), 0, 0);
   if (t == 0) a.sx[c] = s;
 }
 
@@ -214,11 +219,14 @@ struct SiluArgs {
 };
 
 // y = silu(gate) * up with the module's roundings: silu in fp32 rounded to the
-// 16-bit type, the product rounded again.  Workgroup c = 64-column tile c.
-template <class XT>
+// 16-bit type, the product rounded again.  Workgroup c = 64-column tile c;
+// thread t takes rows wave + 4 i, i < TR (TR >= n / 4).
+template <class XT, int TR>
 __global__ void __launch_bounds__(kFuseThreads)
 silu_mul_quant_kernel(SiluArgs a, L2Warm warm) {
   __shared__ float red[kFuseThreads / kWave];
+  TQ_ARGS_IN_SGPRS("s"(a.gu), "s"(a.y), "s"(a.q), "s"(a.sx), "s"(a.ldg), "s"(a.ldy), "s"(a.ldq), "s"(a.n),
+                   "s"(a.inter), "s"(warm.first));
   if ((int)blockIdx.x >= warm.first) {   // the warm-up workgroups (none without a warm-up)
     __shared__ uint32_t warm_sink[64];
     l2_warm_rows<kFuseThreads>(warm, warm_sink);
@@ -226,49 +234,37 @@ silu_mul_quant_kernel(SiluArgs a, L2Warm warm) {
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int col = blockIdx.x * 64 + lane;
-  const int nper = (a.n + 3) >> 2;   // rows per wave (wave-uniform)
   // rows >= n read 0 and their stores are dropped (buffer ranges); every
   // load is issued before the first use
   const __amdgpu_buffer_rsrc_t gr = rows_rsrc(a.gu, a.ldg, a.n, 2 * a.inter, 2);
   const __amdgpu_buffer_rsrc_t yr = rows_rsrc(a.y, a.ldy, a.n, a.inter, 2);
-  uint32_t gw[16], uw[16];
+  uint32_t gw[TR], uw[TR];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    gw[i] = 0;
-    uw[i] = 0;
-    if (i < nper) {
-      const int off = (int)(((int64_t)(wave + 4 * i) * a.ldg + col) * 2);
-      gw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, off, 0, 0);
-      uw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, off + a.inter * 2, 0, 0);
-    }
+  for (int i = 0; i < TR; ++i) {
+    const int row = wave + 4 * i;
+    gw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, row_off(row, a.n, a.ldg, col, 2), 0, 0);
+    uw[i] = __builtin_amdgcn_raw_buffer_load_b16(gr, row_off(row, a.n, a.ldg, col + a.inter, 2), 0, 0);
   }
   float am = 0.0f;
-  float yv[16];
+  float yv[TR];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    yv[i] = 0.0f;
-    if (i < nper) {
-      const int row = wave + 4 * i;
-      const float g = XT::to_f32((uint16_t)gw[i]);
-      const float u = XT::to_f32((uint16_t)uw[i]);
-      const float sg = XT::round(g / (1.0f + expf(-g)));
-      const float y = XT::round(sg * u);
-      __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, (int)(((int64_t)row * a.ldy + col) * 2), 0, 0);
-      yv[i] = row < a.n ? y : 0.0f;
-      am = fmaxf(am, fabsf(yv[i]));
-    }
+  for (int i = 0; i < TR; ++i) {
+    const int row = wave + 4 * i;
+    const float g = XT::to_f32((uint16_t)gw[i]);
+    const float u = XT::to_f32((uint16_t)uw[i]);
+    const float sg = XT::round(g / (1.0f + expf(-g)));
+    const float y = XT::round(sg * u);
+    __builtin_amdgcn_raw_buffer_store_b16(XT::from_f32(y), yr, row_off(row, a.n, a.ldy, col, 2), 0, 0);
+    yv[i] = row < a.n ? y : 0.0f;
+    am = fmaxf(am, fabsf(yv[i]));
   }
   if (a.q == nullptr) return;
   const float s = act_scale_from_absmax<XT>(wg_max_nonneg(am, red));
   const CodeScale cs(s);
   const __amdgpu_buffer_rsrc_t qr = rows_rsrc(a.q, a.ldq, a.n, a.inter, 1);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (i < nper) {
-      const int row = wave + 4 * i;
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, (int)((int64_t)row * a.ldq + col), 0, 0);
-    }
-  }
+  for (int i = 0; i < TR; ++i)
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)cs.code(yv[i]), qr, row_off(wave + 4 * i, a.n, a.ldq, col, 1), 0, 0);
   if (t == 0) a.sx[blockIdx.x] = s;
 }
 
@@ -565,6 +561,30 @@ rope_prefill_kernel(RopePrefillArgs a) {
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Launches a glue kernel instantiated for TR = tile rows per wave, the
+// smallest of 1, 2, 4, 16 with 4 * TR >= n (n <= 64).
+template <class XT, bool HAS_DELTA>
+struct NormLaunch {
+  template <int TR>
+  static void go(dim3 grid, hipStream_t s, const NormArgs& a, const L2Warm& w) {
+    hipLaunchKernelGGL((add_rmsnorm_quant_kernel<XT, HAS_DELTA, TR>), grid, dim3(kFuseThreads), 0, s, a, w);
+  }
+};
+template <class XT>
+struct SiluLaunch {
+  template <int TR>
+  static void go(dim3 grid, hipStream_t s, const SiluArgs& a, const L2Warm& w) {
+    hipLaunchKernelGGL((silu_mul_quant_kernel<XT, TR>), grid, dim3(kFuseThreads), 0, s, a, w);
+  }
+};
+template <class L, class Args>
+static void launch_by_rows(int n, dim3 grid, hipStream_t s, const Args& a, const L2Warm& w) {
+  if (n <= 4) L::template go<1>(grid, s, a, w);
+  else if (n <= 8) L::template go<2>(grid, s, a, w);
+  else if (n <= 16) L::template go<4>(grid, s, a, w);
+  else L::template go<16>(grid, s, a, w);
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -593,10 +613,13 @@ extern "C" int tq_add_rmsnorm_quant(const void* x, int64_t x_stride, const void*
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(k / 64 + warm.blocks);
-  if (dtype == TQ_DTYPE_BF16)
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Bf16>, grid, dim3(kFuseThreads), 0, s, a, warm);
-  else
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<Fp16>, grid, dim3(kFuseThreads), 0, s, a, warm);
+  if (dtype == TQ_DTYPE_BF16) {
+    if (delta) launch_by_rows<NormLaunch<Bf16, true>>(n, grid, s, a, warm);
+    else launch_by_rows<NormLaunch<Bf16, false>>(n, grid, s, a, warm);
+  } else {
+    if (delta) launch_by_rows<NormLaunch<Fp16, true>>(n, grid, s, a, warm);
+    else launch_by_rows<NormLaunch<Fp16, false>>(n, grid, s, a, warm);
+  }
   return (int)hipGetLastError();
 }
 
@@ -619,10 +642,8 @@ extern "C" int tq_silu_mul_quant(const void* gate_up, int64_t gu_stride, void* y
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(inter / 64 + warm.blocks);
-  if (dtype == TQ_DTYPE_BF16)
-    hipLaunchKernelGGL(silu_mul_quant_kernel<Bf16>, grid, dim3(kFuseThreads), 0, s, a, warm);
-  else
-    hipLaunchKernelGGL(silu_mul_quant_kernel<Fp16>, grid, dim3(kFuseThreads), 0, s, a, warm);
+  if (dtype == TQ_DTYPE_BF16) launch_by_rows<SiluLaunch<Bf16>>(n, grid, s, a, warm);
+  else launch_by_rows<SiluLaunch<Fp16>>(n, grid, s, a, warm);
   return (int)hipGetLastError();
 }
 
