@@ -83,8 +83,10 @@ WARM_MAX_BLOCKS_PER_XCD = 128
 # 2304-token cache; TPOT, ms): none 1.905, QKV 1.888, QKV+O+Down 1.893-1.912,
 # Down 1.936, all four 2.12.  Only the QKV weights (16 MB) arrive within the
 # norm kernel that precedes them; O (inside the short attention merge), Gate/Up
-# (50 MB: more than the XCDs' L2) and Down (25 MB inside the 4.7 us SiLU
-# kernel) stretch their producer by more than their GEMM gains.
+# (50 MB: more than the XCDs' L2) and Down (25 MB inside the SiLU kernel)
+# stretch their producer by more than their GEMM gains.  Since the glue kernels
+# load their arguments in one round trip (3.4 us norm instead of 4.6) the
+# effect is within 0.2% either way: none 1.676, QKV 1.674, QKV+O+Down 1.673.
 WARM_GEMMS = ("qkv",)
 
 
