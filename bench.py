@@ -71,6 +71,10 @@ def parse():
                     help="run only three eager decode-attention calls (RoPE form with the INT8 merge; B=4, 24/8 "
                          "heads, 2304 keys) and a 256 MiB copy: the workload of the FETCH_SIZE pass behind "
                          "profiles/decode_attention_traffic.md")
+    ap.add_argument("--decode-glue-probe", action="store_true",
+                    help="run only graph timings of the fused decode step's glue kernels (configs[4] decode shape): "
+                         "residual add + RMSNorm + codes, SiLU * up + codes, and the RoPE attention split + INT8 "
+                         "merge over 28 distinct caches; microseconds per launch")
     ap.add_argument("--trace-split", metavar="KERNEL_TRACE_CSV",
                     help="per-layer split of the prompt forwards in a rocprofv3 kernel trace (no GPU needed)")
     ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -1097,6 +1101,99 @@ def released_maps_measure(args, device):
     return out
 
 
+def decode_glue_probe(device) -> dict:
+    """Per-launch graph timings of the fused decode step's glue kernels at the
+    configs[4] decode shape (B = 4, hidden 3072, MLP 8192, 24 / 8 heads, 2304-key
+    caches): each kernel launched 50 times (the attention once per distinct
+    cache of 28) inside one HIP graph, HIP events around 20 replays, best of 3."""
+    import torch
+    from tilequant_amd import _native as nat
+    from tilequant_amd.attention import decode_attention_workspace
+
+    B, H, I, hq, hkv, D, L = 4, 3072, 8192, 24, 8, 128, 2304
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(0)
+    s = torch.cuda.Stream()
+
+    def per_launch_us(fn, launches):
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            fn()
+        best = float("inf")
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                gr.replay()
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                for _ in range(20):
+                    gr.replay()
+                e1.record(s)
+                e1.synchronize()
+                best = min(best, e0.elapsed_time(e1) * 1e3 / 20 / launches)
+        torch.cuda.synchronize()
+        del gr
+        return round(best, 3)
+
+    x = (torch.randn((B, H), generator=g) * 3).to(bf).to(device)
+    d = (torch.randn((B, H), generator=g) * 2).to(bf).to(device)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(bf).to(device)
+    h, y = torch.empty_like(x), torch.empty_like(x)
+    q = torch.empty((B, H), dtype=torch.int8, device=device)
+    sx = torch.empty((H // 64,), dtype=torch.float32, device=device)
+    gu = (torch.randn((B, 2 * I), generator=g) * 2).to(bf).to(device)
+    m = torch.empty((B, I), dtype=bf, device=device)
+    mq = torch.empty((B, I), dtype=torch.int8, device=device)
+    msx = torch.empty((I // 64,), dtype=torch.float32, device=device)
+
+    def norm(delta):
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(50):
+            nat.check(nat.lib().tq_add_rmsnorm_quant(
+                x.data_ptr(), H, delta.data_ptr() if delta is not None else None, H, w.data_ptr(), 1e-5,
+                h.data_ptr() if delta is not None else None, H, y.data_ptr(), H, q.data_ptr(), H, sx.data_ptr(), 0,
+                B, H, None, st), "tq_add_rmsnorm_quant")
+
+    def silu():
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(50):
+            nat.check(nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * I, m.data_ptr(), I, mq.data_ptr(), I,
+                                                  msx.data_ptr(), 0, B, I, None, st), "tq_silu_mul_quant")
+
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g).to(bf).to(device)
+    cos = torch.randn((L, D), generator=g).to(bf).to(device)
+    sin = torch.randn((L, D), generator=g).to(bf).to(device)
+    caches = [(torch.randn((B, hkv, L, D), device=device).to(bf), torch.randn((B, hkv, L, D), device=device).to(bf))
+              for _ in range(28)]
+    out = torch.empty((B, hq * D), dtype=bf, device=device)
+    qo = torch.empty((B, hq * D), dtype=torch.int8, device=device)
+    osx = torch.empty((hq * D // 64,), dtype=torch.float32, device=device)
+    pos = torch.tensor([L - 2], dtype=torch.int64, device=device)
+    seq = torch.full((B,), L - 1, device=device, dtype=torch.int32)
+    with torch.cuda.stream(s):
+        ws = decode_attention_workspace(B, hq, L, device)
+
+    def attention():
+        st = torch.cuda.current_stream().cuda_stream
+        for kc, vc in caches:
+            nat.check(nat.lib().tq_decode_attention_rope(
+                qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), kc.data_ptr(),
+                vc.data_ptr(), kc.stride(0), kc.stride(2), kc.stride(1), seq.data_ptr(), out.data_ptr(), out.stride(0),
+                D, qo.data_ptr(), qo.stride(0), osx.data_ptr(), 0, B, hq, hkv, D, L, D ** -0.5, ws.data_ptr(),
+                ws.numel(), None, st), "tq_decode_attention_rope")
+
+    return {"shape": f"B={B}, hidden {H}, MLP {I}, {hq}/{hkv} heads, {L - 1}-key caches",
+            "add_rmsnorm_quant_us": per_launch_us(lambda: norm(d), 50),
+            "rmsnorm_quant_no_delta_us": per_launch_us(lambda: norm(None), 50),
+            "silu_mul_quant_us": per_launch_us(silu, 50),
+            "attention_split_merge_quant_us": per_launch_us(attention, 28),
+            "timing": "HIP events around 20 replays of one graph of the launches, best of 3; per launch"}
+
+
 def attention_traffic_probe(device) -> None:
     """Three eager calls of the fused decode step's attention (RoPE form, INT8 merge) at the configs[4]
     decode shape with every key valid, then a 256 MiB elementwise copy for the counter calibration."""
@@ -1168,6 +1265,9 @@ def main():
         return
     if args.attention_traffic_probe:
         attention_traffic_probe(device)
+        return
+    if args.decode_glue_probe:
+        print(json.dumps({"decode_glue": decode_glue_probe(device)}), flush=True)
         return
     layers, info = build_layers(args, device)
     xs = make_inputs(args, device)
