@@ -174,6 +174,22 @@ __device__ inline void dump_i32(const GemmArgs& a, int p, int row0, int col, con
   }
 }
 
+// The W wave partials of element e (red[w * E + e]) summed in wave order --
+// bitwise the loop sum = red[e]; sum += red[w * E + e] for w = 1 .. W - 1 --
+// with every LDS read issued before the first add (reads for w >= W re-read
+// wave W - 1 and are not added).  Used where a thread sums several elements:
+// the rolled loop waits one LDS round trip per wave and element.
+template <int WMAX>
+__device__ inline float wave_order_sum(const float* red, int E, int e, int W) {
+  float v[WMAX];
+#pragma unroll
+  for (int w = 0; w < WMAX; ++w) v[w] = red[min(w, W - 1) * E + e];
+  float sum = v[0];
+#pragma unroll
+  for (int w = 1; w < WMAX; ++w) sum = w < W ? sum + v[w] : sum;
+  return sum;
+}
+
 // ---- split-K decode kernel (N <= 64 tokens) ---------------------------------
 //
 // Workgroup (r, s), s < S, owns split s of row tile r: INT8 positions
@@ -503,6 +519,24 @@ gemm_splitk_kernel(GemmArgs a) {
   };
 
   if (S == 1) {
+    if (JBW == 4 && E >= 4 * (int)blockDim.x) {
+      // whole-tile workgroups at 33-64 rows: 8+ elements per thread, four at a
+      // time with all of their reads in flight together (the rolled loop below
+      // took ~3.7 us on the stacked Gate/Up at 64 rows)
+      for (int e0 = threadIdx.x; e0 < E; e0 += 4 * blockDim.x) {
+        float sums[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sums[i] = wave_order_sum<8>(red, E, min(e0 + i * (int)blockDim.x, E - 1), W);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = e0 + i * (int)blockDim.x;
+          int row, jcol;
+          coords(min(e, E - 1), row, jcol);
+          if (e < E && row < a.n) store(row, jcol, sums[i]);
+        }
+      }
+      return;
+    }
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
       int row, jcol;
       coords(e, row, jcol);
