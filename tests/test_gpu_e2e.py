@@ -242,7 +242,8 @@ def _ulp_close(a: torch.Tensor, b: torch.Tensor, ulps: float = 1.0) -> bool:
     return bool(((a - b).abs() <= ulps * ulp).all())
 
 
-@pytest.mark.parametrize("n,k,with_delta", [(4, 3072, True), (1, 3072, False), (16, 512, True), (3, 8192, True)])
+@pytest.mark.parametrize("n,k,with_delta", [(4, 3072, True), (1, 3072, False), (16, 512, True), (3, 8192, True),
+                                          (7, 3072, True), (40, 1024, True), (64, 512, False), (13, 3072, False)])
 def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
     from transformers.models.llama.modeling_llama import LlamaRMSNorm
 
@@ -271,7 +272,7 @@ def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
     assert torch.equal(q, q_ref) and torch.equal(sx, sx_ref)   # same closed form as the quantizer, bitwise
 
 
-@pytest.mark.parametrize("n,inter", [(4, 8192), (1, 1024), (16, 512)])
+@pytest.mark.parametrize("n,inter", [(4, 8192), (1, 1024), (16, 512), (7, 8192), (33, 1024), (64, 512)])
 def test_silu_mul_quant_matches_module_and_quantizer(n, inter):
     g = torch.Generator().manual_seed(n + inter)
     gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(torch.bfloat16).to(DEV)
