@@ -875,9 +875,11 @@ gemm_decode_kernel(GemmArgs a) {
   // weights, codes given, 4 tokens, per launch): Llama-3.2-3B Q/K/V 7.36 ->
   // 6.59 us, O 5.61 -> 5.10, Down 8.81 -> 8.16, Gate/Up (12-tile batches,
   // IA 6) 12.07 -> 11.43; Qwen2.5-7B keep10 Q/K/V 8.68 -> 8.37, O 7.98 ->
-  // 7.84, Down 25.77 -> 25.45.  16-tile batches keep issuing at once (their
+  // 7.84, Down 25.77 -> 25.45.  Whole-tile waves (6-tile batches of 4 KiB
+  // tiles, 9-16 rows) lead by 2: stacked Gate/Up at 16 rows 13.90 -> 12.65 us,
+  // at 9 rows 13.56 -> 12.44.  16-tile batches keep issuing at once (their
   // Gate/Up is slower with any shorter lead).
-  constexpr int IA = UMAX == 8 ? 4 : (UMAX == 12 ? 6 : UMAX);
+  constexpr int IA = UMAX == 8 ? 4 : (UMAX == 12 ? 6 : (UMAX == 6 ? 2 : UMAX));
   const int first_q = wave;
   if (!idle) {   // the COOP loader and HELP helper waves take no tiles
     load_meta(first_q);
