@@ -1426,11 +1426,51 @@ def main():
         dense_bytes = sum(sum(w) * k * 2 for _, w, k in GROUPS) * args.layers
         dense = {"ms_per_step": d_s * 1e3, "tops": info["ops"] / d_s / 1e12, "gbps": dense_bytes / d_s / 1e9,
                  "speedup_of_tilequant": d_s / step_s}
+        del dg
+        if args.m_sweep:
+            # the same dense step at the M-sweep's token counts (one graph each, best of 3 x 10 replays)
+            dense["ms_per_step_at"] = {}
+            for m in (1, 16, 64):
+                a2 = argparse.Namespace(**vars(args))
+                a2.tokens = m
+                xm = make_inputs(a2, device)
+
+                def dstep_m():
+                    return [torch.nn.functional.linear(xm[name], lw[name]) for lw in ws for name, _, _ in GROUPS]
+
+                dstep_m()
+                torch.cuda.synchronize()
+                with torch.cuda.stream(s):
+                    dstep_m()
+                torch.cuda.synchronize()
+                gm = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gm, stream=s):
+                    dstep_m()
+                best = float("inf")
+                with torch.cuda.stream(s):
+                    for _ in range(2):
+                        gm.replay()
+                    for _ in range(3):
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record(s)
+                        for _ in range(10):
+                            gm.replay()
+                        e1.record(s)
+                        e1.synchronize()
+                        best = min(best, e0.elapsed_time(e1) / 10)
+                torch.cuda.synchronize()
+                dense["ms_per_step_at"][str(m)] = best
+                del gm, xm
         del ws
 
     cpu = cpu_baseline(args, layers, xs) if args.cpu_layers > 0 else None
     config0 = config0_measure(args, device) if args.config0 else None
     m_sweep = decode_m_sweep(args, device, layers, info) if args.m_sweep else None
+    if m_sweep and dense and "ms_per_step_at" in dense:
+        for m, r in m_sweep.items():
+            if m in dense["ms_per_step_at"]:
+                r["dense_bf16_ms_per_step"] = dense["ms_per_step_at"][m]
+                r["speedup_vs_dense_bf16"] = dense["ms_per_step_at"][m] / r["ms_per_step"]
     del layers
     prefill = prefill_measure(args, device) if args.prefill_tokens > 0 else None
     torch.cuda.empty_cache()
