@@ -237,21 +237,27 @@ from tilequant_amd.quant_utils import quantize_activation_tile_absmax   # noqa: 
 
 
 def _ulp_close(a: torch.Tensor, b: torch.Tensor, ulps: float = 1.0) -> bool:
+    """|a - b| within `ulps` units in the last place of b in b's 16-bit type
+    (7 fraction bits for bf16, 10 for fp16; fp16's subnormal spacing below 2^-14)."""
+    frac, low = (10, -14) if b.dtype == torch.float16 else (7, -126)
     a, b = a.float(), b.float()
-    ulp = torch.exp2(torch.floor(torch.log2(b.abs().clamp_min(2.0 ** -126))) - 7)
+    ulp = torch.exp2(torch.floor(torch.log2(b.abs().clamp_min(2.0 ** low))) - frac)
     return bool(((a - b).abs() <= ulps * ulp).all())
 
 
-@pytest.mark.parametrize("n,k,with_delta", [(4, 3072, True), (1, 3072, False), (16, 512, True), (3, 8192, True),
-                                          (7, 3072, True), (40, 1024, True), (64, 512, False), (13, 3072, False)])
-def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
+@pytest.mark.parametrize("n,k,with_delta,dtype", [(4, 3072, True, torch.bfloat16), (1, 3072, False, torch.bfloat16),
+                                                  (16, 512, True, torch.bfloat16), (3, 8192, True, torch.bfloat16),
+                                                  (7, 3072, True, torch.bfloat16), (40, 1024, True, torch.bfloat16),
+                                                  (64, 512, False, torch.bfloat16), (13, 3072, False, torch.bfloat16),
+                                                  (4, 3584, True, torch.float16), (20, 1024, False, torch.float16)])
+def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta, dtype):
     from transformers.models.llama.modeling_llama import LlamaRMSNorm
 
     g = torch.Generator().manual_seed(n * 7 + k)
-    x = (torch.randn((n, k), generator=g) * 3).to(torch.bfloat16).to(DEV)
-    d = (torch.randn((n, k), generator=g) * 2).to(torch.bfloat16).to(DEV)
-    norm = LlamaRMSNorm(k, eps=1e-5).to(DEV).to(torch.bfloat16)
-    norm.weight.data = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16).to(DEV)
+    x = (torch.randn((n, k), generator=g) * 3).to(dtype).to(DEV)
+    d = (torch.randn((n, k), generator=g) * 2).to(dtype).to(DEV)
+    norm = LlamaRMSNorm(k, eps=1e-5).to(DEV).to(dtype)
+    norm.weight.data = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype).to(DEV)
     h_ref = (x + d) if with_delta else x
     with torch.inference_mode():
         y_ref = norm(h_ref)
@@ -261,7 +267,7 @@ def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
     sx = torch.empty((k // 64,), dtype=torch.float32, device=DEV)
     rc = nat.lib().tq_add_rmsnorm_quant(x.data_ptr(), k, d.data_ptr() if with_delta else None, k,
                                         norm.weight.data_ptr(), 1e-5, h.data_ptr(), k, y.data_ptr(), k,
-                                        q.data_ptr(), k, sx.data_ptr(), 0, n, k, None,
+                                        q.data_ptr(), k, sx.data_ptr(), nat.dtype_code(dtype), n, k, None,
                                         torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
@@ -272,17 +278,21 @@ def test_add_rmsnorm_quant_matches_module_and_quantizer(n, k, with_delta):
     assert torch.equal(q, q_ref) and torch.equal(sx, sx_ref)   # same closed form as the quantizer, bitwise
 
 
-@pytest.mark.parametrize("n,inter", [(4, 8192), (1, 1024), (16, 512), (7, 8192), (33, 1024), (64, 512)])
-def test_silu_mul_quant_matches_module_and_quantizer(n, inter):
+@pytest.mark.parametrize("n,inter,dtype", [(4, 8192, torch.bfloat16), (1, 1024, torch.bfloat16),
+                                           (16, 512, torch.bfloat16), (7, 8192, torch.bfloat16),
+                                           (33, 1024, torch.bfloat16), (64, 512, torch.bfloat16),
+                                           (4, 18944, torch.float16), (9, 1024, torch.float16)])
+def test_silu_mul_quant_matches_module_and_quantizer(n, inter, dtype):
     g = torch.Generator().manual_seed(n + inter)
-    gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(torch.bfloat16).to(DEV)
+    gu = (torch.randn((n, 2 * inter), generator=g) * 2).to(dtype).to(DEV)
     with torch.inference_mode():
         y_ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
-    y = torch.empty((n, inter), dtype=torch.bfloat16, device=DEV)
+    y = torch.empty((n, inter), dtype=dtype, device=DEV)
     q = torch.empty((n, inter), dtype=torch.int8, device=DEV)
     sx = torch.empty((inter // 64,), dtype=torch.float32, device=DEV)
     rc = nat.lib().tq_silu_mul_quant(gu.data_ptr(), 2 * inter, y.data_ptr(), inter, q.data_ptr(), inter,
-                                     sx.data_ptr(), 0, n, inter, None, torch.cuda.current_stream().cuda_stream)
+                                     sx.data_ptr(), nat.dtype_code(dtype), n, inter, None,
+                                     torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
     assert _ulp_close(y, y_ref, 1.0)
