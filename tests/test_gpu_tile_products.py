@@ -171,14 +171,15 @@ def test_config0_products_every_decode_kernel():
 
 @pytest.mark.parametrize("proj", sorted(LLAMA))
 def test_llama_decode_products_all_token_counts(proj):
-    """Each Llama-3.2-3B projection group at 1 / 4 / 16 / 64 tokens, keep01:
-    the kernel the schedule picks on row-major codes, on token-blocked codes,
-    and the one-launch kernel where the row count allows it."""
+    """Each Llama-3.2-3B projection group at 1 / 4 / 16 / 24 / 64 tokens,
+    keep01: the kernel the schedule picks on row-major codes, on token-blocked
+    codes, and the one-launch kernel where the row count allows it (24 rows:
+    the stacked Gate/Up runs half-tile split-K workgroups)."""
     members = LLAMA[proj]
     k = members[0][1]
     pack, op = _stacked(members, 0.01, seed=sum(m for m, _ in members) + k)
     seen = set()
-    for n in (1, 4, 16, 64):
+    for n in (1, 4, 16, 24, 64):
         x = make_x(n, k, seed=k + n)
         xd = x.to(DEV)
         xq_ref, _ = nm.act_quant(values(x))

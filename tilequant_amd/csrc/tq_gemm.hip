@@ -303,13 +303,14 @@ __device__ inline float quant_col_tile(const GemmArgs& a, const XSlice<NPOW, XVE
 }
 
 // JBW = j-blocks (16 output features each) per workgroup: 4 = whole 4 KiB
-// tiles per wave; 1 = one 1 KiB j-block of each tile (four workgroups share
-// a row tile, so narrow outputs still fill the GPU without any
-// cross-workgroup reduction).  Launch bound: 16 waves at JBW 1, 8 at JBW 4.
+// tiles per wave; 2 = half tiles (two workgroups per row tile); 1 = one 1 KiB
+// j-block of each tile (four workgroups share a row tile, so narrow outputs
+// still fill the GPU without any cross-workgroup reduction).  Launch bound:
+// 16 waves at JBW 1, 8 at JBW 2 and 4.
 // XBLK: the codes are token-blocked (a.xblk blocks of 16 rows per column
 // tile): each activation operand is one contiguous 1 KiB load.
 template <class XT, int TB, int U, bool FUSED, int NPOW, bool XVEC, int JBW, bool XBLK = false, bool DUMP = false>
-__global__ void __launch_bounds__(JBW == 4 ? 512 : 1024)
+__global__ void __launch_bounds__(JBW == 1 ? 1024 : 512)
 gemm_splitk_kernel(GemmArgs a) {
   static_assert(!(XBLK && FUSED), "the fused prologue stages its own codes");
   // a batch of U tiles must never straddle two 64-tile metadata windows
@@ -2225,7 +2226,7 @@ static int plan_max_waves(int jbw, int tb) {
   // token blocks, whose waves otherwise take a dozen tiles each one batch at a
   // time); launch bound 16 / 8 waves
   int w = (tb == 4 ? 128 : 64) / (jbw * tb);
-  const int bound = jbw == 4 ? 8 : 16;
+  const int bound = jbw == 1 ? 16 : 8;
   return w < bound ? w : bound;
 }
 
@@ -2264,6 +2265,12 @@ static SplitPlan plan_split(int n, int n_tr, int n_tc, int split_k) {
   SplitPlan p;
   p.tb = pick_tb(n);
   p.jbw = pick_jbw(n, n_tr);
+  // 17-32 rows: wide projections take half tiles per workgroup (twice the
+  // workgroups); measured on MI355X, stacked Gate/Up at 17 / 24 / 32 rows
+  // 15.49 / 15.59 / 15.82 -> 14.46 / 14.57 / 14.69 us, bitwise unchanged (the
+  // same tiles per wave in the same order).  At 33-64 rows whole tiles stay
+  // (half tiles 18.7 -> 21.6 us at 64 rows).
+  if (p.jbw == 4 && p.tb == 2) p.jbw = 2;
   p.S = split_k > 1 ? split_k : 1;
   const int units = n_tr * (4 / p.jbw);
   if (p.S > 1 && units > kCounterCap) p.S = 1;
@@ -2357,6 +2364,9 @@ static hipError_t launch_split(GemmArgs a, const SplitPlan& p, float* ws, hipStr
   if (p.jbw == 4)
     return a.xvec ? launch_split_v<XT, FUSED, true, 4, DUMP>(a, p, grid, block, lds, s)
                   : launch_split_v<XT, FUSED, false, 4, DUMP>(a, p, grid, block, lds, s);
+  if (p.jbw == 2)
+    return a.xvec ? launch_split_v<XT, FUSED, true, 2, DUMP>(a, p, grid, block, lds, s)
+                  : launch_split_v<XT, FUSED, false, 2, DUMP>(a, p, grid, block, lds, s);
   return a.xvec ? launch_split_v<XT, FUSED, true, 1, DUMP>(a, p, grid, block, lds, s)
                 : launch_split_v<XT, FUSED, false, 1, DUMP>(a, p, grid, block, lds, s);
 }
