@@ -70,6 +70,33 @@ def test_decode_attention_matches_reference(B, Hq, Hkv, L, token_major):
                                         scale=scale), out)
 
 
+@pytest.mark.parametrize("q_scale", [1.0, 4.0])
+def test_decode_attention_fp32_accuracy_near_uniform(q_scale):
+    """Near-uniform attention over long sequences (random q, k, v; 2304 keys)
+    gives outputs that cancel to a small fraction of sum_t p_t |v_t|, where an
+    error of the probabilities' precision shows in ulps: with fp32-accurate
+    products and sums at most 0.1% of the bf16 outputs may differ from the
+    correctly rounded float64 result (fp32 probabilities: 0.02-0.07%;
+    probabilities carried to 16 significant bits: 0.12-0.26%), and each output
+    stays within 2 ulp plus 2^-18 of sum_t p_t |v_t|."""
+    B, Hq, Hkv, L, D = 4, 24, 8, 2304, 128
+    lens = [2304, 2049, 1000, 77]
+    for seed in range(3):
+        g = torch.Generator().manual_seed(100 + seed)
+        q = (torch.randn((B, Hq, D), generator=g) * q_scale).to(torch.bfloat16)
+        k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16)
+        v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16)
+        out = decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                               scale=D ** -0.5)
+        ref = _attention_reference(q, k, v, lens, D ** -0.5)
+        mag = _attention_reference(q, k, v.abs(), lens, D ** -0.5)   # sum_t p_t |v_t|
+        got = out.double().cpu()
+        mismatch = float((got != ref.to(torch.bfloat16).double()).double().mean())
+        assert mismatch <= 1e-3, (seed, mismatch)
+        ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -126))) - 7)
+        assert bool(((got - ref).abs() <= 2 * ulp + mag * 2.0 ** -18).all()), seed
+
+
 def test_decode_attention_graph_replays_follow_device_length():
     B, Hq, Hkv, L, D = 2, 24, 8, 600, 128
     g = torch.Generator().manual_seed(5)
