@@ -355,6 +355,7 @@ def qwen_measure(args, device):
     from tilequant_amd.mixed_linear import MixedLinear
     from tilequant_amd.pack import concat_packs_along_rows
     from tilequant_amd.quant_utils import quantize_activation_tile_absmax
+    from tilequant_amd.quantize_activation import quantize_activation_token_blocked
 
     cfg = SimpleNamespace(quant_style="gi", dtype_out="bf16")
     out = {}
@@ -407,7 +408,10 @@ def qwen_measure(args, device):
             xs = {name: (torch.randn((4, k), generator=gx) * 1.0).to(torch.bfloat16).to(device) for name, _, k in groups}
             ops = sum(2 * 4 * mods[name].M_orig * mods[name].K_orig for mods in layers for name, _, _ in groups)
             step_ms = graph_time(lambda: [mods[name](xs[name]) for mods in layers for name, _, _ in groups], 10)
-            quant = {name: quantize_activation_tile_absmax(xs[name]) for name, _, _ in groups}
+            # the codes in the layout MixedLinear gives each projection's GEMM at 4 rows
+            blocked = {name: layers[0][name].token_blocked_codes(4) for name, _, _ in groups}
+            quant = {name: (quantize_activation_token_blocked if blocked[name] else quantize_activation_tile_absmax)(
+                xs[name]) for name, _, _ in groups}
             outs = {(i, name): torch.empty((4, mods[name].M_orig), device=device, dtype=torch.bfloat16)
                     for i, mods in enumerate(layers) for name, _, _ in groups}
 
@@ -422,7 +426,8 @@ def qwen_measure(args, device):
                                                fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
                                                M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
                                                out_dtype=torch.bfloat16, out=outs[(i, name)],
-                                               tile_layout=lin.tile_layout)
+                                               tile_layout=lin.tile_layout,
+                                               x_int8_layout="token_blocked" if blocked[name] else "row_major")
             gemm_ms = graph_time(gemms, 10)
             n_launch = len(layers) * len(groups)
             achieved = packed / n_launch / (gemm_ms / n_launch / 1e3) / 1e9
@@ -441,7 +446,8 @@ def qwen_measure(args, device):
                                                fp16_tile_ids=lin.fp16_tile_ids, fp16_row_ptr=lin.fp16_row_ptr,
                                                M=lin.M_orig, K=lin.K_orig, n_tr=lin.n_tr, n_tc=lin.n_tc,
                                                out_dtype=torch.bfloat16, out=outs[(i, gname)],
-                                               tile_layout=lin.tile_layout)
+                                               tile_layout=lin.tile_layout,
+                                               x_int8_layout="token_blocked" if blocked[gname] else "row_major")
                 us = graph_time(group_gemms, 10) * 1e3 / len(layers)
                 lin0 = layers[0][gname]
                 gbytes = 4096 * int(lin0.int8_tiles.shape[0]) + 8192 * int(lin0.fp16_tiles.shape[0]) \

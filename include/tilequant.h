@@ -281,7 +281,8 @@ int tq_linear_forward(const tq_linear_desc* d);
 /* Host function: 1 when the automatic GEMM schedule for n rows of a weight
  * with n_tr x n_tc tiles (k = 64 * n_tc) runs faster on token-blocked codes
  * (TQ_XQ_TOKEN_BLOCKED) -- 17..64 rows, and up to 16 rows where the codes do
- * not fit the LDS-staged kernel -- else 0.  No reference counterpart (the
+ * not fit the LDS-staged kernel (more than 144 KiB of them) or a row holds
+ * 256+ column tiles (k >= 16384) -- else 0.  No reference counterpart (the
  * reference keeps codes row-major); MixedLinear asks it per row count. */
 int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc);
 

@@ -142,12 +142,14 @@ def test_token_blocked_gemm_rejects_wrong_buffers():
 @pytest.mark.parametrize("m,k,n,blocked", [
     (5120, 3072, 16, False), (5120, 3072, 17, True), (5120, 3072, 24, True), (5120, 3072, 32, True),
     (5120, 3072, 33, True), (5120, 3072, 48, True), (5120, 3072, 64, True),
-    (3072, 8192, 8, False), (3072, 8192, 16, True), (3072, 8192, 24, True)])
+    (3072, 8192, 8, False), (3072, 8192, 16, False), (3072, 8192, 17, True), (3072, 8192, 24, True),
+    (3584, 18944, 4, True), (3584, 18944, 16, True)])
 def test_mixed_linear_token_blocked_rows_are_bitwise_row_major(m, k, n, blocked):
     """MixedLinear quantizes token-blocked where the GEMM prefers it (17..64
-    rows; fewer for wide inputs whose codes do not fit LDS) -- through the
-    cached eager launch below 32 rows, the shared-quantization path from 32 --
-    and its output is the row-major computation's bit for bit."""
+    rows; fewer for rows of 256+ column tiles and for inputs whose codes do not
+    fit LDS) -- through the cached eager launch below 32 rows, the
+    shared-quantization path from 32 -- and its output is the row-major
+    computation's bit for bit."""
     _, pack, _ = _pack(m, k, 0.01, seed=77)
     lin = MixedLinear(pack, None, CFG)
     assert lin.token_blocked_codes(n) == blocked

@@ -71,13 +71,17 @@ def test_argument_errors_return_before_any_launch(lib):
 
 
 def test_token_blocked_preference(lib):
-    """Token-blocked codes for 17..64 rows, and below that only where the codes
-    do not fit the LDS-staged decode kernel (k = 8192 from 12 rows on)."""
+    """Token-blocked codes for 17..64 rows; below that only where the codes do
+    not fit the LDS-staged decode kernel (144 KiB: k = 8192 fits up to 16
+    rows, k = 13824 up to 9) or rows hold 256+ column tiles (k >= 16384)."""
     pref = lib.tq_gemm_prefers_token_blocked
     assert pref(64, 3072, 80, 48) == 1 and pref(33, 3072, 48, 48) == 1 and pref(17, 3072, 256, 48) == 1
     assert pref(32, 8192, 48, 128) == 1
     assert pref(16, 3072, 80, 48) == 0 and pref(4, 3072, 256, 48) == 0 and pref(4, 8192, 48, 128) == 0
-    assert pref(16, 8192, 48, 128) == 1
+    assert pref(16, 8192, 48, 128) == 0 and pref(12, 8192, 48, 128) == 0
+    assert pref(9, 13824, 80, 216) == 0 and pref(10, 13824, 80, 216) == 1
+    assert pref(1, 18944, 56, 296) == 1 and pref(4, 18944, 56, 296) == 1 and pref(4, 16384, 48, 256) == 1
+    assert pref(4, 16320, 48, 255) == 0
     assert pref(65, 3072, 48, 48) == 0 and pref(0, 3072, 48, 48) == 0 and pref(16, 3000, 48, 47) == 0
 
 

@@ -609,7 +609,11 @@ gemm_splitk_kernel(GemmArgs a) {
 // A-operand read over different banks); the reduction buffer reuses the area
 // afterwards.  Needs k == 64 * n_tc, 16-byte aligned activation rows, S == 1.
 
-constexpr int kDecCodesMax = 96 * 1024;   // LDS bytes for staged codes
+// LDS bytes for staged codes.  144 KiB takes k = 8192 up to 16 rows (Down of
+// Llama-3.2-3B: a 16-wave workgroup is alone on its CU anyway); measured on
+// MI355X, Down at 9 / 12 / 16 rows 10.14 / 10.17 / 10.20 us on the split-K
+// kernel (token-blocked codes) -> 8.98 / 9.03 / 9.15 us staged, bitwise equal.
+constexpr int kDecCodesMax = 144 * 1024;
 
 // ---- cooperative activation quantization (COOP decode launches) -------------
 // The decode GEMM's input codes are a function of all n rows of each 64-column
@@ -2841,14 +2845,23 @@ extern "C" int tq_gemm_l2_warm_ok(int n, int k, int n_tr, int n_tc) {
   return d.ok && (d.jbw == 4 || (n_tr & 7) == 0) ? 1 : 0;
 }
 
+constexpr int kDecLongRowTiles = 256;
+
 extern "C" int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc) {
   if (n < 1 || n > kDecodeMaxTokens || n_tr < 1 || k != n_tc * 64) return 0;
   // 17..64 rows: the split-K kernel on token-blocked codes beats the
   // LDS-staged kernel wherever that one fits (Llama-3.2-3B projections at 32
   // tokens on MI355X: QKV 13.2 -> 9.7 us, O 8.9 -> 7.7, Gate/Up 17.1 -> 16.7);
-  // up to 16 rows only where the codes do not fit LDS (Down at 16 tokens:
-  // 12.1 -> 10.3 us; the others stay faster staged).
+  // up to 16 rows only where the codes do not fit the staged kernel's LDS
+  // (kDecCodesMax), and for the long rows below.
   if (n > 16) return 1;
+  // Rows of 256+ column tiles (k >= 16384): the split-K kernel at every row
+  // count.  Measured on MI355X, Qwen2.5-7B Down (3584 x 18944, clustered keep10,
+  // cold weights), staged -> split-K: 1 row 23.69 -> 21.85 us, 4 rows 25.68 ->
+  // 22.30, 6 rows 26.21 -> 22.61, 12-16 rows within 0.1 us; k = 13824 (216
+  // tiles) and below stay faster staged (Qwen2.5-14B Down at 4 rows 22.81 vs
+  // 24.95).  Bitwise the same outputs either way.
+  if (n_tc >= kDecLongRowTiles) return 1;
   return plan_decode(n, k, n_tr, n_tc, false).ok ? 0 : 1;
 }
 

@@ -329,7 +329,8 @@ class MixedLinear(nn.Module):
         """Whether this module quantizes ``n_rows``-row inputs into
         token-blocked codes: where the GEMM's schedule runs faster on them
         (``tq_gemm_prefers_token_blocked``: 17..64 rows, and fewer where the
-        codes do not fit the LDS-staged kernel).  Outputs are bitwise those of
+        codes do not fit the LDS-staged kernel or rows hold 256+ column
+        tiles).  Outputs are bitwise those of
         row-major codes; only the operand loads change (each 16-row x 64-column
         slice one contiguous 1 KiB instead of 16 row pieces of 64 bytes)."""
         hit = self._blocked_rows.get(n_rows)
