@@ -275,7 +275,13 @@ def test_qwen_clustered_products(proj, frac):
     xq_ref, _ = nm.act_quant(values(x))
     P, kern = _run_codes(pack, xd, xq, sx)
     _assert_products(P, _oracle_products(op, xq_ref), f"{proj} n=4 {kern}")
-    del x, xd, xq
+    # the split-K kernel on token-blocked codes too: MixedLinear's choice for
+    # rows of 256+ column tiles (Qwen2.5-7B Down) at every decode row count
+    xqb, sxb = quantize_activation_token_blocked(xd)
+    P, kern = _run_codes(pack, xd, xqb, sxb, layout="token_blocked")
+    assert kern == "splitk_token_blocked"
+    _assert_products(P, _oracle_products(op, xq_ref), f"{proj} n=4 {kern}")
+    del x, xd, xq, xqb
     assert _prefill_products(pack, op, make_x(8192, k, seed=k + 8192)) == {"prefill_v5"}
 
 
