@@ -101,6 +101,12 @@ def _gemm(pack, xd, xq, sx, layout, bias=None, split_k=None):
     (3072, 3072, 0.01, 64, 4, torch.bfloat16, "mfma", False),       # explicit split-K
     (704, 1280, 0.30, 5, 2, torch.float16, "mfma", True),           # one block, ragged rows and outputs
     (3584, 18944, 0.10, 64, None, torch.bfloat16, "mfma", False),   # Qwen2.5-7B Down width
+    # at 1-16 rows row-major codes run the LDS-staged kernel and token-blocked ones the split-K
+    # kernel: the planner's choice between them must not change a bit
+    (3584, 18944, 0.10, 4, None, torch.bfloat16, "mfma", False),    # Qwen2.5-7B Down, its schedule now
+    (3072, 8192, 0.01, 16, None, torch.bfloat16, "mfma", False),    # Down staged up to 16 rows
+    (5120, 3072, 0.01, 1, None, torch.bfloat16, "mfma", True),
+    (16384, 3072, 0.01, 9, None, torch.float16, "mfma", False),     # whole-tile workgroups in both
 ])
 def test_token_blocked_gemm_is_bitwise_the_row_major_gemm(m, k, frac, n, split_k, dtype, tiles, bias):
     W, pack, ids16 = _pack(m, k, frac, seed=m + k + n, dtype=dtype, layout=tiles)
