@@ -512,6 +512,44 @@ def steady_ms(fn):
     return statistics.median(times)
 
 
+def plain_read_launch_us(device, stream, n_launch, nbytes, reps):
+    """Per-launch time of a plain HBM read (tq_read_probe) of nbytes, n_launch
+    launches over distinct buffers back to back in one HIP graph on stream,
+    HIP events around the replays: the GEMM roofline's context (a kernel that
+    only reads its bytes, at the same size and in the same protocol)."""
+    import torch
+    from tilequant_amd import _native as nat
+
+    nbytes = nbytes // 16 * 16
+    bufs = torch.empty((n_launch, nbytes), device=device, dtype=torch.uint8)
+    sink = torch.zeros((256,), device=device, dtype=torch.int32)
+
+    def reads():
+        h = nat.stream_handle(device)
+        for i in range(n_launch):
+            nat.check(nat.lib().tq_read_probe(nat.ptr(bufs[i]), nbytes, nat.ptr(sink), h), "tq_read_probe")
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        reads()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        reads()
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * n_launch)
+    del g, bufs, sink
+    return us
+
+
 def decode_m_sweep(args, device, layers, info, token_counts=(1, 16, 64)):
     """BASELINE configs[1] at the other token counts it names (M in {1, 4, 16,
     64}; 4 is the headline): the same 28-layer linear set, quantize + GEMM per
@@ -1402,6 +1440,7 @@ def main():
     gemm_avg_s = total_ms / n_launch / 1e3
     bytes_per_launch = info["packed_bytes"] / len(launches)
     achieved = bytes_per_launch / gemm_avg_s / 1e9
+    plain_read_us = plain_read_launch_us(device, s, len(launches), int(bytes_per_launch), reps)
 
     # dense bf16 context: the same linear set through torch.nn.functional.linear (hipBLASLt)
     dense = None
@@ -1513,9 +1552,14 @@ def main():
                      "kernel": "tq::gemm_decode_kernel", "avg_launch_us": gemm_avg_s * 1e6,
                      "bytes_per_launch": bytes_per_launch, "launches_per_step": len(launches),
                      "group_avg_us": group_us,
+                     "plain_read_us": plain_read_us,
+                     "frac_of_plain_read": plain_read_us / (gemm_avg_s * 1e6),
                      "timing": "HIP events on the launch stream around replays of one HIP graph holding the "
                                "step's 112 GEMM launches back to back (activations quantized beforehand); "
-                               "per-launch average includes the inter-kernel gaps"},
+                               "per-launch average includes the inter-kernel gaps. plain_read_us: the same "
+                               "protocol for 112 launches of a read-only kernel (tq_read_probe) over as many "
+                               "distinct bytes each as a GEMM launch reads; frac_of_plain_read = plain / GEMM "
+                               "time per launch"},
         "dense_bf16": dense,
         "config0": config0,
         "decode_m_sweep": m_sweep,

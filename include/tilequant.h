@@ -286,6 +286,14 @@ int tq_linear_forward(const tq_linear_desc* d);
  * reference keeps codes row-major); MixedLinear asks it per row count. */
 int tq_gemm_prefers_token_blocked(int n, int k, int n_tr, int n_tc);
 
+/* MEASUREMENT HELPER.  One kernel that reads bytes (a multiple of 16) from a
+ * 16-byte aligned device buffer once and writes nothing in practice (sink: 256
+ * device words, stored to only if the folded data equals a fixed constant).
+ * bench.py times it per launch beside the decode GEMM, over as many bytes as
+ * a GEMM launch reads, as the context of the GEMM's HBM roofline fraction.
+ * No reference counterpart. */
+int tq_read_probe(const void* data, int64_t bytes, uint32_t* sink, void* stream);
+
 /* TEST-ONLY.  Kernel families of the automatic GEMM schedule, as reported by
  * the *_products_i32 entries below. */
 enum {

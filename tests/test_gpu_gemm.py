@@ -718,3 +718,18 @@ def test_prefill_plan_fp16_bias_and_ragged_rows():
     rows = np.unique(np.r_[0:3, n - 3:n])
     acc, sab = _oracle_f64(pack, op, x[rows], xq_ref[rows], sx_ref)
     assert_gemm_close(y[rows], acc, sab, pack.n_tc, bias=bias.float().numpy())
+
+
+def test_read_probe_reads_and_leaves_the_sink():
+    """tq_read_probe (bench.py's plain-read context for the GEMM roofline):
+    runs over sizes that are not a multiple of its 16 KiB block share (the
+    clamped tail re-reads the last word) and, on data that does not fold to its
+    constant, writes nothing."""
+    from tilequant_amd import _native as nat
+
+    for nbytes in (16, 16 * 1023, 16 * 4097, 25446144):
+        buf = torch.zeros((nbytes,), dtype=torch.uint8, device="cuda")
+        sink = torch.full((256,), 7, dtype=torch.int32, device="cuda")
+        assert nat.lib().tq_read_probe(nat.ptr(buf), nbytes, nat.ptr(sink), nat.stream_handle(buf.device)) == 0
+        torch.cuda.synchronize()
+        assert bool((sink == 7).all()), nbytes

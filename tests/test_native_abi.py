@@ -68,6 +68,11 @@ def test_argument_errors_return_before_any_launch(lib):
     assert lib.tq_gemm_mixed_rows(None, 0, None, None, None, None, None, None, 0, 0, None, None, None,
                                   None, 0, 0, None, 0, 64, 64, 1, 1, 0, 1, None, 0, None) == 0
     assert lib.tq_pack_int8_tiles(None, 64, 0, 64, 64, None, 0, 1, 1, None, None, None, None) == 0
+    # the read-probe measurement helper: sizes in whole 16-byte words, aligned data, a sink
+    assert lib.tq_read_probe(None, 0, None, None) == 0
+    assert lib.tq_read_probe(None, 17, None, None) == -1 and lib.tq_read_probe(None, -16, None, None) == -1
+    assert lib.tq_read_probe(None, 16, None, None) == -1
+    assert lib.tq_read_probe(ctypes.c_void_p(8), 16, ctypes.c_void_p(256), None) == -3
 
 
 def test_token_blocked_preference(lib):

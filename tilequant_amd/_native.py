@@ -35,6 +35,7 @@ _SIGNATURES = {
     "tq_act_quant_fused": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _i64, _p, _p]),
     "tq_act_quant_token_blocked": (_i, [_p, _i64, _i, _i, _i, _p, _p, _p]),
     "tq_gemm_prefers_token_blocked": (_i, [_i, _i, _i, _i]),
+    "tq_read_probe": (_i, [_p, _i64, _p, _p]),
     "tq_act_absmax_workspace_elems": (_i64, [_i, _i]),
     "tq_act_absmax_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),
     "tq_act_quant_with_scales": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _i64, _p]),

@@ -3018,3 +3018,40 @@ extern "C" int tq_linear_mixed_fused_products_i32(
                                   out_dtype, bias, n, m, k, n_tr, n_tc, split_k, tile_layout, workspace,
                                   workspace_elems, products, row0, rows, kernel, stream);
 }
+
+// ---- measurement helper: a plain read of HBM --------------------------------
+//
+// Context for the decode GEMM's roofline: the time a kernel that does nothing
+// but read the same number of bytes takes per launch, timed the same way
+// (bench.py).  Each thread loads four 16-byte words, all in flight together
+// (indexes past the end re-read the last word), and folds them into one word
+// that is stored only if it equals a constant: the loads cannot be dropped and
+// nothing is written in practice.  sink holds 256 words.
+constexpr int kReadProbeThreads = 256;
+constexpr int kReadProbeWords = 4;
+
+__global__ void __launch_bounds__(kReadProbeThreads)
+read_probe_kernel(const u32x4* __restrict__ p, int64_t n16, uint32_t* __restrict__ sink) {
+  const int64_t base = (int64_t)blockIdx.x * (kReadProbeThreads * kReadProbeWords) + threadIdx.x;
+  u32x4 v[kReadProbeWords];
+#pragma unroll
+  for (int u = 0; u < kReadProbeWords; ++u) v[u] = p[min(base + (int64_t)u * kReadProbeThreads, n16 - 1)];
+  uint32_t x = 0;
+#pragma unroll
+  for (int u = 0; u < kReadProbeWords; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  if (x == 0x9e3779b9u) sink[blockIdx.x & 255] = x;
+}
+
+extern "C" int tq_read_probe(const void* data, int64_t bytes, uint32_t* sink, void* stream) {
+  if (bytes < 0 || (bytes & 15) != 0) return TQ_ERR_ARG;
+  if (bytes == 0) return TQ_OK;
+  if (data == nullptr || sink == nullptr) return TQ_ERR_ARG;
+  if ((reinterpret_cast<uintptr_t>(data) & 15) != 0) return TQ_ERR_ALIGN;
+  const int64_t n16 = bytes / 16;
+  const int64_t per_block = (int64_t)kReadProbeThreads * kReadProbeWords;
+  const int64_t blocks = (n16 + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff) return TQ_ERR_ARG;
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(kReadProbeThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(data), n16, sink);
+  return (int)hipGetLastError();
+}
