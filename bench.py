@@ -1441,6 +1441,12 @@ def main():
     bytes_per_launch = info["packed_bytes"] / len(launches)
     achieved = bytes_per_launch / gemm_avg_s / 1e9
     plain_read_us = plain_read_launch_us(device, s, len(launches), int(bytes_per_launch), reps)
+    group_plain_us = {}
+    for gname, _, _ in GROUPS:
+        lin0 = layers[0][gname]
+        gbytes = 4096 * int(lin0.int8_tiles.shape[0]) + 8192 * int(lin0.fp16_tiles.shape[0]) + \
+            4 * int(lin0.int8_tiles.shape[0])
+        group_plain_us[gname] = plain_read_launch_us(device, s, len(layers), gbytes, reps)
 
     # dense bf16 context: the same linear set through torch.nn.functional.linear (hipBLASLt)
     dense = None
@@ -1554,6 +1560,8 @@ def main():
                      "group_avg_us": group_us,
                      "plain_read_us": plain_read_us,
                      "frac_of_plain_read": plain_read_us / (gemm_avg_s * 1e6),
+                     "group_plain_read_us": group_plain_us,
+                     "group_frac_of_plain_read": {g: group_plain_us[g] / group_us[g] for g in group_us},
                      "timing": "HIP events on the launch stream around replays of one HIP graph holding the "
                                "step's 112 GEMM launches back to back (activations quantized beforehand); "
                                "per-launch average includes the inter-kernel gaps. plain_read_us: the same "
