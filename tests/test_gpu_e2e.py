@@ -597,16 +597,19 @@ def test_rotary_tables_equal_per_position_values():
         assert torch.equal(c.reshape(-1), cos_t[0, p]) and torch.equal(s_.reshape(-1), sin_t[0, p]), p
 
 
-@pytest.mark.parametrize("family", ["llama", "qwen"])
-def test_fused_decode_step_matches_module_forward(family):
+@pytest.mark.parametrize("family,dtype", [("llama", torch.bfloat16), ("qwen", torch.bfloat16),
+                                          ("llama", torch.float16), ("qwen", torch.float16)])
+def test_fused_decode_step_matches_module_forward(family, dtype):
     """The fused one-token step against the model's own forward in the same
     captured decoder (fused_decode=False): same tokens fed, logits within
-    bf16 rounding noise, argmax equal wherever the margin is clear."""
+    16-bit rounding noise, argmax equal wherever the margin is clear; bf16 and
+    fp16 models (every fused kernel's fp16 instantiation end to end)."""
     from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
 
     config = tiny_llama_config(layers=2) if family == "llama" else tiny_qwen2_config(layers=2)
-    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out="bf16"), DEV,
-                                               keep_frac=0.05, seed=31)
+    out = "bf16" if dtype == torch.bfloat16 else "fp16"
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out=out), DEV,
+                                               torch_dtype=dtype, keep_frac=0.05, seed=31)
     B, P, O = 4, 80, 10
     prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(32))
     dec = CudaGraphGreedyDecoder.prepare(model, prompt_tokens=P, max_new_tokens=O, batch_size=B, device=DEV)
@@ -637,17 +640,20 @@ def test_fused_decode_step_matches_module_forward(family):
     ref.close()
 
 
-@pytest.mark.parametrize("family", ["llama", "qwen"])
-def test_fused_prefill_matches_module_prefill(family):
+@pytest.mark.parametrize("family,dtype", [("llama", torch.bfloat16), ("qwen", torch.bfloat16),
+                                          ("llama", torch.float16)])
+def test_fused_prefill_matches_module_prefill(family, dtype):
     """The decoder's fused prompt forward against the model's own forward
-    (fused_prefill=False): last-token logits within bf16 rounding noise,
+    (fused_prefill=False): last-token logits within 16-bit rounding noise,
     argmax equal where the margin is clear, the caches' prompt k/v close, and
-    the tokens decoded after either prefill agree where the margins are clear."""
+    the tokens decoded after either prefill agree where the margins are clear;
+    bf16 models and an fp16 one."""
     from tilequant_amd.graph_decode import CudaGraphGreedyDecoder
 
     config = tiny_llama_config(layers=2) if family == "llama" else tiny_qwen2_config(layers=2)
-    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out="bf16"), DEV,
-                                               keep_frac=0.05, seed=41)
+    out = "bf16" if dtype == torch.bfloat16 else "fp16"
+    model, _ = api.build_mixed_precision_model(config, ApplyConfig(model_type=family, dtype_out=out), DEV,
+                                               torch_dtype=dtype, keep_frac=0.05, seed=41)
     B, P, O = 3, 100, 6
     prompt = torch.randint(0, config.vocab_size, (B, P), generator=torch.Generator().manual_seed(42))
     runs = {}
